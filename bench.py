@@ -1,0 +1,228 @@
+"""Benchmark of the LUMA optimizer step on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config llama3_8b]
+
+A step is one ``LUMA.step()`` over the whole synthetic parameter set with
+gradients already resident in HBM.  Prints one JSON line with:
+  value        Gparams/s of the whole step (params / ms_per_step)
+  roofline     the dominant kernel's algorithmic HBM bytes per launch over its
+               average launch time (HIP events on the launch stream) vs 8 TB/s
+  cpu_baseline the CPU oracle (the reference's PyTorch backend restated) timed
+               on this host on a bounded sample of the same workload
+Bytes model per parameter: pass 1 reads grad + Q_m + Q_w (G + 4 bytes), pass 2
+reads grad + Q_m + Q_w + param and writes Q_m + Q_w + param (G + 16), so a
+step moves 2G + 20 bytes (G = gradient element size).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "LUMA step Gparams/s + achieved HBM GB/s (% of peak), 8B-param fp32 set"
+HBM_PEAK = 8.0e12
+
+
+# ── synthetic parameter sets ─────────────────────────────────────────────────
+
+def llama3_8b_shapes():
+    """Llama-3-8B: 32 layers of q/k/v/o, gate/up/down, two RMSNorms; embed, lm_head, norm."""
+    shapes = [(128256, 4096)]
+    for _ in range(32):
+        shapes += [(4096, 4096), (1024, 4096), (1024, 4096), (4096, 4096),
+                   (14336, 4096), (14336, 4096), (4096, 14336), (4096,), (4096,)]
+    shapes += [(4096,), (128256, 4096)]
+    return shapes
+
+
+def gpt2_small_shapes():
+    shapes = [(50257, 768), (1024, 768)]
+    for _ in range(12):
+        shapes += [(768,), (768,), (768, 2304), (2304,), (768, 768), (768,),
+                   (768,), (768,), (768, 3072), (3072,), (3072, 768), (768,)]
+    shapes += [(768,), (768,)]
+    return shapes
+
+
+def many_small_shapes(n=20000, seed=3):
+    g = torch.Generator().manual_seed(seed)
+    u = torch.rand(n, generator=g, dtype=torch.float64)
+    sizes = torch.exp(u * math.log(65536.0)).round().clamp(1, 65536).long().tolist()
+    return [(s,) for s in sizes]
+
+
+CONFIGS = {
+    "llama3_8b": dict(shapes=llama3_8b_shapes, grad=torch.bfloat16, std=1e-3, outliers=1e-3,
+                      desc="Llama-3-8B-shaped fp32 param set (291 tensors), bf16 grads "
+                           "N(0,1e-3) with 0.1% x100 outliers"),
+    "gpt2_small": dict(shapes=gpt2_small_shapes, grad=torch.bfloat16, std=1e-3, outliers=0.0,
+                       desc="GPT-2-small-shaped fp32 param list (148 tensors), bf16 grads N(0,1e-3)"),
+    "many_small": dict(shapes=many_small_shapes, grad=torch.float32, std=1e-4, outliers=0.0,
+                       zeros=0.01, desc="20,000 fp32 tensors, sizes log-uniform in [1, 65536], "
+                                        "fp32 grads N(0,1e-4) with 1% exact zeros"),
+    "single_4096": dict(shapes=lambda: [(4096, 4096)], grad=torch.float32, std=1e-3,
+                        outliers=0.0, desc="single fp32 4096x4096 param, fp32 grads N(0,1e-3)"),
+}
+
+
+def make_set(cfg, device):
+    shapes = cfg["shapes"]()
+    torch.manual_seed(0)
+    params, grads = [], []
+    for s in shapes:
+        p = torch.randn(s, device=device) * 0.02
+        if len(s) == 1 and cfg["shapes"] is not many_small_shapes:
+            p.fill_(1.0)                             # norm weights
+        g = torch.randn(s, device=device) * cfg["std"]
+        if cfg.get("outliers"):
+            g = torch.where(torch.rand(s, device=device) < cfg["outliers"], g * 100.0, g)
+        if cfg.get("zeros"):
+            g = torch.where(torch.rand(s, device=device) < cfg["zeros"], torch.zeros_like(g), g)
+        p.requires_grad_(True)
+        p.grad_dtype = None        # allow bf16 / fp16 grads on fp32 params
+        params.append(p)
+        grads.append(g.to(cfg["grad"]))
+    return params, grads
+
+
+# ── CPU baseline: the oracle on a bounded sample ─────────────────────────────
+
+def cpu_baseline(cfg_name):
+    from oracle import luma_oracle as O
+
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    n = 4096 * 4096 if cfg_name != "many_small" else 4 * 1024 * 1024
+    gen = torch.Generator().manual_seed(1)
+    p = torch.randn(n, generator=gen) * 0.02
+    p.grad_dtype = None
+    gdt = CONFIGS[cfg_name]["grad"]
+    grads = [(torch.randn(n, generator=gen) * 1e-3).to(gdt) for _ in range(4)]
+    opt = O.OracleLUMA([dict(params=[p], lr=1e-3, betas=(0.9, 0.999), eps=1e-8,
+                             weight_decay=0.01)], 12345, "torch")
+    times = []
+    for i, g in enumerate(grads):
+        p.grad = g
+        t0 = time.perf_counter()
+        opt.step()
+        dt = time.perf_counter() - t0
+        if i >= 1:
+            times.append(dt)
+    times.sort()
+    med = times[len(times) // 2]
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(n / med / 1e9, 6), "unit": "Gparams/s", "cores": threads,
+            "kind": "port",
+            "sample": f"oracle (reference PyTorch backend restated, torch CPU ops) on one "
+                      f"{n}-element fp32 tensor with {str(gdt).replace('torch.', '')} grads; "
+                      f"median of {len(times)} update steps after the init step; {cpu_model}"}
+
+
+# ── main ─────────────────────────────────────────────────────────────────────
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="llama3_8b", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
+              "the LUMA step is rank-local and shards with no exchange", file=sys.stderr)
+        sys.exit(2)
+
+    from luma_amd import LUMA
+
+    cfg = CONFIGS[args.config]
+    dev = torch.device("cuda:0")
+    params, grads = make_set(cfg, dev)
+    n_params = sum(p.numel() for p in params)
+    gbytes = torch.tensor([], dtype=cfg["grad"]).element_size()
+    opt = LUMA(params, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01)
+    for p, g in zip(params, grads):
+        p.grad = g
+    print(f"bench: {args.config} {len(params)} tensors {n_params} params", file=sys.stderr, flush=True)
+
+    for _ in range(args.warmup):
+        opt.step()
+    torch.cuda.synchronize()
+    print("bench: warmup done", file=sys.stderr, flush=True)
+
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    for e in evs:
+        e.record()
+    torch.cuda.synchronize()
+    opt._engine.profile_events = evs
+    k_times = [[], [], []]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        opt.step()
+        torch.cuda.synchronize()
+        for k in range(3):
+            k_times[k].append(evs[k].elapsed_time(evs[k + 1]))
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    opt._engine.profile_events = None
+    ms = wall * 1e3 / args.steps
+
+    avg = [sum(v) / len(v) for v in k_times]
+    pass_bytes = [n_params * (gbytes + 4), 0, n_params * (gbytes + 16)]
+    dom = 0 if avg[0] > avg[2] else 2
+    achieved = pass_bytes[dom] / (avg[dom] * 1e-3)
+    step_bytes = n_params * (2 * gbytes + 20)
+    step_gbps = step_bytes / (ms * 1e-3)
+    names = ["luma_pass1", "luma_finalize", "luma_pass2"]
+    print(f"bench: kernel ms pass1 {avg[0]:.3f} finalize {avg[1]:.3f} pass2 {avg[2]:.3f}; "
+          f"step {ms:.3f} ms", file=sys.stderr, flush=True)
+
+    cpu = None if args.no_cpu else cpu_baseline(args.config)
+    out = {
+        "metric": METRIC,
+        "value": round(n_params / (ms * 1e-3) / 1e9, 3),
+        "unit": "Gparams/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": cfg["desc"], "params": n_params, "tensors": len(params),
+                   "grad_dtype": str(cfg["grad"]).replace("torch.", ""),
+                   "bytes_per_param": 2 * gbytes + 20},
+        "step_hbm_gbps": round(step_gbps / 1e9, 1),
+        "step_hbm_frac": round(step_gbps / HBM_PEAK, 4),
+        "kernel_ms": {names[i]: round(avg[i], 4) for i in range(3)},
+        "roofline": {"bound": "hbm", "kernel": names[dom],
+                     "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),
+                     "traffic": None},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

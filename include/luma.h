@@ -1,0 +1,180 @@
+/*
+ * luma.h -- C ABI of the MI355X (gfx950) LUMA optimizer-step library
+ * (libluma_hip.so).  Plain C types only; every pointer documented as
+ * "device" is HIP device memory owned by the caller.  The library never
+ * allocates, never synchronises the stream it is given, and never throws:
+ * each entry point returns 0 on success or a nonzero status whose text is
+ * available from luma_last_error().
+ *
+ * What each entry point replaces in the reference (IgorYashch/LUMA 0.1.0):
+ *
+ *   luma_step          -- the per-parameter loop body of LUMA.step for all
+ *                         parameters at once: luma_init_step (t = 1,
+ *                         src/luma_optimizer/functional.py:183-228) and
+ *                         luma_update_step (t >= 2, functional.py:231-298),
+ *                         i.e. the Triton pipelines luma_triton_init_step /
+ *                         luma_triton_step (triton_kernel.py:409-492).
+ *   luma_step_profiled -- luma_step with event records between its launches.
+ *   luma_set_scales    -- the scale half of load_state_dict /
+ *                         _init_triton_buffers (optimizer.py:146-183,341-387).
+ *   luma_get_scales    -- the S_m / S_v read-back of state_dict
+ *                         (optimizer.py:119-144).
+ *   luma_decode        -- the decode of export_adamw_state
+ *                         (optimizer.py:231-235, functional.py:113-126).
+ *   luma_quantize      -- the quantisation of import_adamw_state
+ *                         (optimizer.py:304-321, functional.py:133-176).
+ *   luma_philox4x32    -- host-side Philox4x32-10 block function used by the
+ *                         stochastic rounding (Salmon et al., SC'11); the
+ *                         reference's Triton path draws from tl.rand
+ *                         (triton_kernel.py:103,124).
+ */
+#ifndef LUMA_H
+#define LUMA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LUMA_ABI_VERSION 1
+
+/* Elements per chunk-table entry (one workgroup's share of a tensor). */
+#define LUMA_CHUNK_ELEMS 32768
+
+/* Bytes of one opaque scale slot (per-tensor persistent state). */
+#define LUMA_SLOT_BYTES 256
+
+/* Gradient element types. */
+#define LUMA_GRAD_F32 0
+#define LUMA_GRAD_BF16 1
+#define LUMA_GRAD_F16 2
+
+/* Where the stochastic-rounding uniforms come from. */
+#define LUMA_NOISE_PHILOX 0   /* counter-based Philox4x32-10, keyed per (seed, step, param) */
+#define LUMA_NOISE_INJECTED 1 /* caller-supplied u_m / u_w float32 arrays in [0, 1) */
+
+/* luma_step flags. */
+#define LUMA_FLAG_EXACT_ONLY 1 /* take the exact per-element path everywhere */
+
+/* One parameter tensor taking part in a step (array in device memory). */
+typedef struct LumaTensor {
+  float *param;         /* device f32 [numel], updated in place            */
+  const void *grad;     /* device f32 / bf16 / f16 [numel]                  */
+  int16_t *q_m;         /* device [numel] signed log-grid momentum codes    */
+  int16_t *q_w;         /* device [numel] uint16 preconditioner codes       */
+  const float *u_m;     /* device [numel] injected uniforms, or NULL        */
+  const float *u_w;     /* device [numel] injected uniforms, or NULL        */
+  int64_t numel;        /* elements                                          */
+  int64_t step;         /* this update's step number t (1 = first update)   */
+  int64_t param_id;     /* position of the parameter in param_groups order  */
+  int32_t grad_dtype;   /* LUMA_GRAD_*                                       */
+  int32_t hyper;        /* index into the LumaHyper table                    */
+  int32_t slot;         /* index into the scale-slot table                   */
+  int32_t first_chunk;  /* index of this tensor's first LumaChunk            */
+} LumaTensor;
+
+/* Chunk c of a tensor covers elements [c*LUMA_CHUNK_ELEMS, min(numel, (c+1)*LUMA_CHUNK_ELEMS)). */
+typedef struct LumaChunk {
+  int32_t tensor; /* index into the LumaTensor table */
+  int32_t index;  /* chunk number within that tensor */
+} LumaChunk;
+
+/*
+ * Per (param group, step) coefficients.  The caller computes them in double
+ * exactly as the reference does and rounds each to float32 once:
+ * beta1 = f32(b1), omb1 = f32(1 - b1), beta2 = f32(b2), omb2 = f32(1 - b2),
+ * decay = f32(1 - wd*lr), neg_eta = f32(-(lr / (1 - b1^t))),
+ * bc2 = f32(1 - b2^t), eps = f32(eps); eps_d is eps itself.
+ */
+typedef struct LumaHyper {
+  float beta1, omb1, beta2, omb2;
+  float decay, neg_eta, bc2, eps;
+  double eps_d;
+} LumaHyper;
+
+typedef struct LumaStepArgs {
+  const LumaTensor *tensors; /* device */
+  int32_t n_tensors;
+  int32_t n_chunks;
+  const LumaChunk *chunks;   /* device */
+  const LumaHyper *hypers;   /* device */
+  void *slots;               /* device, LUMA_SLOT_BYTES per slot, zero-initialised */
+  float *partials;           /* device workspace, 2 floats per chunk */
+  uint64_t base_seed;        /* LUMA._base_seed as its two's-complement bits */
+  int32_t noise_mode;        /* LUMA_NOISE_* */
+  int32_t flags;             /* LUMA_FLAG_* */
+} LumaStepArgs;
+
+/* One scale-slot write (array in device memory). */
+typedef struct LumaScaleInit {
+  int32_t slot;
+  int32_t pad;
+  int64_t step;  /* the tensor's current step count t (parity selects the buffer) */
+  double s_m;    /* S_m as stored by the reference (>= 1e-9) */
+  double s_v;    /* S_v (>= 0) */
+  double eps;    /* the group's eps */
+} LumaScaleInit;
+
+int luma_abi_version(void);
+const char *luma_last_error(void);
+
+/*
+ * Struct sizes as compiled, for binding checks: LumaTensor, LumaChunk,
+ * LumaHyper, LumaScaleInit, LumaStepArgs, slot bytes, LUMA_CHUNK_ELEMS, 0.
+ */
+void luma_layout(int32_t out[8]);
+
+/* Bytes of workspace luma_step needs for n_chunks chunks. */
+size_t luma_workspace_bytes(int32_t n_chunks);
+
+/*
+ * One optimizer step for every tensor in the table: pass 1 (decode + EMA +
+ * per-chunk maxima), per-tensor finalize (new S_m/S_v and grid in float64),
+ * pass 2 (re-decode + EMA + AdamW update + LogSR re-quantisation).  Three
+ * kernel launches on `stream` (a hipStream_t), no host synchronisation.
+ */
+int luma_step(const LumaStepArgs *args, void *stream);
+
+/*
+ * luma_step that also records caller-created hipEvent_t events[0..3] on the
+ * stream: before pass 1, after pass 1, after finalize, after pass 2 (NULL
+ * entries are skipped).  Used to time each kernel on its own stream.
+ */
+int luma_step_profiled(const LumaStepArgs *args, void *stream, void *const events[4]);
+
+/* Write S_m/S_v of n slots (items: device array) and derive their grids. */
+int luma_set_scales(void *slots, const LumaScaleInit *items, int32_t n, void *stream);
+
+/* Read S_m/S_v of n (slot, step) pairs into out[2*i], out[2*i+1] (device doubles). */
+int luma_get_scales(const void *slots, const int32_t *slot_idx, const int64_t *steps,
+                    int32_t n, double *out, void *stream);
+
+/*
+ * Decode one tensor's codes into float32 m (exp_avg) and v (exp_avg_sq) using
+ * the scales of (slot, step) and the group's eps.
+ */
+int luma_decode(const int16_t *q_m, const int16_t *q_w, int64_t numel, const void *slots,
+                int32_t slot, int64_t step, double eps, float *m_out, float *v_out,
+                void *stream);
+
+/*
+ * Quantise given float32 m, v (clamped at 0) into codes with fresh scales
+ * S_m = max(max|m|, 1e-9), S_v = max(max v, 0), stored into (slot, step).
+ * Uniforms: Philox keyed by seed (noise_mode 0) or u_m/u_w (noise_mode 1).
+ * `partials` needs luma_workspace_bytes(ceil(numel / LUMA_CHUNK_ELEMS)).
+ */
+int luma_quantize(const float *m, const float *v, int64_t numel, int16_t *q_m, int16_t *q_w,
+                  void *slots, int32_t slot, int64_t step, double eps, uint64_t seed,
+                  int32_t noise_mode, const float *u_m, const float *u_w, float *partials,
+                  void *stream);
+
+/* Host: one Philox4x32-10 block. */
+void luma_philox4x32(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LUMA_H */

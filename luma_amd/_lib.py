@@ -1,0 +1,131 @@
+"""ctypes binding of libluma_hip.so (C ABI in include/luma.h).
+
+The table layouts below mirror the C structs byte for byte; ``check_layout``
+compares them with the sizes the library reports.  Loading fails loudly: there
+is no fallback implementation of the step.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_NAME = "libluma_hip.so"
+LIB_PATH = os.path.join(HERE, LIB_NAME)
+
+CHUNK_ELEMS = 32768          # LUMA_CHUNK_ELEMS
+SLOT_BYTES = 256             # LUMA_SLOT_BYTES
+ABI_VERSION = 1              # LUMA_ABI_VERSION
+
+GRAD_F32, GRAD_BF16, GRAD_F16 = 0, 1, 2
+NOISE_PHILOX, NOISE_INJECTED = 0, 1
+FLAG_EXACT_ONLY = 1
+
+TENSOR_DTYPE = np.dtype([
+    ("param", "<u8"), ("grad", "<u8"), ("q_m", "<u8"), ("q_w", "<u8"),
+    ("u_m", "<u8"), ("u_w", "<u8"),
+    ("numel", "<i8"), ("step", "<i8"), ("param_id", "<i8"),
+    ("grad_dtype", "<i4"), ("hyper", "<i4"), ("slot", "<i4"), ("first_chunk", "<i4"),
+])
+CHUNK_DTYPE = np.dtype([("tensor", "<i4"), ("index", "<i4")])
+HYPER_DTYPE = np.dtype([
+    ("beta1", "<f4"), ("omb1", "<f4"), ("beta2", "<f4"), ("omb2", "<f4"),
+    ("decay", "<f4"), ("neg_eta", "<f4"), ("bc2", "<f4"), ("eps", "<f4"),
+    ("eps_d", "<f8"),
+])
+SCALE_INIT_DTYPE = np.dtype([
+    ("slot", "<i4"), ("pad", "<i4"), ("step", "<i8"),
+    ("s_m", "<f8"), ("s_v", "<f8"), ("eps", "<f8"),
+])
+
+
+class StepArgs(ctypes.Structure):
+    _fields_ = [
+        ("tensors", ctypes.c_void_p),
+        ("n_tensors", ctypes.c_int32),
+        ("n_chunks", ctypes.c_int32),
+        ("chunks", ctypes.c_void_p),
+        ("hypers", ctypes.c_void_p),
+        ("slots", ctypes.c_void_p),
+        ("partials", ctypes.c_void_p),
+        ("base_seed", ctypes.c_uint64),
+        ("noise_mode", ctypes.c_int32),
+        ("flags", ctypes.c_int32),
+    ]
+
+
+class LumaLibraryError(RuntimeError):
+    pass
+
+
+_lib = None
+
+_VP = ctypes.c_void_p
+_SIGNATURES = {
+    "luma_abi_version": (ctypes.c_int, []),
+    "luma_last_error": (ctypes.c_char_p, []),
+    "luma_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int32]),
+    "luma_layout": (None, [ctypes.POINTER(ctypes.c_int32)]),
+    "luma_step": (ctypes.c_int, [ctypes.POINTER(StepArgs), _VP]),
+    "luma_step_profiled": (ctypes.c_int, [ctypes.POINTER(StepArgs), _VP,
+                                          ctypes.POINTER(ctypes.c_void_p)]),
+    "luma_set_scales": (ctypes.c_int, [_VP, _VP, ctypes.c_int32, _VP]),
+    "luma_get_scales": (ctypes.c_int, [_VP, _VP, _VP, ctypes.c_int32, _VP, _VP]),
+    "luma_decode": (ctypes.c_int, [_VP, _VP, ctypes.c_int64, _VP, ctypes.c_int32, ctypes.c_int64,
+                                   ctypes.c_double, _VP, _VP, _VP]),
+    "luma_quantize": (ctypes.c_int, [_VP, _VP, ctypes.c_int64, _VP, _VP, _VP, ctypes.c_int32,
+                                     ctypes.c_int64, ctypes.c_double, ctypes.c_uint64,
+                                     ctypes.c_int32, _VP, _VP, _VP, _VP]),
+    "luma_philox4x32": (None, [ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint32),
+                               ctypes.POINTER(ctypes.c_uint32)]),
+}
+
+
+def load(path: str = LIB_PATH):
+    """Load the HIP library (once) and bind every entry point."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise LumaLibraryError(
+            f"{LIB_NAME} not found at {path}; build it with "
+            "`python -c 'import luma_amd.build as b; b.build()'` (needs hipcc)")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if lib.luma_abi_version() != ABI_VERSION:
+        raise LumaLibraryError(f"{LIB_NAME} ABI {lib.luma_abi_version()} != {ABI_VERSION}")
+    check_layout(lib)
+    _lib = lib
+    return lib
+
+
+def check_layout(lib) -> None:
+    out = (ctypes.c_int32 * 8)()
+    lib.luma_layout(out)
+    want = [TENSOR_DTYPE.itemsize, CHUNK_DTYPE.itemsize, HYPER_DTYPE.itemsize,
+            SCALE_INIT_DTYPE.itemsize, ctypes.sizeof(StepArgs), SLOT_BYTES, CHUNK_ELEMS]
+    got = list(out)[:7]
+    if got != want:
+        raise LumaLibraryError(f"struct layout mismatch: library {got} vs python {want}")
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = _lib.luma_last_error().decode() if _lib is not None else ""
+        raise LumaLibraryError(f"{what} failed ({rc}): {msg}")
+
+
+def philox4x32(ctr, key):
+    """Host Philox4x32-10 block from the library (no GPU needed)."""
+    lib = load()
+    c = (ctypes.c_uint32 * 4)(*[int(x) & 0xFFFFFFFF for x in ctr])
+    k = (ctypes.c_uint32 * 2)(*[int(x) & 0xFFFFFFFF for x in key])
+    o = (ctypes.c_uint32 * 4)()
+    lib.luma_philox4x32(c, k, o)
+    return [int(x) for x in o]

@@ -1,0 +1,101 @@
+// Philox4x32-10 counter-based generator (Salmon, Moraes, Dror, Shaw,
+// "Parallel Random Numbers: As Easy as 1, 2, 3", SC'11), host and device.
+//
+// One block maps a 128-bit counter and a 64-bit key to 128 random bits with
+// ten rounds of two 32x32->64 multiplies; the key is bumped by the Weyl
+// constants between rounds.
+//
+// How the LUMA step uses it (the uniform stream of one (param, step)):
+//   key      = seed = ((t << 32) | 2*param_id) ^ base_seed  (the reference's
+//              per-step seed, functional.py:99-106), split lo/hi.
+//   element e gets two 24-bit uniforms u_m(e), u_w(e) in [0, 1):
+//     high 8 bits  -- bytes 2j, 2j+1 (j = e & 7) of block ctr = (e >> 3, 0, 0)
+//     low 16 bits  -- halves 2i, 2i+1 (i = e & 3) of block ctr = (e >> 2, 1, 0)
+//   (counter words: c0 = lo32(index), c1 = hi32(index), c2 = stream, c3 = 0).
+// The split lets the fast path decide most roundings from one block per 8
+// elements and fetch the low bits only for the rare elements whose decision
+// depends on them.
+#pragma once
+
+#include <stdint.h>
+
+#if defined(__HIPCC__)
+#define LUMA_HD __host__ __device__ __forceinline__
+#else
+#define LUMA_HD static inline
+#endif
+
+namespace luma {
+
+constexpr uint32_t kPhiloxM0 = 0xD2511F53u;
+constexpr uint32_t kPhiloxM1 = 0xCD9E8D57u;
+constexpr uint32_t kPhiloxW0 = 0x9E3779B9u;
+constexpr uint32_t kPhiloxW1 = 0xBB67AE85u;
+
+struct U4 {
+  uint32_t x, y, z, w;
+};
+
+LUMA_HD void philox_round(uint32_t &c0, uint32_t &c1, uint32_t &c2, uint32_t &c3, uint32_t k0,
+                          uint32_t k1) {
+  const uint64_t p0 = (uint64_t)kPhiloxM0 * c0;
+  const uint64_t p1 = (uint64_t)kPhiloxM1 * c2;
+  const uint32_t hi0 = (uint32_t)(p0 >> 32), lo0 = (uint32_t)p0;
+  const uint32_t hi1 = (uint32_t)(p1 >> 32), lo1 = (uint32_t)p1;
+  const uint32_t n0 = hi1 ^ c1 ^ k0;
+  const uint32_t n2 = hi0 ^ c3 ^ k1;
+  c0 = n0;
+  c1 = lo1;
+  c2 = n2;
+  c3 = lo0;
+}
+
+// Ten rounds; round r uses key (k0 + r*W0, k1 + r*W1).
+LUMA_HD U4 philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint32_t k0,
+                         uint32_t k1) {
+#if defined(__HIP_DEVICE_COMPILE__)
+#pragma unroll
+#endif
+  for (int r = 0; r < 10; ++r) {
+    philox_round(c0, c1, c2, c3, k0, k1);
+    k0 += kPhiloxW0;
+    k1 += kPhiloxW1;
+  }
+  U4 o;
+  o.x = c0;
+  o.y = c1;
+  o.z = c2;
+  o.w = c3;
+  return o;
+}
+
+// Counter-block indices for element e (see the header comment).
+LUMA_HD U4 philox_coarse_block(uint64_t e, uint32_t k0, uint32_t k1) {
+  const uint64_t b = e >> 3;
+  return philox4x32_10((uint32_t)b, (uint32_t)(b >> 32), 0u, 0u, k0, k1);
+}
+
+LUMA_HD U4 philox_fine_block(uint64_t e, uint32_t k0, uint32_t k1) {
+  const uint64_t b = e >> 2;
+  return philox4x32_10((uint32_t)b, (uint32_t)(b >> 32), 1u, 0u, k0, k1);
+}
+
+LUMA_HD uint32_t u4_word(const U4 &v, int i) {
+  return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
+}
+
+// Byte i (0..15) of a block, little-endian across x, y, z, w.
+LUMA_HD uint32_t u4_byte(const U4 &v, int i) { return (u4_word(v, i >> 2) >> (8 * (i & 3))) & 0xFFu; }
+
+// 16-bit half i (0..7) of a block.
+LUMA_HD uint32_t u4_half(const U4 &v, int i) { return (u4_word(v, i >> 1) >> (16 * (i & 1))) & 0xFFFFu; }
+
+// The two 24-bit integers (u * 2^24) of element e, from its two blocks.
+LUMA_HD void philox_uniform_bits(const U4 &coarse, const U4 &fine, uint64_t e, uint32_t &bits_m,
+                                 uint32_t &bits_w) {
+  const int j = (int)(e & 7), i = (int)(e & 3);
+  bits_m = (u4_byte(coarse, 2 * j) << 16) | u4_half(fine, 2 * i);
+  bits_w = (u4_byte(coarse, 2 * j + 1) << 16) | u4_half(fine, 2 * i + 1);
+}
+
+}  // namespace luma

@@ -1,0 +1,477 @@
+"""``LUMA`` -- ``torch.optim.Optimizer`` front end over the HIP step.
+
+Same public surface as the reference (src/luma_optimizer/optimizer.py:39-524):
+``LUMA(params, lr, betas, eps, weight_decay, backend)``, ``step(closure)``,
+``state_dict()`` / ``load_state_dict()``, ``export_adamw_state()``,
+``import_adamw_state()`` and ``_base_seed``.  Per parameter the state holds
+``step``, ``param_id``, ``Q_m`` and ``Q_w`` (int16, the parameter's shape);
+``S_m`` / ``S_v`` live in device scale slots and appear in ``state_dict()``.
+
+One ``step()`` is one multi-tensor launch sequence on the current stream
+(luma_step in include/luma.h) with no host synchronisation.  The stochastic
+rounding draws come from Philox4x32-10 keyed by the reference's per-step seed
+``((t << 32) | 2*param_id) ^ _base_seed`` (functional.py:99-106), or from
+uniforms injected with ``inject_noise`` (used to compare against the
+reference's own draws).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Dict, Optional, Tuple
+
+import numpy as np
+import torch
+from torch.optim import Optimizer
+
+from . import _lib as L
+from .config import SCALE_FLOOR_M  # noqa: F401  (re-exported constant)
+
+_GRAD_CODES = {torch.float32: L.GRAD_F32, torch.bfloat16: L.GRAD_BF16, torch.float16: L.GRAD_F16}
+_MASK64 = (1 << 64) - 1
+
+
+def make_step_seed(base_seed: int, step: int, param_id: int) -> int:
+    """functional.py:99-106 -- the per-(step, param) seed."""
+    return ((step << 32) | (param_id * 2)) ^ base_seed
+
+
+def _is_dense(t: torch.Tensor) -> bool:
+    return (t.is_contiguous() or t.is_contiguous(memory_format=torch.channels_last)
+            or t.is_contiguous(memory_format=torch.channels_last_3d))
+
+
+def _ptr(t: Optional[torch.Tensor]) -> int:
+    return 0 if t is None else t.data_ptr()
+
+
+class _Engine:
+    """Device-side tables of one optimizer: scale slots, chunk plan, uploads."""
+
+    def __init__(self, device: torch.device):
+        self.lib = L.load()
+        self.device = device
+        self.n_slots = 0
+        self.slots = torch.zeros(64 * L.SLOT_BYTES, dtype=torch.uint8, device=device)
+        self._plan_key = None
+        self._chunks = None
+        self._first_chunk = None
+        self._partials = None
+        # torch.cuda.Event x4 (already recorded once) -> per-kernel timing
+        self.profile_events = None
+
+    # -- slots --------------------------------------------------------------
+    def reset_slots(self):
+        self.n_slots = 0
+
+    def new_slot(self) -> int:
+        cap = self.slots.numel() // L.SLOT_BYTES
+        if self.n_slots >= cap:
+            grown = torch.zeros(2 * cap * L.SLOT_BYTES, dtype=torch.uint8, device=self.device)
+            grown[: self.slots.numel()].copy_(self.slots)
+            self.slots = grown
+        self.n_slots += 1
+        return self.n_slots - 1
+
+    # -- helpers ------------------------------------------------------------
+    def _stream(self) -> int:
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+    def _upload(self, arr: np.ndarray) -> torch.Tensor:
+        host = torch.from_numpy(arr.view(np.uint8).reshape(-1)).pin_memory()
+        return host.to(self.device, non_blocking=True)
+
+    def workspace(self, n_chunks: int) -> torch.Tensor:
+        need = max(2 * n_chunks, 2)
+        if self._partials is None or self._partials.numel() < need:
+            self._partials = torch.empty(need, dtype=torch.float32, device=self.device)
+        return self._partials
+
+    def _plan(self, numels: Tuple[int, ...]):
+        if numels != self._plan_key:
+            nch = (np.asarray(numels, dtype=np.int64) + L.CHUNK_ELEMS - 1) // L.CHUNK_ELEMS
+            total = int(nch.sum())
+            if total >= 2**31:
+                raise ValueError("LUMA: too many chunks for one launch")
+            first = np.zeros(len(numels), dtype=np.int64)
+            np.cumsum(nch[:-1], out=first[1:])
+            ch = np.empty(total, dtype=L.CHUNK_DTYPE)
+            ch["tensor"] = np.repeat(np.arange(len(numels), dtype=np.int32), nch)
+            ch["index"] = np.arange(total, dtype=np.int64) - np.repeat(first, nch)
+            self._chunks = self._upload(ch)
+            self._first_chunk = first.astype(np.int32)
+            self._n_chunks = total
+            self._plan_key = numels
+        return self._chunks, self._first_chunk, self._n_chunks
+
+    # -- entry points -------------------------------------------------------
+    def step(self, rows, hypers: np.ndarray, base_seed: int, noise_mode: int, flags: int = 0):
+        """rows: list of (param, grad, q_m, q_w, u_m, u_w, step, param_id, grad_code,
+        hyper_idx, slot)."""
+        n = len(rows)
+        numels = tuple(r[0].numel() for r in rows)
+        chunks, first, n_chunks = self._plan(numels)
+        tt = np.empty(n, dtype=L.TENSOR_DTYPE)
+        tt["param"] = [r[0].data_ptr() for r in rows]
+        tt["grad"] = [r[1].data_ptr() for r in rows]
+        tt["q_m"] = [r[2].data_ptr() for r in rows]
+        tt["q_w"] = [r[3].data_ptr() for r in rows]
+        tt["u_m"] = [_ptr(r[4]) for r in rows]
+        tt["u_w"] = [_ptr(r[5]) for r in rows]
+        tt["numel"] = numels
+        tt["step"] = [r[6] for r in rows]
+        tt["param_id"] = [r[7] for r in rows]
+        tt["grad_dtype"] = [r[8] for r in rows]
+        tt["hyper"] = [r[9] for r in rows]
+        tt["slot"] = [r[10] for r in rows]
+        tt["first_chunk"] = first
+        d_tensors = self._upload(tt)
+        d_hypers = self._upload(hypers)
+        partials = self.workspace(n_chunks)
+        args = L.StepArgs(
+            tensors=d_tensors.data_ptr(), n_tensors=n, n_chunks=n_chunks,
+            chunks=chunks.data_ptr(), hypers=d_hypers.data_ptr(),
+            slots=self.slots.data_ptr(), partials=partials.data_ptr(),
+            base_seed=base_seed & _MASK64, noise_mode=noise_mode, flags=flags)
+        if self.profile_events is None:
+            L.check(self.lib.luma_step(ctypes.byref(args), self._stream()), "luma_step")
+        else:
+            evs = (ctypes.c_void_p * 4)(*[e.cuda_event for e in self.profile_events])
+            L.check(self.lib.luma_step_profiled(ctypes.byref(args), self._stream(), evs),
+                    "luma_step_profiled")
+
+    def set_scales(self, items):
+        """items: list of (slot, step, S_m, S_v, eps)."""
+        arr = np.zeros(len(items), dtype=L.SCALE_INIT_DTYPE)
+        arr["slot"] = [i[0] for i in items]
+        arr["step"] = [i[1] for i in items]
+        arr["s_m"] = [i[2] for i in items]
+        arr["s_v"] = [i[3] for i in items]
+        arr["eps"] = [i[4] for i in items]
+        d = self._upload(arr)
+        L.check(self.lib.luma_set_scales(self.slots.data_ptr(), d.data_ptr(), len(items),
+                                         self._stream()), "luma_set_scales")
+
+    def get_scales(self, slots, steps):
+        """Returns a list of (S_m, S_v) Python floats (synchronises)."""
+        n = len(slots)
+        d_idx = self._upload(np.asarray(slots, dtype=np.int32))
+        d_steps = self._upload(np.asarray(steps, dtype=np.int64))
+        out = torch.empty(2 * n, dtype=torch.float64, device=self.device)
+        L.check(self.lib.luma_get_scales(self.slots.data_ptr(), d_idx.data_ptr(),
+                                         d_steps.data_ptr(), n, out.data_ptr(), self._stream()),
+                "luma_get_scales")
+        vals = out.cpu().tolist()
+        return [(vals[2 * i], vals[2 * i + 1]) for i in range(n)]
+
+    def decode(self, q_m, q_w, slot, step, eps, m_out, v_out):
+        L.check(self.lib.luma_decode(q_m.data_ptr(), q_w.data_ptr(), q_m.numel(),
+                                     self.slots.data_ptr(), slot, step, float(eps),
+                                     m_out.data_ptr(), v_out.data_ptr(), self._stream()),
+                "luma_decode")
+
+    def quantize(self, m, v, q_m, q_w, slot, step, eps, seed, noise_mode, u_m, u_w):
+        n = m.numel()
+        nch = (n + L.CHUNK_ELEMS - 1) // L.CHUNK_ELEMS
+        ws = torch.empty(max(2 * nch, 2), dtype=torch.float32, device=self.device)
+        L.check(self.lib.luma_quantize(m.data_ptr(), v.data_ptr(), n, q_m.data_ptr(),
+                                       q_w.data_ptr(), self.slots.data_ptr(), slot, step,
+                                       float(eps), seed & _MASK64, noise_mode, _ptr(u_m),
+                                       _ptr(u_w), ws.data_ptr(), self._stream()),
+                "luma_quantize")
+
+
+class LUMA(Optimizer):
+    r"""LUMA: Log-space Unbiased Momentum AdamW on the MI355X HIP backend.
+
+    Stores two int16 tensors per parameter (signed log-grid momentum ``Q_m``,
+    unsigned log-grid preconditioner ``Q_w``): 4 bytes/param of state.
+
+    ``backend`` accepts ``"auto"``, ``"hip"`` and ``"triton"`` (an alias kept
+    for drop-in use); all select the HIP library.  Parameters must be float32
+    and live on a ROCm GPU; gradients may be float32, bfloat16 or float16
+    (others are promoted to float32 first).
+    """
+
+    _BACKENDS = ("auto", "hip", "triton")
+
+    def __init__(self, params, lr: float = 1e-3, betas: Tuple[float, float] = (0.9, 0.999),
+                 eps: float = 1e-8, weight_decay: float = 0.01, backend: str = "auto"):
+        # optimizer.py:80-89
+        if lr < 0.0:
+            raise ValueError(f"Invalid learning rate: {lr}")
+        if eps <= 0.0:
+            raise ValueError(f"Invalid epsilon: {eps}")
+        if not 0.0 <= betas[0] < 1.0:
+            raise ValueError(f"Invalid beta1: {betas[0]}")
+        if not 0.0 <= betas[1] < 1.0:
+            raise ValueError(f"Invalid beta2: {betas[1]}")
+        if weight_decay < 0.0:
+            raise ValueError(f"Invalid weight_decay: {weight_decay}")
+        defaults = dict(lr=lr, betas=betas, eps=eps, weight_decay=weight_decay)
+        super().__init__(params, defaults)
+        # optimizer.py:94-96: one int64 draw from the global CPU generator
+        self._base_seed: int = int(
+            torch.randint(-(2**63), 2**63 - 1, (1,), dtype=torch.int64).item())
+        if backend not in self._BACKENDS:
+            raise ValueError(f"Invalid backend: {backend}. Expected one of "
+                             "{'auto', 'hip', 'triton'} (this build has the HIP backend only).")
+        self._engine: Optional[_Engine] = None
+        self._noise: Optional[Dict[int, Tuple[torch.Tensor, torch.Tensor]]] = None
+        self._flags = 0
+
+    # ------------------------------------------------------------------
+    #  Helpers
+    # ------------------------------------------------------------------
+    @staticmethod
+    def _unwrap_tensor(t):
+        """optimizer.py:399-407: DTensor -> local shard."""
+        if t is None:
+            return None
+        return t._local_tensor if hasattr(t, "_local_tensor") else t
+
+    def _get_engine(self, device: torch.device) -> _Engine:
+        if self._engine is None:
+            if device.type != "cuda":
+                raise RuntimeError(f"LUMA (HIP) steps parameters on a ROCm GPU; got device {device}")
+            self._engine = _Engine(device)
+        elif self._engine.device != device:
+            raise RuntimeError("LUMA (HIP): all parameters must be on one device "
+                               f"({self._engine.device} vs {device})")
+        return self._engine
+
+    def inject_noise(self, noise: Dict[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]):
+        """Use the given uniforms (u_m, u_w), float32 in [0, 1) with each parameter's
+        shape and device, for the next ``step()`` or ``import_adamw_state()``
+        instead of Philox draws.  Every parameter updated by that call needs an
+        entry."""
+        self._noise = {id(p): (u_m, u_w) for p, (u_m, u_w) in noise.items()}
+
+    def _take_noise(self, p, like):
+        if self._noise is None:
+            return None, None
+        if id(p) not in self._noise:
+            raise ValueError("LUMA.inject_noise: missing uniforms for a parameter")
+        u_m, u_w = self._noise[id(p)]
+        out = []
+        for u in (u_m, u_w):
+            u = u.to(device=like.device, dtype=torch.float32)
+            if u.shape != like.shape:
+                raise ValueError("LUMA.inject_noise: uniform shape mismatch")
+            if u.stride() != like.stride():
+                u = torch.empty_like(like, dtype=torch.float32).copy_(u)
+            out.append(u)
+        return out[0], out[1]
+
+    @staticmethod
+    def _hyper_row(group, t: int):
+        b1, b2 = group["betas"]
+        lr, wd, eps = group["lr"], group["weight_decay"], group["eps"]
+        bc1 = 1.0 - b1 ** t       # functional.py:209,262 (1 - b1 at t = 1)
+        bc2 = 1.0 - b2 ** t
+        eta = lr / bc1
+        return (b1, 1.0 - b1, b2, 1.0 - b2, 1.0 - wd * lr, -eta, bc2, eps, eps)
+
+    # ------------------------------------------------------------------
+    #  Checkpoint: portable save / load  (optimizer.py:119-183)
+    # ------------------------------------------------------------------
+    def state_dict(self) -> dict:
+        raw = super().state_dict()
+        keys, slots, steps = [], [], []
+        for idx, s in raw["state"].items():
+            if "_slot" in s:
+                keys.append(idx)
+                slots.append(s["_slot"])
+                steps.append(s["step"])
+        clean = {idx: {k: v for k, v in s.items() if not k.startswith("_")}
+                 for idx, s in raw["state"].items()}
+        if keys:
+            for idx, (sm, sv) in zip(keys, self._engine.get_scales(slots, steps)):
+                clean[idx]["S_m"] = sm
+                clean[idx]["S_v"] = sv
+        raw["state"] = clean
+        raw["_base_seed"] = self._base_seed
+        return raw
+
+    def load_state_dict(self, state_dict: dict) -> None:
+        self._base_seed = state_dict.get("_base_seed", self._base_seed)
+        super().load_state_dict(state_dict)
+        pending = []
+        for group in self.param_groups:
+            for p in group["params"]:
+                state = self.state[p]
+                if len(state) == 0:
+                    continue
+                param = self._unwrap_tensor(p)
+                for key in ("Q_m", "Q_w"):
+                    # torch's load casts state tensors of a float parameter to the
+                    # parameter's dtype (Optimizer._process_value_according_to_param_policy);
+                    # the codes are exact integers, so restore int16 in the param's layout.
+                    if key in state:
+                        q = state[key]
+                        if (q.dtype != torch.int16 or q.device != param.device
+                                or q.stride() != param.stride()):
+                            fixed = torch.empty_like(param, dtype=torch.int16)
+                            fixed.copy_(q.reshape(param.shape))
+                            state[key] = fixed
+                if "S_m" not in state:
+                    raise ValueError("LUMA.load_state_dict: state without S_m/S_v")
+                pending.append((p, param, state, group["eps"]))
+        if not pending:
+            return
+        engine = self._get_engine(pending[0][1].device)
+        engine.reset_slots()
+        items = []
+        for _, param, state, eps in pending:
+            self._get_engine(param.device)
+            state["_slot"] = engine.new_slot()
+            items.append((state["_slot"], state["step"], float(state.pop("S_m")),
+                          float(state.pop("S_v")), eps))
+        engine.set_scales(items)
+
+    # ------------------------------------------------------------------
+    #  AdamW interop  (optimizer.py:189-335)
+    # ------------------------------------------------------------------
+    def export_adamw_state(self) -> dict:
+        param_to_idx: Dict[int, int] = {}
+        for group in self.param_groups:
+            for p in group["params"]:
+                param_to_idx[id(p)] = len(param_to_idx)
+        adamw_state: dict = {}
+        for group in self.param_groups:
+            eps = group["eps"]
+            for p in group["params"]:
+                state = self.state[p]
+                if len(state) == 0:
+                    continue
+                param = self._unwrap_tensor(p)
+                engine = self._get_engine(param.device)
+                exp_avg = torch.empty_like(param, dtype=torch.float32)
+                exp_avg_sq = torch.empty_like(param, dtype=torch.float32)
+                engine.decode(state["Q_m"], state["Q_w"], state["_slot"], state["step"], eps,
+                              exp_avg, exp_avg_sq)
+                adamw_state[param_to_idx[id(p)]] = {
+                    "step": torch.tensor(float(state["step"])),
+                    "exp_avg": exp_avg,
+                    "exp_avg_sq": exp_avg_sq,
+                }
+        param_groups = []
+        for group in self.param_groups:
+            pg = {k: v for k, v in group.items() if k != "params"}
+            pg["params"] = [param_to_idx[id(p)] for p in group["params"]]
+            param_groups.append(pg)
+        return {"state": adamw_state, "param_groups": param_groups}
+
+    def import_adamw_state(self, adamw_sd: dict) -> None:
+        all_params = []
+        group_of = {}
+        for group in self.param_groups:
+            for p in group["params"]:
+                group_of[len(all_params)] = group
+                all_params.append(p)
+        noise_mode = L.NOISE_INJECTED if self._noise is not None else L.NOISE_PHILOX
+        for idx_key, s in adamw_sd["state"].items():
+            idx = int(idx_key) if isinstance(idx_key, str) else idx_key
+            if idx >= len(all_params):
+                raise ValueError(f"AdamW state has index {idx} but LUMA only has "
+                                 f"{len(all_params)} parameters")
+            p = all_params[idx]
+            group = group_of[idx]
+            step_val = s["step"]
+            step = int(step_val.item() if isinstance(step_val, torch.Tensor) else step_val)
+            param = self._unwrap_tensor(p)
+            engine = self._get_engine(param.device)
+            m = torch.empty_like(param, dtype=torch.float32).copy_(s["exp_avg"])
+            v = torch.empty_like(param, dtype=torch.float32).copy_(s["exp_avg_sq"])
+            q_m = torch.empty_like(param, dtype=torch.int16)
+            q_w = torch.empty_like(param, dtype=torch.int16)
+            state = self.state[p]
+            slot = state["_slot"] if "_slot" in state else engine.new_slot()
+            u_m, u_w = self._take_noise(p, param)
+            seed = make_step_seed(self._base_seed, 0, idx)   # optimizer.py:315-317
+            engine.quantize(m, v, q_m, q_w, slot, step, group["eps"], seed, noise_mode, u_m, u_w)
+            state["step"] = step
+            state["param_id"] = idx
+            state["Q_m"] = q_m
+            state["Q_w"] = q_w
+            state["_slot"] = slot
+        self._noise = None
+
+    # ------------------------------------------------------------------
+    #  Main entry point  (optimizer.py:413-524)
+    # ------------------------------------------------------------------
+    @torch.no_grad()
+    def step(self, closure=None):
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+
+        work = []
+        param_idx = 0
+        for gi, group in enumerate(self.param_groups):
+            for p in group["params"]:
+                param_idx += 1
+                if p.grad is None:
+                    continue
+                param = self._unwrap_tensor(p)
+                grad = self._unwrap_tensor(p.grad)
+                if param.numel() == 0:
+                    continue
+                if grad.is_sparse:
+                    raise RuntimeError("LUMA does not support sparse gradients")
+                if param.dtype != torch.float32:
+                    raise ValueError(
+                        f"LUMA requires float32 parameters (got {param.dtype}). "
+                        f"Use torch.amp.autocast() or FSDP MixedPrecision "
+                        f"instead of casting model weights to a reduced dtype.")
+                if not param.is_cuda:
+                    raise RuntimeError(
+                        f"LUMA (HIP) steps parameters on a ROCm GPU; got device {param.device}")
+                if not _is_dense(param):
+                    raise ValueError("LUMA requires dense (contiguous) parameters")
+                work.append((gi, p, param, grad, param_idx - 1))
+        if not work:
+            self._noise = None
+            return loss
+
+        engine = self._get_engine(work[0][2].device)
+        noise_mode = L.NOISE_INJECTED if self._noise is not None else L.NOISE_PHILOX
+        hyper_index: Dict[Tuple[int, int], int] = {}
+        hyper_rows = []
+        rows = []
+        for gi, p, param, grad, pidx in work:
+            engine_dev = self._get_engine(param.device)  # noqa: F841  (one device)
+            state = self.state[p]
+            if len(state) == 0:
+                state["step"] = 0
+                state["param_id"] = pidx
+            state["step"] += 1
+            t = state["step"]
+            if t == 1 or "Q_m" not in state:
+                state["Q_m"] = torch.empty_like(param, dtype=torch.int16)
+                state["Q_w"] = torch.empty_like(param, dtype=torch.int16)
+            if "_slot" not in state:
+                state["_slot"] = engine.new_slot()
+            code = _GRAD_CODES.get(grad.dtype)
+            if code is None:
+                grad = grad.float()
+                code = L.GRAD_F32
+            if grad.device != param.device:
+                grad = grad.to(param.device)
+            if grad.stride() != param.stride() or not _is_dense(grad):
+                grad = torch.empty_like(param, dtype=grad.dtype).copy_(grad)
+            key = (gi, t)
+            if key not in hyper_index:
+                hyper_index[key] = len(hyper_rows)
+                hyper_rows.append(self._hyper_row(self.param_groups[gi], t))
+            u_m, u_w = self._take_noise(p, param)
+            rows.append((param, grad, state["Q_m"], state["Q_w"], u_m, u_w, t,
+                         state["param_id"], code, hyper_index[key], state["_slot"]))
+        hypers = np.array(hyper_rows, dtype=np.float64)
+        harr = np.empty(len(hyper_rows), dtype=L.HYPER_DTYPE)
+        for j, name in enumerate(L.HYPER_DTYPE.names):
+            harr[name] = hypers[:, j]
+        engine.step(rows, harr, self._base_seed, noise_mode, self._flags)
+        self._noise = None
+        return loss

@@ -1,0 +1,98 @@
+"""HIP step vs the CPU oracle on identical inputs and injected uniforms.
+
+Against the correctly rounded oracle ("cr") the int16 states and scales must
+agree exactly, and the parameters within 1e-6 of the tensor's scale (the AdamW
+update itself is not bit-matched).  The comparison with the reference's own
+outputs is in test_gpu_golden.py.
+"""
+
+import pytest
+import torch
+
+from parity_util import normal_grads, run_pair
+
+pytestmark = pytest.mark.gpu
+
+P_TOL = 1e-6
+
+
+def _check_exact(res):
+    for s in res.steps:
+        assert s.qm_mismatch == 0 and s.qw_mismatch == 0, s
+        assert s.s_exact, s
+        assert s.p_rel <= P_TOL, s
+
+
+SIZES = [(1,), (127,), (4096,), (65543,), (300, 1000)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_exact_vs_cr_oracle(dtype):
+    print(f"case exact dtype={dtype}", flush=True)
+    res = run_pair(SIZES, normal_grads(1e-3, dtype), n_steps=4, math_mode="cr")
+    _check_exact(res)
+
+
+def test_exact_other_hyperparams():
+    hyper = dict(lr=5e-4, betas=(0.95, 0.98), eps=1e-6, weight_decay=0.1)
+    res = run_pair([(2048,), (33, 77)], normal_grads(3e-2), n_steps=5, math_mode="cr",
+                   hyper=hyper)
+    _check_exact(res)
+
+
+def test_exact_zero_grads():
+    """All-zero grads: S_v = 0 -> delta_w = 0 -> Q_w == 0 (functional.py:166-171)."""
+    res = run_pair([(300,), (5000,)], lambda t, i, s: torch.zeros(s), n_steps=3, math_mode="cr")
+    _check_exact(res)
+
+
+def test_exact_outliers_and_zeros():
+    def grads(t, i, shape):
+        g = torch.Generator().manual_seed(77 * t + i)
+        x = torch.randn(shape, generator=g) * 1e-4
+        x[torch.rand(shape, generator=g) < 0.01] = 0.0
+        x[torch.rand(shape, generator=g) < 0.001] *= 100.0
+        return x.to(torch.bfloat16)
+    res = run_pair([(70001,), (1,), (4096,)], grads, n_steps=4, math_mode="cr")
+    _check_exact(res)
+
+
+def test_exact_heterogeneous_scales():
+    """Per-tensor grad std from 1e-7 to 1e-1, fp16 grads (GradScaler-style unscale)."""
+    stds = [1e-7, 1e-5, 1e-3, 1e-1]
+
+    def grads(t, i, shape):
+        g = torch.Generator().manual_seed(31 * t + i)
+        x = torch.randn(shape, generator=g) * stds[i]
+        g16 = (x * 2.0 ** 16).half()
+        return (g16.float() * 2.0 ** -16).half()
+    res = run_pair([(8192,)] * 4, grads, n_steps=4, math_mode="cr")
+    _check_exact(res)
+
+
+def test_multi_group_exact():
+    res = run_pair([(64, 32), (32,), (16, 8), (8,)], normal_grads(1e-2), n_steps=3,
+                   math_mode="cr", groups_split=2)
+    _check_exact(res)
+
+
+def test_single_step_vs_host_torch_math():
+    """One step from a shared state vs the oracle with this host's torch CPU math.
+
+    The strict criterion (<= 1e-5 of codes) is checked against the reference's
+    own golden outputs in test_gpu_golden.py.  Here the oracle calls this host's
+    MKL/SLEEF kernels, whose rounding depends on the CPU: measured non-correctly
+    rounded fractions for float32 sqrt / log are ~0% / 2e-5 on the Intel build
+    host but 16% / 0.9% on an AMD EPYC host, which moves ~1e-4 of the codes by
+    one.  The bound below covers both; S and parameters stay within 1e-6.
+    """
+    res = run_pair([(1 << 20,), (300, 1000)], normal_grads(1e-3, torch.bfloat16), n_steps=5,
+                   math_mode="torch", resync=True)
+    for s in res.steps:
+        rate = (s.qm_mismatch + s.qw_mismatch) / (2 * s.n)
+        print(f"step {s.t}: mismatch rate {rate:.2e} max|dQ| {s.q_max_abs_diff} "
+              f"S rel {s.s_rel:.2e} p rel {s.p_rel:.2e}", flush=True)
+        assert s.q_max_abs_diff <= 1
+        assert rate <= 5e-4
+        assert s.s_rel <= 1e-6
+        assert s.p_rel <= 1e-6

@@ -1,0 +1,152 @@
+"""Host-side checks that need no GPU: the C ABI library, Philox, API contract."""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+import torch.nn as nn
+
+import luma_amd
+from luma_amd import LUMA
+from luma_amd import _lib as L
+from luma_amd.optimizer import make_step_seed
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_symbols():
+    text = open(os.path.join(ROOT, "include", "luma.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(luma_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = L.load()
+    names = _declared_symbols()
+    assert "luma_step" in names and len(names) >= 9
+    for name in names:
+        assert hasattr(lib, name), name
+        assert ctypes.cast(getattr(lib, name), ctypes.c_void_p).value
+
+
+def test_layout_and_version():
+    lib = L.load()
+    assert lib.luma_abi_version() == L.ABI_VERSION
+    L.check_layout(lib)
+    assert lib.luma_workspace_bytes(10) == 80
+
+
+# Random123 known-answer vectors for philox4x32_10 (kat_vectors).
+PHILOX_KAT = [
+    ([0, 0, 0, 0], [0, 0], [0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8]),
+    ([0xFFFFFFFF] * 4, [0xFFFFFFFF] * 2, [0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD]),
+    ([0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344], [0xA4093822, 0x299F31D0],
+     [0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1]),
+]
+
+# The same block function as computed by Triton's tl.randint4x (an independent
+# implementation) for key = 0x123456789abcdef0 and counters (i, 0, 0, 0).
+PHILOX_TRITON = [
+    (0, [0x092C9B44, 0x78384BC0, 0xC9FB80BE, 0x2B3BE4DD]),
+    (3, [0xF708969C, 0x62778C12, 0xE11922B4, 0x6D6AF8E0]),
+    (7, [0x2A23B679, 0x84C69006, 0x0481A097, 0x0AE2270E]),
+]
+
+
+@pytest.mark.parametrize("ctr,key,out", PHILOX_KAT)
+def test_philox_known_answers(ctr, key, out):
+    assert L.philox4x32(ctr, key) == out
+
+
+@pytest.mark.parametrize("i,out", PHILOX_TRITON)
+def test_philox_matches_triton(i, out):
+    seed = 0x123456789ABCDEF0
+    assert L.philox4x32([i, 0, 0, 0], [seed & 0xFFFFFFFF, seed >> 32]) == out
+
+
+def test_step_seed_matches_reference_formula():
+    # functional.py:99-106
+    for base in [0, 12345, -(2**63), 2**63 - 1, -987654321]:
+        for t in [0, 1, 2, 1000]:
+            for pid in [0, 1, 77]:
+                assert make_step_seed(base, t, pid) == ((t << 32) | (2 * pid)) ^ base
+
+
+# ── API contract (optimizer.py:71-113), no GPU needed ────────────────────────
+
+def test_default_params():
+    assert LUMA(nn.Linear(8, 4).parameters()) is not None
+
+
+def test_custom_params():
+    opt = LUMA(nn.Linear(8, 4).parameters(), lr=5e-4, betas=(0.95, 0.98), eps=1e-6,
+               weight_decay=0.1)
+    assert opt.defaults["lr"] == 5e-4
+
+
+def test_invalid_backend():
+    with pytest.raises(ValueError, match="Invalid backend"):
+        LUMA(nn.Linear(8, 4).parameters(), backend="tritonn")
+
+
+@pytest.mark.parametrize("kwargs", [{"lr": -1}, {"eps": -1}, {"eps": 0}, {"betas": (1.0, 0.999)},
+                                    {"betas": (0.9, -0.1)}, {"weight_decay": -0.01}])
+def test_invalid_hyperparams(kwargs):
+    with pytest.raises(ValueError):
+        LUMA(nn.Linear(4, 2).parameters(), **kwargs)
+
+
+def test_base_seed_from_global_generator():
+    torch.manual_seed(42)
+    a = LUMA([torch.zeros(3, requires_grad=True)])._base_seed
+    torch.manual_seed(42)
+    b = int(torch.randint(-(2**63), 2**63 - 1, (1,), dtype=torch.int64).item())
+    assert a == b
+
+
+def test_step_without_grads_is_noop():
+    opt = LUMA(nn.Linear(8, 4).parameters())
+    assert opt.step() is None
+
+
+def test_cpu_params_fail_loudly():
+    """No CPU fallback: the step refuses parameters that are not on the GPU."""
+    model = nn.Linear(8, 4)
+    opt = LUMA(model.parameters())
+    model(torch.randn(2, 8)).sum().backward()
+    with pytest.raises(RuntimeError, match="GPU"):
+        opt.step()
+
+
+def test_rejects_reduced_precision_params():
+    model = nn.Linear(16, 8).to(torch.bfloat16)
+    opt = LUMA(model.parameters())
+    for p in model.parameters():
+        p.grad = torch.randn_like(p)
+    with pytest.raises(ValueError, match="float32"):
+        opt.step()
+
+
+def test_sparse_grad_rejected():
+    emb = nn.Embedding(10, 4, sparse=True)
+    opt = LUMA(emb.parameters())
+    emb(torch.tensor([1, 2])).sum().backward()
+    with pytest.raises(RuntimeError, match="sparse"):
+        opt.step()
+
+
+def test_hyper_row_matches_reference_scalars():
+    """Coefficients are the reference's double expressions (functional.py:209-214,262-279)."""
+    g = {"betas": (0.9, 0.999), "lr": 1e-3, "weight_decay": 0.01, "eps": 1e-8}
+    row = LUMA._hyper_row(g, 7)
+    assert row == (0.9, 1.0 - 0.9, 0.999, 1.0 - 0.999, 1.0 - 0.01 * 1e-3,
+                   -(1e-3 / (1.0 - 0.9 ** 7)), 1.0 - 0.999 ** 7, 1e-8, 1e-8)
+    row1 = LUMA._hyper_row(g, 1)
+    assert row1[5] == -(1e-3 / (1.0 - 0.9)) and row1[6] == 1.0 - 0.999
+
+
+def test_package_exports():
+    assert luma_amd.__all__ == ["LUMA", "get_kernel_config"]
+    assert "CHUNK_ELEMS" in luma_amd.get_kernel_config()
