@@ -18,6 +18,7 @@
 
 #include "../../include/luma.h"
 #include "luma_exact.h"
+#include "luma_fast.h"
 #include "luma_philox.h"
 
 namespace luma {
@@ -28,13 +29,24 @@ constexpr int64_t kChunk = LUMA_CHUNK_ELEMS;
 static_assert(kChunk % (kThreads * kVec) == 0, "chunk must be a whole number of iterations");
 static_assert(sizeof(LumaHyper) == sizeof(Hyper), "hyper layout");
 
-struct Tensor {  // mirror of LumaTensor
-  float *param;
-  const void *grad;
-  int16_t *q_m;
-  int16_t *q_w;
-  const float *u_m;
-  const float *u_w;
+// Device view of LumaTensor.  The pointer fields are declared in the global
+// address space so loads and stores through them compile to global_* (not
+// flat_*) instructions.
+#if defined(__HIP_DEVICE_COMPILE__)
+#define LUMA_GLOBAL __attribute__((address_space(1)))
+#else
+#define LUMA_GLOBAL
+#endif
+typedef float vf4 __attribute__((ext_vector_type(4)));
+typedef uint32_t vu4 __attribute__((ext_vector_type(4)));
+
+struct Tensor {
+  LUMA_GLOBAL float *param;
+  const LUMA_GLOBAL void *grad;
+  LUMA_GLOBAL int16_t *q_m;
+  LUMA_GLOBAL int16_t *q_w;
+  const LUMA_GLOBAL float *u_m;
+  const LUMA_GLOBAL float *u_w;
   int64_t numel;
   int64_t step;
   int64_t param_id;
@@ -45,9 +57,9 @@ struct Tensor {  // mirror of LumaTensor
 };
 static_assert(sizeof(Tensor) == sizeof(LumaTensor), "tensor layout");
 
-__device__ __forceinline__ float load_grad(const void *g, int64_t i, int dt) {
-  if (dt == LUMA_GRAD_F32) return static_cast<const float *>(g)[i];
-  const uint16_t b = static_cast<const uint16_t *>(g)[i];
+__device__ __forceinline__ float load_grad(const LUMA_GLOBAL void *g, int64_t i, int dt) {
+  if (dt == LUMA_GRAD_F32) return ((const LUMA_GLOBAL float *)g)[i];
+  const uint16_t b = ((const LUMA_GLOBAL uint16_t *)g)[i];
   if (dt == LUMA_GRAD_BF16) return __uint_as_float((uint32_t)b << 16);
   return __half2float(__ushort_as_half(b));
 }
@@ -98,7 +110,7 @@ __device__ __forceinline__ void element_ema(const Tensor &T, const Hyper &h, con
   exact_ema(m, v, g, h, mn, vn);
 }
 
-__global__ __launch_bounds__(kThreads) void pass1_kernel(const Tensor *__restrict__ tensors,
+__global__ __launch_bounds__(kThreads) void pass1_exact_kernel(const Tensor *__restrict__ tensors,
                                                          const LumaChunk *__restrict__ chunks,
                                                          const Hyper *__restrict__ hypers,
                                                          const Slot *__restrict__ slots,
@@ -153,10 +165,11 @@ __global__ __launch_bounds__(64) void finalize_kernel(const Tensor *__restrict__
     s.s_m[par] = s_m;
     s.s_v[par] = s_v;
     make_grid(s_m, s_v, hypers[T.hyper].eps_d, s.grid[par]);
+    make_fast(s.grid[par]);
   }
 }
 
-__global__ __launch_bounds__(kThreads) void pass2_kernel(const Tensor *__restrict__ tensors,
+__global__ __launch_bounds__(kThreads) void pass2_exact_kernel(const Tensor *__restrict__ tensors,
                                                          const LumaChunk *__restrict__ chunks,
                                                          const Hyper *__restrict__ hypers,
                                                          const Slot *__restrict__ slots,
@@ -202,6 +215,449 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const Tensor *__restric
 }
 
 // ---------------------------------------------------------------------------
+//  Fast path: 8 consecutive elements per thread per iteration, 16-byte
+//  loads/stores, certified decisions, exact fallback for flagged elements.
+// ---------------------------------------------------------------------------
+
+struct Group8 {
+  int qm[kVec];   // signed momentum codes
+  int qw[kVec];   // unsigned preconditioner codes
+  float g[kVec];  // gradient promoted to float32
+};
+
+__device__ __forceinline__ void unpack_i16(uint32_t w, int &lo, int &hi) {
+  lo = (int)(int16_t)(w & 0xFFFFu);
+  hi = (int)w >> 16;
+}
+
+__device__ __forceinline__ void unpack_u16(uint32_t w, int &lo, int &hi) {
+  lo = (int)(w & 0xFFFFu);
+  hi = (int)(w >> 16);
+}
+
+template <int GD>
+__device__ __forceinline__ float grad_lo(uint32_t w) {
+  if (GD == LUMA_GRAD_BF16) return __uint_as_float(w << 16);
+  return __half2float(__ushort_as_half((uint16_t)(w & 0xFFFFu)));
+}
+
+template <int GD>
+__device__ __forceinline__ float grad_hi(uint32_t w) {
+  if (GD == LUMA_GRAD_BF16) return __uint_as_float(w & 0xFFFF0000u);
+  return __half2float(__ushort_as_half((uint16_t)(w >> 16)));
+}
+
+// Load the codes and gradients of elements e0 .. e0+7 (n of them valid).
+template <int GD>
+__device__ __forceinline__ void load_group(const Tensor &T, int64_t e0, int n, bool vec, Group8 &G) {
+  if (vec) {
+    const vu4 a = *(const LUMA_GLOBAL vu4 *)(T.q_m + e0);
+    const vu4 b = *(const LUMA_GLOBAL vu4 *)(T.q_w + e0);
+    unpack_i16(a.x, G.qm[0], G.qm[1]);
+    unpack_i16(a.y, G.qm[2], G.qm[3]);
+    unpack_i16(a.z, G.qm[4], G.qm[5]);
+    unpack_i16(a.w, G.qm[6], G.qm[7]);
+    unpack_u16(b.x, G.qw[0], G.qw[1]);
+    unpack_u16(b.y, G.qw[2], G.qw[3]);
+    unpack_u16(b.z, G.qw[4], G.qw[5]);
+    unpack_u16(b.w, G.qw[6], G.qw[7]);
+    if (GD == LUMA_GRAD_F32) {
+      const vf4 g0 = *(const LUMA_GLOBAL vf4 *)((const LUMA_GLOBAL float *)T.grad + e0);
+      const vf4 g1 = *(const LUMA_GLOBAL vf4 *)((const LUMA_GLOBAL float *)T.grad + e0 + 4);
+      G.g[0] = g0.x; G.g[1] = g0.y; G.g[2] = g0.z; G.g[3] = g0.w;
+      G.g[4] = g1.x; G.g[5] = g1.y; G.g[6] = g1.z; G.g[7] = g1.w;
+    } else {
+      const vu4 gw = *(const LUMA_GLOBAL vu4 *)((const LUMA_GLOBAL uint16_t *)T.grad + e0);
+      G.g[0] = grad_lo<GD>(gw.x); G.g[1] = grad_hi<GD>(gw.x);
+      G.g[2] = grad_lo<GD>(gw.y); G.g[3] = grad_hi<GD>(gw.y);
+      G.g[4] = grad_lo<GD>(gw.z); G.g[5] = grad_hi<GD>(gw.z);
+      G.g[6] = grad_lo<GD>(gw.w); G.g[7] = grad_hi<GD>(gw.w);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) {
+      const bool ok = j < n;
+      G.qm[j] = ok ? (int)T.q_m[e0 + j] : 0;
+      G.qw[j] = ok ? (int)(uint16_t)T.q_w[e0 + j] : 0;
+      G.g[j] = ok ? load_grad(T.grad, e0 + j, GD) : 0.0f;
+    }
+  }
+}
+
+__device__ __forceinline__ bool tensor_vec_ok(const Tensor &T) {
+  const uintptr_t bits = (uintptr_t)T.param | (uintptr_t)T.grad | (uintptr_t)T.q_m |
+                         (uintptr_t)T.q_w | (uintptr_t)T.u_m | (uintptr_t)T.u_w;
+  return (bits & 15u) == 0;
+}
+
+// Exact path for one element, kept out of line so that its float64 constants
+// are not hoisted into (and do not crowd) the registers of the fast loops.
+// Takes the element's old codes and gradient; returns (m', v').
+__device__ __noinline__ float2 exact_mv(int qm, int qw, float g, const LUMA_GLOBAL Grid *old,
+                                        Hyper h) {
+  float m = 0.0f, v = 0.0f;
+  if (old) {
+    m = exact_decode_m(qm, old->dm);
+    v = exact_decode_v(qw, old->wmin, old->dw, h.eps);
+  }
+  float mn, vn;
+  exact_ema(m, v, g, h, mn, vn);
+  return make_float2(mn, vn);
+}
+
+// New codes of one element (int16 momentum code | uint16 preconditioner << 16).
+__device__ __noinline__ uint32_t exact_codes(int qm, int qw, float g, const LUMA_GLOBAL Grid *old,
+                                             const LUMA_GLOBAL Grid *nw, Hyper h, float um,
+                                             float uw) {
+  const float2 e = exact_mv(qm, qw, g, old, h);
+  const Grid G = *nw;
+  const int cm = exact_quant_m(e.x, G, um);
+  const int cw = exact_quant_w(e.y, G, h.eps, uw);
+  return ((uint32_t)cm & 0xFFFFu) | ((uint32_t)cw << 16);
+}
+
+// Per-wave queue of elements whose fast result is not certified.  Elements
+// are appended with ballot/mbcnt (no atomics) and run through the exact path
+// 64 at a time, one per lane, so the exact path runs at full SIMD width.
+constexpr int kQueueCap = kVec * 64 + 64;
+
+__device__ __forceinline__ uint32_t lane_id() {
+  return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+}
+
+// Position of this lane's entry among the lanes of `mask`, offset by base.
+__device__ __forceinline__ uint32_t queue_pos(uint64_t mask, uint32_t base) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                   __builtin_amdgcn_mbcnt_lo((uint32_t)mask, base));
+}
+
+// Decode constants of the fast path.  At t = 1 there is nothing to decode:
+// all-zero constants make the fast decode return m = v = 0 exactly whatever
+// the (uninitialised) codes are, so the loops carry no branch for it.
+struct DecodeK {
+  float dm, dw, iwmin, eps;
+};
+
+__device__ __forceinline__ DecodeK decode_consts(const LUMA_GLOBAL Grid *old, float eps) {
+  DecodeK k;
+  k.dm = old ? old->dm : 0.0f;
+  k.dw = old ? old->dw : 0.0f;
+  k.iwmin = old ? old->fast[kIwmin] : 0.0f;
+  k.eps = old ? eps : 0.0f;
+  return k;
+}
+
+// Pass 1 body: exact max |m'| and max v' of the chunk.  Fast values are
+// tracked per lane; an element needs the exact path only when its certified
+// upper bound reaches the lane's certified lower bound of the maximum.  Such
+// candidates go through the wave's queue.
+template <int GD, bool SMALL>
+__device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOBAL Grid *old,
+                                int64_t beg, int64_t end, float &exm, float &exv,
+                                uint32_t *queue) {
+  const Bounds B = make_bounds((const Grid *)old, nullptr, h.beta1, h.beta2);
+  const DecodeK D = decode_consts(old, h.eps);
+  const bool vec_ok = tensor_vec_ok(T);
+  const float lo_m = 1.0f - B.dlt_m, hi_m = 1.0f / (1.0f + B.dlt_m);
+  const float lo_v = 1.0f - B.dlt_v, hi_v = 1.0f / (1.0f + B.dlt_v);
+  const float sub_m = 2.0f * B.abs_m, sub_v = 2.0f * B.abs_v;
+  const uint32_t lane = lane_id();
+  float Mm = -INFINITY, Mv = -INFINITY, Tm = -INFINITY, Tv = -INFINITY;
+  uint32_t qlen = 0;
+  auto run = [&](uint32_t off) {
+    const int64_t i = beg + off;
+    const float2 e = exact_mv(T.q_m[i], (int)(uint16_t)T.q_w[i], load_grad(T.grad, i, GD), old, h);
+    exm = nan_max(exm, fabsf(e.x));
+    exv = nan_max(exv, e.y);
+  };
+  // Every lane runs the same number of iterations (lanes past the end carry
+  // n = 0), so the ballots and the queue length stay uniform across the wave.
+  const int n_it = (int)((end - beg + kThreads * kVec - 1) / (kThreads * kVec));
+  for (int it = 0; it < n_it; ++it) {
+    const int64_t e0 = beg + ((int64_t)it * kThreads + threadIdx.x) * kVec;
+    const int64_t rem = end - e0;
+    const int n = rem <= 0 ? 0 : (rem < kVec ? (int)rem : kVec);
+    Group8 G;
+    load_group<GD>(T, e0, n, vec_ok && n == kVec, G);
+    float am[kVec], av[kVec];
+    float im = -INFINITY, iv = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) {
+      const FastEma f = fast_ema<SMALL>(G.qm[j], G.qw[j], G.g[j], D.dm, D.dw, D.iwmin, D.eps,
+                                        h.beta1, h.omb1, h.beta2, h.omb2);
+      am[j] = j < n ? fabsf(f.mn) : -INFINITY;
+      av[j] = j < n ? f.vn : -INFINITY;
+      im = nan_max(im, am[j]);
+      iv = nan_max(iv, av[j]);
+    }
+    uint32_t cand = 0;
+    if (im >= Tm || iv >= Tv || im != im || iv != iv) {
+      Mm = nan_max(Mm, im);
+      Mv = nan_max(Mv, iv);
+      Tm = (Mm * lo_m - sub_m) * hi_m;
+      Tv = (Mv * lo_v - sub_v) * hi_v;
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) {
+        const bool c = am[j] >= Tm || av[j] >= Tv || am[j] != am[j] || av[j] != av[j];
+        cand |= (c && j < n) ? (1u << j) : 0u;
+      }
+    }
+    if (__ballot(cand != 0)) {
+      const uint32_t off0 = (uint32_t)(e0 - beg);
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) {
+        const bool f = (cand >> j) & 1u;
+        const uint64_t bm = __ballot(f);
+        if (f) queue[queue_pos(bm, qlen)] = off0 + j;
+        qlen += (uint32_t)__popcll(bm);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      while (qlen >= 64) {
+        qlen -= 64;
+        run(queue[qlen + lane]);
+      }
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  if (lane < qlen) run(queue[lane]);
+}
+
+__global__ __launch_bounds__(kThreads) void pass1_fast_kernel(const Tensor *__restrict__ tensors,
+                                                              const LumaChunk *__restrict__ chunks,
+                                                              const Hyper *__restrict__ hypers,
+                                                              const Slot *__restrict__ slots,
+                                                              float *__restrict__ partials) {
+  const LumaChunk c = chunks[blockIdx.x];
+  const Tensor T = tensors[c.tensor];
+  const Hyper h = hypers[T.hyper];
+  const LUMA_GLOBAL Grid *old =
+      T.step >= 2 ? (const LUMA_GLOBAL Grid *)&slots[T.slot].grid[(T.step - 1) & 1] : nullptr;
+  const int64_t beg = (int64_t)c.index * kChunk;
+  const int64_t end = beg + kChunk < T.numel ? beg + kChunk : T.numel;
+  const bool small = old == nullptr || old->fast[kXTopM] <= kSmall;
+  __shared__ uint32_t qbuf[kThreads / 64][kQueueCap];
+  uint32_t *q = qbuf[threadIdx.x >> 6];
+  float exm = 0.0f, exv = 0.0f;
+  if (T.grad_dtype == LUMA_GRAD_BF16) {
+    if (small) pass1_fast_body<LUMA_GRAD_BF16, true>(T, h, old, beg, end, exm, exv, q);
+    else pass1_fast_body<LUMA_GRAD_BF16, false>(T, h, old, beg, end, exm, exv, q);
+  } else if (T.grad_dtype == LUMA_GRAD_F16) {
+    if (small) pass1_fast_body<LUMA_GRAD_F16, true>(T, h, old, beg, end, exm, exv, q);
+    else pass1_fast_body<LUMA_GRAD_F16, false>(T, h, old, beg, end, exm, exv, q);
+  } else {
+    if (small) pass1_fast_body<LUMA_GRAD_F32, true>(T, h, old, beg, end, exm, exv, q);
+    else pass1_fast_body<LUMA_GRAD_F32, false>(T, h, old, beg, end, exm, exv, q);
+  }
+  block_max2(exm, exv);
+  if (threadIdx.x == 0) {
+    partials[2 * (int64_t)blockIdx.x] = exm;
+    partials[2 * (int64_t)blockIdx.x + 1] = exv;
+  }
+}
+
+// Certified LogSR decision (see luma_fast.h).  center: middle of the
+// uniform's interval; e: bound on |y - y_exact| plus the interval's half
+// width.  Returns false when the decision is not certain.
+__device__ __forceinline__ bool certified_code(float y, float center, float e, int kmax, int &q) {
+  const float z = y - center;
+  const float fl = floorf(z);
+  const float fr = z - fl;
+  q = min(max((int)fl + 1, 0), kmax);
+  return fabsf(fr - 0.5f) + e < 0.5f;
+}
+
+template <int GD, bool INJ, bool SMALL>
+__device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOBAL Grid *old,
+                                const LUMA_GLOBAL Grid *nw, int64_t beg, int64_t end,
+                                uint32_t k0, uint32_t k1, uint2 *queue) {
+  const Bounds B = make_bounds((const Grid *)old, (const Grid *)nw, h.beta1, h.beta2);
+  const DecodeK D = decode_consts(old, h.eps);
+  const float idm = nw->fast[kIdm], ytop_m = nw->fast[kYTopM];
+  const float nl2dw = nw->fast[kNl2dw], ytop_w = nw->fast[kYTopW];
+  const float wmin_n = nw->wmin;
+  const float isbc2 = (float)(1.0 / ::sqrt((double)h.bc2));
+  const float hb = INJ ? 0.0f : 1.0f / 512.0f;
+  const float k3 = B.k3 + hb, k8 = B.k8 + hb;
+  const bool vec_ok = tensor_vec_ok(T);
+  const uint32_t lane = lane_id();
+  uint32_t qlen = 0;
+  // Exact codes of a queued element; its fast codes were already stored and
+  // are overwritten (same wavefront, so the stores stay in program order).
+  auto run = [&](uint2 ent) {
+    const int64_t i = beg + (ent.x & 0xFFFFu);
+    const int qmo = (int)(int16_t)(ent.x >> 16);
+    const int qwo = (int)(ent.y & 0xFFFFu);
+    const float g = load_grad(T.grad, i, GD);
+    float um, uw;
+    if (INJ) {
+      um = T.u_m[i];
+      uw = T.u_w[i];
+    } else {
+      const U4 fine = philox_fine_block((uint64_t)i, k0, k1);
+      const int r = (int)(i & 3);
+      um = (float)((((ent.y >> 16) & 0xFFu) << 16) | u4_half(fine, 2 * r)) * 0x1p-24f;
+      uw = (float)(((ent.y >> 24) << 16) | u4_half(fine, 2 * r + 1)) * 0x1p-24f;
+    }
+    const uint32_t codes = exact_codes(qmo, qwo, g, old, nw, h, um, uw);
+    T.q_m[i] = (int16_t)(codes & 0xFFFFu);
+    T.q_w[i] = (int16_t)(codes >> 16);
+  };
+  // Every lane runs the same number of iterations (lanes past the end carry
+  // n = 0), so the ballots and the queue length stay uniform across the wave.
+  const int n_it = (int)((end - beg + kThreads * kVec - 1) / (kThreads * kVec));
+  for (int it = 0; it < n_it; ++it) {
+    const int64_t e0 = beg + ((int64_t)it * kThreads + threadIdx.x) * kVec;
+    const int64_t rem = end - e0;
+    const int n = rem <= 0 ? 0 : (rem < kVec ? (int)rem : kVec);
+    const bool vec = vec_ok && n == kVec;
+    Group8 Q;
+    load_group<GD>(T, e0, n, vec, Q);
+    float p[kVec], um[kVec], uw[kVec];
+    if (vec) {
+      const vf4 p0 = *(const LUMA_GLOBAL vf4 *)(T.param + e0);
+      const vf4 p1 = *(const LUMA_GLOBAL vf4 *)(T.param + e0 + 4);
+      p[0] = p0.x; p[1] = p0.y; p[2] = p0.z; p[3] = p0.w;
+      p[4] = p1.x; p[5] = p1.y; p[6] = p1.z; p[7] = p1.w;
+    } else {
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) p[j] = j < n ? T.param[e0 + j] : 0.0f;
+    }
+    U4 coarse{};
+    if (INJ) {
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) {
+        um[j] = j < n ? T.u_m[e0 + j] : 0.5f;
+        uw[j] = j < n ? T.u_w[e0 + j] : 0.5f;
+      }
+    } else {
+      coarse = philox_coarse_block((uint64_t)e0, k0, k1);
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) {
+        um[j] = fmaf((float)u4_byte(coarse, 2 * j), 1.0f / 256.0f, 1.0f / 512.0f);
+        uw[j] = fmaf((float)u4_byte(coarse, 2 * j + 1), 1.0f / 256.0f, 1.0f / 512.0f);
+      }
+    }
+    int om[kVec], ow[kVec];
+    uint32_t flags = 0;
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) {
+      const FastEma f = fast_ema<SMALL>(Q.qm[j], Q.qw[j], Q.g[j], D.dm, D.dw, D.iwmin, D.eps,
+                                        h.beta1, h.omb1, h.beta2, h.omb2);
+      const float s = __builtin_amdgcn_sqrtf(f.vn);
+      // AdamW update (functional.py:278-279), within 1e-6 of the exact path
+      const float den = fmaf(s, isbc2, h.eps);
+      p[j] = fmaf(p[j], h.decay, (h.neg_eta * f.mn) * __builtin_amdgcn_rcpf(den));
+      // momentum code
+      const float a = fabsf(f.mn);
+      const float L = SMALL ? fast_log1p_small(a) : fast_log1p_general(a);
+      const float ym = fminf(L * idm, ytop_m);
+      const float em = fmaf(f.am, B.k1, fmaf(ym, B.k2, k3));
+      int qm;
+      const bool okm = certified_code(ym, um[j], em, 32767, qm);
+      om[j] = f.mn < 0.0f ? -qm : qm;
+      // preconditioner code (delta_w = 0 gives nl2dw = ytop_w = 0, i.e. y = 0)
+      const float t = s + h.eps;
+      const float yw = fminf(__builtin_amdgcn_logf(wmin_n * t) * nl2dw, ytop_w);
+      const float ew = fmaf(yw, B.k7, k8);
+      int qw;
+      const bool okw = certified_code(yw, uw[j], ew, 65535, qw);
+      ow[j] = qw;
+      flags |= (!(okm && okw) && j < n) ? (1u << j) : 0u;
+    }
+    if (vec) {
+      vf4 p0, p1;
+      p0.x = p[0]; p0.y = p[1]; p0.z = p[2]; p0.w = p[3];
+      p1.x = p[4]; p1.y = p[5]; p1.z = p[6]; p1.w = p[7];
+      *(LUMA_GLOBAL vf4 *)(T.param + e0) = p0;
+      *(LUMA_GLOBAL vf4 *)(T.param + e0 + 4) = p1;
+      vu4 a, b;
+      a.x = (uint32_t)(om[0] & 0xFFFF) | ((uint32_t)om[1] << 16);
+      a.y = (uint32_t)(om[2] & 0xFFFF) | ((uint32_t)om[3] << 16);
+      a.z = (uint32_t)(om[4] & 0xFFFF) | ((uint32_t)om[5] << 16);
+      a.w = (uint32_t)(om[6] & 0xFFFF) | ((uint32_t)om[7] << 16);
+      b.x = (uint32_t)(ow[0] & 0xFFFF) | ((uint32_t)ow[1] << 16);
+      b.y = (uint32_t)(ow[2] & 0xFFFF) | ((uint32_t)ow[3] << 16);
+      b.z = (uint32_t)(ow[4] & 0xFFFF) | ((uint32_t)ow[5] << 16);
+      b.w = (uint32_t)(ow[6] & 0xFFFF) | ((uint32_t)ow[7] << 16);
+      *(LUMA_GLOBAL vu4 *)(T.q_m + e0) = a;
+      *(LUMA_GLOBAL vu4 *)(T.q_w + e0) = b;
+    } else {
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) {
+        if (j < n) {
+          T.param[e0 + j] = p[j];
+          T.q_m[e0 + j] = (int16_t)om[j];
+          T.q_w[e0 + j] = (int16_t)(uint16_t)ow[j];
+        }
+      }
+    }
+    if (__ballot(flags != 0)) {
+      const uint32_t off0 = (uint32_t)(e0 - beg);
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) {
+        const bool f = (flags >> j) & 1u;
+        const uint64_t bm = __ballot(f);
+        if (f) {
+          const uint32_t half = INJ ? 0u : (u4_word(coarse, j >> 1) >> (16 * (j & 1))) & 0xFFFFu;
+          queue[queue_pos(bm, qlen)] =
+              make_uint2((off0 + j) | ((uint32_t)Q.qm[j] << 16), (uint32_t)Q.qw[j] | (half << 16));
+        }
+        qlen += (uint32_t)__popcll(bm);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      while (qlen >= 64) {
+        qlen -= 64;
+        run(queue[qlen + lane]);
+      }
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  if (lane < qlen) run(queue[lane]);
+}
+
+template <int GD>
+__device__ __forceinline__ void pass2_dispatch(const Tensor &T, const Hyper &h,
+                                               const LUMA_GLOBAL Grid *old,
+                                               const LUMA_GLOBAL Grid *nw, int64_t beg,
+                                               int64_t end, uint32_t k0, uint32_t k1, bool inj,
+                                               bool small, uint2 *q) {
+  if (inj) {
+    if (small) pass2_fast_body<GD, true, true>(T, h, old, nw, beg, end, k0, k1, q);
+    else pass2_fast_body<GD, true, false>(T, h, old, nw, beg, end, k0, k1, q);
+  } else {
+    if (small) pass2_fast_body<GD, false, true>(T, h, old, nw, beg, end, k0, k1, q);
+    else pass2_fast_body<GD, false, false>(T, h, old, nw, beg, end, k0, k1, q);
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void pass2_fast_kernel(const Tensor *__restrict__ tensors,
+                                                              const LumaChunk *__restrict__ chunks,
+                                                              const Hyper *__restrict__ hypers,
+                                                              const Slot *__restrict__ slots,
+                                                              uint64_t base_seed, int noise_mode) {
+  const LumaChunk c = chunks[blockIdx.x];
+  const Tensor T = tensors[c.tensor];
+  const Hyper h = hypers[T.hyper];
+  const LUMA_GLOBAL Slot *S = (const LUMA_GLOBAL Slot *)&slots[T.slot];
+  const LUMA_GLOBAL Grid *old = T.step >= 2 ? &S->grid[(T.step - 1) & 1] : nullptr;
+  const LUMA_GLOBAL Grid *nw = &S->grid[T.step & 1];
+  const int64_t beg = (int64_t)c.index * kChunk;
+  const int64_t end = beg + kChunk < T.numel ? beg + kChunk : T.numel;
+  uint32_t k0, k1;
+  step_key(base_seed, T.step, T.param_id, k0, k1);
+  const bool inj = noise_mode == LUMA_NOISE_INJECTED;
+  const bool small = (old == nullptr || old->fast[kXTopM] <= kSmall) && nw->sm <= kSmall;
+  __shared__ uint2 qbuf[kThreads / 64][kQueueCap];
+  uint2 *q = qbuf[threadIdx.x >> 6];
+  if (T.grad_dtype == LUMA_GRAD_BF16)
+    pass2_dispatch<LUMA_GRAD_BF16>(T, h, old, nw, beg, end, k0, k1, inj, small, q);
+  else if (T.grad_dtype == LUMA_GRAD_F16)
+    pass2_dispatch<LUMA_GRAD_F16>(T, h, old, nw, beg, end, k0, k1, inj, small, q);
+  else
+    pass2_dispatch<LUMA_GRAD_F32>(T, h, old, nw, beg, end, k0, k1, inj, small, q);
+}
+
+// ---------------------------------------------------------------------------
 //  Scale slots, decode (export) and quantise (import)
 // ---------------------------------------------------------------------------
 
@@ -215,6 +671,7 @@ __global__ void set_scales_kernel(Slot *__restrict__ slots, const LumaScaleInit 
   s.s_m[par] = it.s_m;
   s.s_v[par] = it.s_v;
   make_grid(it.s_m, it.s_v, it.eps, s.grid[par]);
+  make_fast(s.grid[par]);
 }
 
 __global__ void get_scales_kernel(const Slot *__restrict__ slots, const int32_t *__restrict__ idx,
@@ -277,6 +734,7 @@ __global__ __launch_bounds__(64) void quant_finalize_kernel(const float *__restr
     s.s_m[par] = py_max((double)am, 1e-9);
     s.s_v[par] = py_max((double)av, 0.0);
     make_grid(s.s_m[par], s.s_v[par], eps, s.grid[par]);
+    make_fast(s.grid[par]);
   }
 }
 
@@ -378,15 +836,24 @@ static int step_impl(const LumaStepArgs *a, void *stream, void *const *events) {
     return e == hipSuccess ? 0 : fail("luma_step: event record", e);
   };
   if (int r = mark(0)) return r;
-  hipLaunchKernelGGL(pass1_kernel, dim3(a->n_chunks), dim3(kThreads), 0, s, T, a->chunks, H, S,
-                     a->partials);
+  const bool exact = (a->flags & LUMA_FLAG_EXACT_ONLY) != 0;
+  if (exact)
+    hipLaunchKernelGGL(pass1_exact_kernel, dim3(a->n_chunks), dim3(kThreads), 0, s, T, a->chunks,
+                       H, S, a->partials);
+  else
+    hipLaunchKernelGGL(pass1_fast_kernel, dim3(a->n_chunks), dim3(kThreads), 0, s, T, a->chunks,
+                       H, S, a->partials);
   if (int r = check_launch("luma_step: pass 1 launch")) return r;
   if (int r = mark(1)) return r;
   hipLaunchKernelGGL(finalize_kernel, dim3(a->n_tensors), dim3(64), 0, s, T, H, S, a->partials);
   if (int r = check_launch("luma_step: finalize launch")) return r;
   if (int r = mark(2)) return r;
-  hipLaunchKernelGGL(pass2_kernel, dim3(a->n_chunks), dim3(kThreads), 0, s, T, a->chunks, H, S,
-                     a->base_seed, a->noise_mode);
+  if (exact)
+    hipLaunchKernelGGL(pass2_exact_kernel, dim3(a->n_chunks), dim3(kThreads), 0, s, T, a->chunks,
+                       H, S, a->base_seed, a->noise_mode);
+  else
+    hipLaunchKernelGGL(pass2_fast_kernel, dim3(a->n_chunks), dim3(kThreads), 0, s, T, a->chunks,
+                       H, S, a->base_seed, a->noise_mode);
   if (int r = check_launch("luma_step: pass 2 launch")) return r;
   return mark(3);
 }
