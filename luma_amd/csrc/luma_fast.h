@@ -125,7 +125,10 @@ struct FastEma {
   float xw;   // preconditioner decode argument
 };
 
-template <bool SMALL_M>
+// PRECISE_V: form e^-x with the two-word argument reduction (pass 2, whose
+// parameter update and code bounds use v'); pass 1 only needs the cheaper
+// single exp2, whose error its max-tracking bound covers (x * u term).
+template <bool SMALL_M, bool PRECISE_V>
 __device__ __forceinline__ FastEma fast_ema(int qm, int qw, float g, float dm, float dw,
                                             float iwmin, float eps, float b1, float omb1,
                                             float b2, float omb2) {
@@ -140,10 +143,12 @@ __device__ __forceinline__ FastEma fast_ema(int qm, int qw, float g, float dm, f
   // d = -x - a*ln2 is formed with a two-word ln2, so the rounding of the
   // exponent argument does not scale with x.
   const float a = r.xw * -kLog2e;
-  float d = fmaf(a, -kLn2Hi, -r.xw);
-  d = fmaf(a, -kLn2Lo, d);
-  const float e2 = __builtin_amdgcn_exp2f(a);
-  const float ex = fmaf(e2, d, e2);
+  float ex = __builtin_amdgcn_exp2f(a);
+  if (PRECISE_V) {
+    float d = fmaf(a, -kLn2Hi, -r.xw);
+    d = fmaf(a, -kLn2Lo, d);
+    ex = fmaf(ex, d, ex);
+  }
   const float rr = fmaf(iwmin, ex, -eps);  // 1/w - eps
   const float v = rr * rr;
   const float c1g = omb1 * g;
@@ -189,7 +194,7 @@ __device__ inline Bounds make_bounds(const Grid *old, const Grid *nw, float b1, 
   float rho_e1 = 0.0f, rho_p = 0.0f, s_old = 0.0f, w2 = 0.0f;
   if (old) {
     rho_e1 = fast_expm1_relerr(old->fast[kXTopM]) + 0.5f * kU;
-    rho_p = rho_x + 6.0f * kU;
+    rho_p = rho_x + 6.0f * kU + (nw ? 0.0f : old->fast[kXTopW] * kU);
     s_old = old->sm * 1.01f;
     w2 = old->fast[kW2];
   }

@@ -347,10 +347,45 @@ __device__ __forceinline__ DecodeK decode_consts(const LUMA_GLOBAL Grid *old, fl
   return k;
 }
 
-// Pass 1 body: exact max |m'| and max v' of the chunk.  Fast values are
-// tracked per lane; an element needs the exact path only when its certified
-// upper bound reaches the lane's certified lower bound of the maximum.  Such
-// candidates go through the wave's queue.
+// Candidate threshold for a running fast maximum M (float bits): elements
+// whose fast value is below it are provably not the exact maximum.  A NaN
+// maximum gives threshold 0 (every element becomes a candidate).
+__device__ __forceinline__ uint32_t threshold_bits(uint32_t M, float lo, float sub, float hi) {
+  const float t = (__uint_as_float(M) * lo - sub) * hi;
+  return t > 0.0f ? __float_as_uint(t) : 0u;
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, off, 64));
+  return v;
+}
+
+// Fast |m'| and v' of 8 consecutive elements as float bit patterns (for
+// non-negative floats the unsigned order is the float order, with every NaN
+// above +Inf); invalid elements of a partial group give 0.
+template <int GD, bool SMALL, bool FULL>
+__device__ __forceinline__ void p1_iter(const Tensor &T, const DecodeK &D, const Hyper &h,
+                                        int64_t e0, int n, uint32_t (&am)[kVec],
+                                        uint32_t (&av)[kVec]) {
+  Group8 G;
+  load_group<GD>(T, e0, n, FULL, G);
+#pragma unroll
+  for (int j = 0; j < kVec; ++j) {
+    const FastEma f = fast_ema<SMALL, false>(G.qm[j], G.qw[j], G.g[j], D.dm, D.dw, D.iwmin,
+                                             D.eps, h.beta1, h.omb1, h.beta2, h.omb2);
+    am[j] = __float_as_uint(f.mn) & 0x7FFFFFFFu;
+    av[j] = __float_as_uint(f.vn) & 0x7FFFFFFFu;
+    if (!FULL && j >= n) am[j] = av[j] = 0u;
+  }
+}
+
+// Pass 1 body: exact max |m'| and max v' of the chunk.  The wave keeps a
+// running maximum of the fast values and from it a certified lower bound of
+// the exact maximum (the threshold, uniform across the wave).  An element
+// whose fast value is below the threshold cannot be the exact maximum; the
+// others (in practice a few per chunk) go through the wave's queue to the
+// exact path.
 template <int GD, bool SMALL>
 __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOBAL Grid *old,
                                 int64_t beg, int64_t end, float &exm, float &exv,
@@ -362,7 +397,9 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   const float lo_v = 1.0f - B.dlt_v, hi_v = 1.0f / (1.0f + B.dlt_v);
   const float sub_m = 2.0f * B.abs_m, sub_v = 2.0f * B.abs_v;
   const uint32_t lane = lane_id();
-  float Mm = -INFINITY, Mv = -INFINITY, Tm = -INFINITY, Tv = -INFINITY;
+  uint32_t Mm = 0, Mv = 0, Tm = 0, Tv = 0;  // wave maxima / thresholds (bits)
+  const bool exact_fast = old == nullptr;
+  uint32_t xbm = 0, xbv = 0;                 // exact maxima when exact_fast (bits)
   uint32_t qlen = 0;
   auto run = [&](uint32_t off) {
     const int64_t i = beg + off;
@@ -377,49 +414,48 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     const int64_t e0 = beg + ((int64_t)it * kThreads + threadIdx.x) * kVec;
     const int64_t rem = end - e0;
     const int n = rem <= 0 ? 0 : (rem < kVec ? (int)rem : kVec);
-    Group8 G;
-    load_group<GD>(T, e0, n, vec_ok && n == kVec, G);
-    float am[kVec], av[kVec];
-    float im = -INFINITY, iv = -INFINITY;
+    uint32_t am[kVec], av[kVec];
+    if (vec_ok && n == kVec)
+      p1_iter<GD, SMALL, true>(T, D, h, e0, n, am, av);
+    else
+      p1_iter<GD, SMALL, false>(T, D, h, e0, n, am, av);
+    const uint32_t im = max(max(max(am[0], am[1]), max(am[2], am[3])),
+                            max(max(am[4], am[5]), max(am[6], am[7])));
+    const uint32_t iv = max(max(max(av[0], av[1]), max(av[2], av[3])),
+                            max(max(av[4], av[5]), max(av[6], av[7])));
+    if (exact_fast) {
+      // t = 1: no decode, the fast m', v' are the exact ones
+      xbm = max(xbm, im);
+      xbv = max(xbv, iv);
+      continue;
+    }
+    if (!__ballot(im >= Tm || iv >= Tv)) continue;
+    // some lane reached the threshold: raise the wave maximum, then queue
+    // the elements that still reach the new threshold
+    Mm = max(Mm, wave_max_u32(im));
+    Mv = max(Mv, wave_max_u32(iv));
+    Tm = threshold_bits(Mm, lo_m, sub_m, hi_m);
+    Tv = threshold_bits(Mv, lo_v, sub_v, hi_v);
+    const uint32_t off0 = (uint32_t)(e0 - beg);
 #pragma unroll
     for (int j = 0; j < kVec; ++j) {
-      const FastEma f = fast_ema<SMALL>(G.qm[j], G.qw[j], G.g[j], D.dm, D.dw, D.iwmin, D.eps,
-                                        h.beta1, h.omb1, h.beta2, h.omb2);
-      am[j] = j < n ? fabsf(f.mn) : -INFINITY;
-      av[j] = j < n ? f.vn : -INFINITY;
-      im = nan_max(im, am[j]);
-      iv = nan_max(iv, av[j]);
+      const bool f = (am[j] >= Tm || av[j] >= Tv) && j < n;
+      const uint64_t bm = __ballot(f);
+      if (f) queue[queue_pos(bm, qlen)] = off0 + j;
+      qlen += (uint32_t)__popcll(bm);
     }
-    uint32_t cand = 0;
-    if (im >= Tm || iv >= Tv || im != im || iv != iv) {
-      Mm = nan_max(Mm, im);
-      Mv = nan_max(Mv, iv);
-      Tm = (Mm * lo_m - sub_m) * hi_m;
-      Tv = (Mv * lo_v - sub_v) * hi_v;
-#pragma unroll
-      for (int j = 0; j < kVec; ++j) {
-        const bool c = am[j] >= Tm || av[j] >= Tv || am[j] != am[j] || av[j] != av[j];
-        cand |= (c && j < n) ? (1u << j) : 0u;
-      }
-    }
-    if (__ballot(cand != 0)) {
-      const uint32_t off0 = (uint32_t)(e0 - beg);
-#pragma unroll
-      for (int j = 0; j < kVec; ++j) {
-        const bool f = (cand >> j) & 1u;
-        const uint64_t bm = __ballot(f);
-        if (f) queue[queue_pos(bm, qlen)] = off0 + j;
-        qlen += (uint32_t)__popcll(bm);
-      }
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      while (qlen >= 64) {
-        qlen -= 64;
-        run(queue[qlen + lane]);
-      }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    while (qlen >= 64) {
+      qlen -= 64;
+      run(queue[qlen + lane]);
     }
   }
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   if (lane < qlen) run(queue[lane]);
+  if (exact_fast) {
+    exm = nan_max(exm, __uint_as_float(xbm));
+    exv = nan_max(exv, __uint_as_float(xbv));
+  }
 }
 
 __global__ __launch_bounds__(kThreads) void pass1_fast_kernel(const Tensor *__restrict__ tensors,
@@ -455,15 +491,119 @@ __global__ __launch_bounds__(kThreads) void pass1_fast_kernel(const Tensor *__re
   }
 }
 
-// Certified LogSR decision (see luma_fast.h).  center: middle of the
-// uniform's interval; e: bound on |y - y_exact| plus the interval's half
-// width.  Returns false when the decision is not certain.
-__device__ __forceinline__ bool certified_code(float y, float center, float e, int kmax, int &q) {
-  const float z = y - center;
+// Certified LogSR decision (see luma_fast.h).  z = y + 1 - c, where c is
+// the middle of the uniform's interval; e bounds |y - y_exact| plus the
+// interval's half width.  The code is floor(z) clamped to [0, kmax]; it is
+// certain when [z - e, z + e] holds no integer.
+__device__ __forceinline__ bool certified_code(float z, float e, int kmax, int &q) {
   const float fl = floorf(z);
   const float fr = z - fl;
-  q = min(max((int)fl + 1, 0), kmax);
+  q = (int)__builtin_amdgcn_fmed3f(fl, 0.0f, (float)kmax);
   return fabsf(fr - 0.5f) + e < 0.5f;
+}
+
+// Per-tensor constants of pass 2.
+struct P2Const {
+  DecodeK D;
+  float b1, omb1, b2, omb2, decay, neg_eta, eps;
+  float isbc2;            // 1 / sqrt(bc2)
+  float idm, ytop_m;      // momentum: 1/dm, largest y (+ zoff)
+  float nl2dw, ytop_w;    // preconditioner: -ln2/dw, largest y (+ zoff)
+  float wmin_n;
+  float zoff;             // 1 - center of a Philox bucket offset (or 1 when injected)
+  float k1, k2, k3, k7, k8;
+};
+
+// One iteration of 8 consecutive elements.  FULL: all 8 valid and 16-byte
+// aligned (vector loads/stores, no masking).  Returns the flags of elements
+// whose codes need the exact path; Q and coarse are kept for the queue.
+template <int GD, bool INJ, bool SMALL, bool FULL>
+__device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, int64_t e0, int n,
+                                            uint32_t k0, uint32_t k1, Group8 &Q, U4 &coarse) {
+  load_group<GD>(T, e0, n, FULL, Q);
+  float p[kVec], zm0[kVec], zw0[kVec];
+  if (FULL) {
+    const vf4 p0 = *(const LUMA_GLOBAL vf4 *)(T.param + e0);
+    const vf4 p1 = *(const LUMA_GLOBAL vf4 *)(T.param + e0 + 4);
+    p[0] = p0.x; p[1] = p0.y; p[2] = p0.z; p[3] = p0.w;
+    p[4] = p1.x; p[5] = p1.y; p[6] = p1.z; p[7] = p1.w;
+  } else {
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) p[j] = j < n ? T.param[e0 + j] : 0.0f;
+  }
+  // uniform interval centers, already subtracted from the 1 + y offset
+  if (INJ) {
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) {
+      zm0[j] = (FULL || j < n) ? T.u_m[e0 + j] : 0.5f;
+      zw0[j] = (FULL || j < n) ? T.u_w[e0 + j] : 0.5f;
+    }
+  } else {
+    coarse = philox_coarse_block((uint64_t)e0, k0, k1);
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) {
+      zm0[j] = (float)u4_byte(coarse, 2 * j) * (1.0f / 256.0f);
+      zw0[j] = (float)u4_byte(coarse, 2 * j + 1) * (1.0f / 256.0f);
+    }
+  }
+  int om[kVec], ow[kVec];
+  uint32_t flags = 0;
+#pragma unroll
+  for (int j = 0; j < kVec; ++j) {
+    const FastEma f = fast_ema<SMALL, true>(Q.qm[j], Q.qw[j], Q.g[j], C.D.dm, C.D.dw, C.D.iwmin,
+                                            C.D.eps, C.b1, C.omb1, C.b2, C.omb2);
+    const float s = __builtin_amdgcn_sqrtf(f.vn);
+    // AdamW update (functional.py:278-279), within 1e-6 of the exact path
+    const float den = fmaf(s, C.isbc2, C.eps);
+    p[j] = fmaf(p[j], C.decay, (C.neg_eta * f.mn) * __builtin_amdgcn_rcpf(den));
+    // momentum code
+    const float a = fabsf(f.mn);
+    const float L = SMALL ? fast_log1p_small(a) : fast_log1p_general(a);
+    const float ym = fminf(fmaf(L, C.idm, C.zoff), C.ytop_m);
+    const float em = fmaf(f.am, C.k1, fmaf(ym, C.k2, C.k3));
+    int qm;
+    const bool okm = certified_code(ym - zm0[j], em, 32767, qm);
+    om[j] = f.mn < 0.0f ? -qm : qm;
+    // preconditioner code (delta_w = 0 gives nl2dw = 0: y = 0)
+    const float t = s + C.eps;
+    const float yw = fminf(fmaf(__builtin_amdgcn_logf(C.wmin_n * t), C.nl2dw, C.zoff), C.ytop_w);
+    const float ew = fmaf(yw, C.k7, C.k8);
+    int qw;
+    const bool okw = certified_code(yw - zw0[j], ew, 65535, qw);
+    ow[j] = qw;
+    if (FULL)
+      flags |= (okm && okw) ? 0u : (1u << j);
+    else
+      flags |= (!(okm && okw) && j < n) ? (1u << j) : 0u;
+  }
+  if (FULL) {
+    vf4 p0, p1;
+    p0.x = p[0]; p0.y = p[1]; p0.z = p[2]; p0.w = p[3];
+    p1.x = p[4]; p1.y = p[5]; p1.z = p[6]; p1.w = p[7];
+    *(LUMA_GLOBAL vf4 *)(T.param + e0) = p0;
+    *(LUMA_GLOBAL vf4 *)(T.param + e0 + 4) = p1;
+    vu4 a, b;
+    a.x = (uint32_t)(om[0] & 0xFFFF) | ((uint32_t)om[1] << 16);
+    a.y = (uint32_t)(om[2] & 0xFFFF) | ((uint32_t)om[3] << 16);
+    a.z = (uint32_t)(om[4] & 0xFFFF) | ((uint32_t)om[5] << 16);
+    a.w = (uint32_t)(om[6] & 0xFFFF) | ((uint32_t)om[7] << 16);
+    b.x = (uint32_t)ow[0] | ((uint32_t)ow[1] << 16);
+    b.y = (uint32_t)ow[2] | ((uint32_t)ow[3] << 16);
+    b.z = (uint32_t)ow[4] | ((uint32_t)ow[5] << 16);
+    b.w = (uint32_t)ow[6] | ((uint32_t)ow[7] << 16);
+    *(LUMA_GLOBAL vu4 *)(T.q_m + e0) = a;
+    *(LUMA_GLOBAL vu4 *)(T.q_w + e0) = b;
+  } else {
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) {
+      if (j < n) {
+        T.param[e0 + j] = p[j];
+        T.q_m[e0 + j] = (int16_t)om[j];
+        T.q_w[e0 + j] = (int16_t)(uint16_t)ow[j];
+      }
+    }
+  }
+  return flags;
 }
 
 template <int GD, bool INJ, bool SMALL>
@@ -471,13 +611,26 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
                                 const LUMA_GLOBAL Grid *nw, int64_t beg, int64_t end,
                                 uint32_t k0, uint32_t k1, uint2 *queue) {
   const Bounds B = make_bounds((const Grid *)old, (const Grid *)nw, h.beta1, h.beta2);
-  const DecodeK D = decode_consts(old, h.eps);
-  const float idm = nw->fast[kIdm], ytop_m = nw->fast[kYTopM];
-  const float nl2dw = nw->fast[kNl2dw], ytop_w = nw->fast[kYTopW];
-  const float wmin_n = nw->wmin;
-  const float isbc2 = (float)(1.0 / ::sqrt((double)h.bc2));
+  P2Const C;
+  C.D = decode_consts(old, h.eps);
+  C.b1 = h.beta1; C.omb1 = h.omb1; C.b2 = h.beta2; C.omb2 = h.omb2;
+  C.decay = h.decay; C.neg_eta = h.neg_eta; C.eps = h.eps;
+  C.isbc2 = (float)(1.0 / ::sqrt((double)h.bc2));
+  // y is formed as y + zoff, zoff = 1 - (half width of the uniform's interval),
+  // so that z = y + zoff - u_low has floor(z) = the LogSR code.
   const float hb = INJ ? 0.0f : 1.0f / 512.0f;
-  const float k3 = B.k3 + hb, k8 = B.k8 + hb;
+  C.zoff = 1.0f - hb;
+  C.idm = nw->fast[kIdm];
+  C.ytop_m = nw->fast[kYTopM] + C.zoff;
+  C.nl2dw = nw->fast[kNl2dw];
+  C.ytop_w = nw->fast[kYTopW] + C.zoff;
+  C.wmin_n = nw->wmin;
+  // the bounds were derived for y; y + zoff adds at most one rounding (u * y)
+  C.k1 = B.k1;
+  C.k2 = B.k2 + kSafety * kU;
+  C.k3 = B.k3 + hb - C.zoff * C.k2;
+  C.k7 = B.k7 + kSafety * kU;
+  C.k8 = B.k8 + hb - C.zoff * C.k7;
   const bool vec_ok = tensor_vec_ok(T);
   const uint32_t lane = lane_id();
   uint32_t qlen = 0;
@@ -509,88 +662,13 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     const int64_t e0 = beg + ((int64_t)it * kThreads + threadIdx.x) * kVec;
     const int64_t rem = end - e0;
     const int n = rem <= 0 ? 0 : (rem < kVec ? (int)rem : kVec);
-    const bool vec = vec_ok && n == kVec;
     Group8 Q;
-    load_group<GD>(T, e0, n, vec, Q);
-    float p[kVec], um[kVec], uw[kVec];
-    if (vec) {
-      const vf4 p0 = *(const LUMA_GLOBAL vf4 *)(T.param + e0);
-      const vf4 p1 = *(const LUMA_GLOBAL vf4 *)(T.param + e0 + 4);
-      p[0] = p0.x; p[1] = p0.y; p[2] = p0.z; p[3] = p0.w;
-      p[4] = p1.x; p[5] = p1.y; p[6] = p1.z; p[7] = p1.w;
-    } else {
-#pragma unroll
-      for (int j = 0; j < kVec; ++j) p[j] = j < n ? T.param[e0 + j] : 0.0f;
-    }
     U4 coarse{};
-    if (INJ) {
-#pragma unroll
-      for (int j = 0; j < kVec; ++j) {
-        um[j] = j < n ? T.u_m[e0 + j] : 0.5f;
-        uw[j] = j < n ? T.u_w[e0 + j] : 0.5f;
-      }
-    } else {
-      coarse = philox_coarse_block((uint64_t)e0, k0, k1);
-#pragma unroll
-      for (int j = 0; j < kVec; ++j) {
-        um[j] = fmaf((float)u4_byte(coarse, 2 * j), 1.0f / 256.0f, 1.0f / 512.0f);
-        uw[j] = fmaf((float)u4_byte(coarse, 2 * j + 1), 1.0f / 256.0f, 1.0f / 512.0f);
-      }
-    }
-    int om[kVec], ow[kVec];
-    uint32_t flags = 0;
-#pragma unroll
-    for (int j = 0; j < kVec; ++j) {
-      const FastEma f = fast_ema<SMALL>(Q.qm[j], Q.qw[j], Q.g[j], D.dm, D.dw, D.iwmin, D.eps,
-                                        h.beta1, h.omb1, h.beta2, h.omb2);
-      const float s = __builtin_amdgcn_sqrtf(f.vn);
-      // AdamW update (functional.py:278-279), within 1e-6 of the exact path
-      const float den = fmaf(s, isbc2, h.eps);
-      p[j] = fmaf(p[j], h.decay, (h.neg_eta * f.mn) * __builtin_amdgcn_rcpf(den));
-      // momentum code
-      const float a = fabsf(f.mn);
-      const float L = SMALL ? fast_log1p_small(a) : fast_log1p_general(a);
-      const float ym = fminf(L * idm, ytop_m);
-      const float em = fmaf(f.am, B.k1, fmaf(ym, B.k2, k3));
-      int qm;
-      const bool okm = certified_code(ym, um[j], em, 32767, qm);
-      om[j] = f.mn < 0.0f ? -qm : qm;
-      // preconditioner code (delta_w = 0 gives nl2dw = ytop_w = 0, i.e. y = 0)
-      const float t = s + h.eps;
-      const float yw = fminf(__builtin_amdgcn_logf(wmin_n * t) * nl2dw, ytop_w);
-      const float ew = fmaf(yw, B.k7, k8);
-      int qw;
-      const bool okw = certified_code(yw, uw[j], ew, 65535, qw);
-      ow[j] = qw;
-      flags |= (!(okm && okw) && j < n) ? (1u << j) : 0u;
-    }
-    if (vec) {
-      vf4 p0, p1;
-      p0.x = p[0]; p0.y = p[1]; p0.z = p[2]; p0.w = p[3];
-      p1.x = p[4]; p1.y = p[5]; p1.z = p[6]; p1.w = p[7];
-      *(LUMA_GLOBAL vf4 *)(T.param + e0) = p0;
-      *(LUMA_GLOBAL vf4 *)(T.param + e0 + 4) = p1;
-      vu4 a, b;
-      a.x = (uint32_t)(om[0] & 0xFFFF) | ((uint32_t)om[1] << 16);
-      a.y = (uint32_t)(om[2] & 0xFFFF) | ((uint32_t)om[3] << 16);
-      a.z = (uint32_t)(om[4] & 0xFFFF) | ((uint32_t)om[5] << 16);
-      a.w = (uint32_t)(om[6] & 0xFFFF) | ((uint32_t)om[7] << 16);
-      b.x = (uint32_t)(ow[0] & 0xFFFF) | ((uint32_t)ow[1] << 16);
-      b.y = (uint32_t)(ow[2] & 0xFFFF) | ((uint32_t)ow[3] << 16);
-      b.z = (uint32_t)(ow[4] & 0xFFFF) | ((uint32_t)ow[5] << 16);
-      b.w = (uint32_t)(ow[6] & 0xFFFF) | ((uint32_t)ow[7] << 16);
-      *(LUMA_GLOBAL vu4 *)(T.q_m + e0) = a;
-      *(LUMA_GLOBAL vu4 *)(T.q_w + e0) = b;
-    } else {
-#pragma unroll
-      for (int j = 0; j < kVec; ++j) {
-        if (j < n) {
-          T.param[e0 + j] = p[j];
-          T.q_m[e0 + j] = (int16_t)om[j];
-          T.q_w[e0 + j] = (int16_t)(uint16_t)ow[j];
-        }
-      }
-    }
+    uint32_t flags;
+    if (vec_ok && n == kVec)
+      flags = p2_iter<GD, INJ, SMALL, true>(T, C, e0, n, k0, k1, Q, coarse);
+    else
+      flags = p2_iter<GD, INJ, SMALL, false>(T, C, e0, n, k0, k1, Q, coarse);
     if (__ballot(flags != 0)) {
       const uint32_t off0 = (uint32_t)(e0 - beg);
 #pragma unroll
