@@ -135,6 +135,91 @@ def cpu_baseline(cfg_name):
                       f"median of {len(times)} update steps after the init step; {cpu_model}"}
 
 
+# ── HBM traffic: rocprofv3 FETCH_SIZE / WRITE_SIZE, calibrated on a copy ─────
+
+TRAFFIC_DIR = os.path.join(ROOT, "profiles")
+COPY_ELEMS = 1 << 28          # float32 elements of the calibration copy (1 GiB each way)
+
+
+def copy_calibration(reps):
+    """A plain copy kernel of known size: y = x * 1 over 2^28 float32 (reads and
+    writes 1 GiB per launch); its FETCH_SIZE / WRITE_SIZE give the counters' scale."""
+    x = torch.randn(COPY_ELEMS, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(reps):
+        torch.mul(x, 1.0, out=y)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_each_way": COPY_ELEMS * 4, "launches": reps}))
+
+
+def _pmc_per_dispatch(path, kernel_prefix, counter):
+    import csv
+    vals = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            if r["Counter_Name"] == counter and r["Kernel_Name"].startswith(kernel_prefix):
+                key = int(r["Dispatch_Id"])
+                vals[key] = vals.get(key, 0.0) + float(r["Counter_Value"])
+    if not vals:
+        raise SystemExit(f"no {counter} rows for {kernel_prefix} in {path}")
+    return [vals[k] for k in sorted(vals)]          # in dispatch order
+
+
+def traffic_report(config, kernel, fetch_csv, write_csv, copy_fetch_csv, copy_write_csv, out):
+    """Write the HBM-traffic summary that the bench line's roofline.traffic reads."""
+    cfg = CONFIGS[config]
+    n_params = sum(math.prod(s) for s in cfg["shapes"]())
+    gbytes = torch.tensor([], dtype=cfg["grad"]).element_size()
+    algo = {"luma::pass1": n_params * (gbytes + 4), "luma::pass2": n_params * (gbytes + 16)}[kernel]
+    copy_bytes = COPY_ELEMS * 4
+    cf = _pmc_per_dispatch(copy_fetch_csv, "void at::native::vectorized_elementwise_kernel", "FETCH_SIZE")
+    cw = _pmc_per_dispatch(copy_write_csv, "void at::native::vectorized_elementwise_kernel", "WRITE_SIZE")
+    # the calibration copy is the largest elementwise launch of its run
+    f_scale = copy_bytes / (max(cf) * 1024.0)
+    w_scale = copy_bytes / (max(cw) * 1024.0)
+    kf = _pmc_per_dispatch(fetch_csv, kernel, "FETCH_SIZE")
+    kw = _pmc_per_dispatch(write_csv, kernel, "WRITE_SIZE")
+    # steady-state launches: drop the first (init step, no decode reads)
+    kf_ss, kw_ss = (kf[1:] or kf), (kw[1:] or kw)
+    fetch = sum(kf_ss) / len(kf_ss) * 1024.0 * f_scale
+    write = sum(kw_ss) / len(kw_ss) * 1024.0 * w_scale
+    lines = [
+        f"# HBM traffic of {kernel} on {config} ({n_params} params, {gbytes}-byte grads)",
+        "",
+        "Commands (each a separate rocprofv3 run):",
+        f"    rocprofv3 --pmc FETCH_SIZE --output-format csv -d <dir> -- python bench.py --config {config} --steps 2 --warmup 1 --no-cpu",
+        f"    rocprofv3 --pmc WRITE_SIZE --output-format csv -d <dir> -- python bench.py --config {config} --steps 2 --warmup 1 --no-cpu",
+        "    rocprofv3 --pmc FETCH_SIZE --output-format csv -d <dir> -- python bench.py --copy-calibration 3",
+        "    rocprofv3 --pmc WRITE_SIZE --output-format csv -d <dir> -- python bench.py --copy-calibration 3",
+        f"    python bench.py --traffic-report {config} {kernel} <fetch.csv> <write.csv> <copy_fetch.csv> <copy_write.csv>",
+        "",
+        f"copy kernel: {copy_bytes} B each way; FETCH_SIZE {max(cf):.0f} KiB -> scale {f_scale:.4f}; "
+        f"WRITE_SIZE {max(cw):.0f} KiB -> scale {w_scale:.4f}",
+        f"{kernel}: FETCH_SIZE per launch (KiB) {', '.join(f'{v:.0f}' for v in kf)}",
+        f"{kernel}: WRITE_SIZE per launch (KiB) {', '.join(f'{v:.0f}' for v in kw)}",
+        f"algorithmic bytes per launch: {algo}",
+        f"calibrated fetch bytes per launch: {fetch:.0f} ({fetch / (n_params * (gbytes + 8 if kernel.endswith('2') else gbytes + 4)):.3f} x algorithmic reads)",
+        f"calibrated write bytes per launch: {write:.0f}",
+        f"traffic_bytes_per_launch: {fetch + write:.0f}",
+        f"traffic_over_algorithmic: {(fetch + write) / algo:.4f}",
+    ]
+    with open(out, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
+def read_traffic(config, kernel):
+    path = os.path.join(TRAFFIC_DIR, f"{kernel.replace('::', '_')}_{config}_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1]), os.path.relpath(path, ROOT)
+    except OSError:
+        pass
+    return None, None
+
+
 # ── main ─────────────────────────────────────────────────────────────────────
 
 def main():
@@ -144,7 +229,19 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="llama3_8b", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--copy-calibration", type=int, metavar="REPS",
+                    help="only run the copy kernel used to scale the HBM counters")
+    ap.add_argument("--traffic-report", nargs=7,
+                    metavar=("CONFIG", "KERNEL", "FETCH_CSV", "WRITE_CSV", "COPY_FETCH_CSV",
+                             "COPY_WRITE_CSV", "OUT"),
+                    help="summarise rocprofv3 FETCH_SIZE/WRITE_SIZE runs into OUT")
     args = ap.parse_args()
+    if args.traffic_report:
+        traffic_report(*args.traffic_report)
+        return
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
               "the LUMA step is rank-local and shards with no exchange", file=sys.stderr)
@@ -195,6 +292,7 @@ def main():
     print(f"bench: kernel ms pass1 {avg[0]:.3f} finalize {avg[1]:.3f} pass2 {avg[2]:.3f}; "
           f"step {ms:.3f} ms", file=sys.stderr, flush=True)
 
+    traffic, traffic_src = read_traffic(args.config, "luma::" + names[dom][5:])
     cpu = None if args.no_cpu else cpu_baseline(args.config)
     out = {
         "metric": METRIC,
@@ -218,7 +316,9 @@ def main():
         "roofline": {"bound": "hbm", "kernel": names[dom],
                      "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),
-                     "traffic": None},
+                     "traffic": None if traffic is None else round(traffic),
+                     "traffic_source": traffic_src,
+                     "algorithmic_bytes": pass_bytes[dom]},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
