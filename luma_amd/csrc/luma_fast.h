@@ -34,7 +34,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kLn2Hi = 0.693145751953125f;       // ln2 with its low 8 bits cleared
 constexpr float kLn2Lo = 1.42860682030941723e-6f;  // ln2 - kLn2Hi
-constexpr float kSmall = 0.015625f;  // 2^-6: polynomial regime bound
+constexpr float kSmall = 0.125f;  // polynomial regime bound of expm1 / log1p
 constexpr float kSafety = 2.0f;
 
 // Indices into Grid::fast, filled by make_fast (finalize) for the new grid.
@@ -50,10 +50,13 @@ enum FastSlot {
   kFastCount
 };
 
-// expm1 on [0, x_top]: Taylor polynomial when x_top <= 2^-6 (relative error
-// <= 3u), else degree-8 Taylor below 0.5 and exp2 - 1 above.
+// expm1 on [0, x_top]: Taylor polynomial x * (1 + x/2 + ... + x^5/720) when
+// x_top <= 1/8 (truncation 0.013u, float32 evaluation < 2.3u), else degree-8
+// Taylor below 0.5 and exp2 - 1 above.
 __device__ __forceinline__ float fast_expm1_small(float x) {
-  float c = fmaf(x, 1.0f / 24.0f, 1.0f / 6.0f);
+  float c = fmaf(x, 1.0f / 720.0f, 1.0f / 120.0f);
+  c = fmaf(x, c, 1.0f / 24.0f);
+  c = fmaf(x, c, 1.0f / 6.0f);
   c = fmaf(x, c, 0.5f);
   c = fmaf(x, c, 1.0f);
   return x * c;
@@ -79,12 +82,16 @@ __device__ __forceinline__ float fast_expm1_relerr(float x_top) {
   return 2.55f * (x_top * kU + 4.0f * kU);
 }
 
-// log1p on [0, a_top]: Taylor polynomial when a_top <= 2^-6 (relative error
-// <= 3u); else 2*atanh(a/(2+a)) (odd series to s^11, s <= 1/5) for a <= 0.5
-// and ln2*log2(b) + (a - (b - 1))/b, b = RN(1 + a), above (log1p >= 0.4
-// there, so v_log_f32's absolute error stays a few u relative).
+// log1p on [0, a_top]: Taylor polynomial a * (1 - a/2 + ... - a^7/8) when
+// a_top <= 1/8 (truncation 0.11u, float32 evaluation < 2u); else
+// 2*atanh(a/(2+a)) (odd series to s^11, s <= 1/5) for a <= 0.5 and
+// ln2*log2(b) + (a - (b - 1))/b, b = RN(1 + a), above (log1p >= 0.4 there,
+// so v_log_f32's absolute error stays a few u relative).
 __device__ __forceinline__ float fast_log1p_small(float a) {
-  float c = fmaf(a, 1.0f / 5.0f, -0.25f);
+  float c = fmaf(a, -1.0f / 8.0f, 1.0f / 7.0f);
+  c = fmaf(a, c, -1.0f / 6.0f);
+  c = fmaf(a, c, 1.0f / 5.0f);
+  c = fmaf(a, c, -0.25f);
   c = fmaf(a, c, 1.0f / 3.0f);
   c = fmaf(a, c, -0.5f);
   c = fmaf(a, c, 1.0f);
@@ -113,7 +120,7 @@ __device__ __forceinline__ float fast_log1p_relerr(float a_top) {
 
 // Largest a / log1p(a) on [0, a_top]: converts |m'| / dm into bins.
 __device__ __forceinline__ float a_over_log1p(float a_top) {
-  return a_top <= kSmall ? 1.01f : (float)((double)a_top / ::log1p((double)a_top)) * 1.01f;
+  return a_top > 0.0f ? (float)((double)a_top / ::log1p((double)a_top)) * 1.01f : 1.01f;
 }
 
 // Fast decode + EMA of one element (functional.py:113-126, 269-275).

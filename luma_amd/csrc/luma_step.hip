@@ -305,21 +305,32 @@ __device__ __noinline__ float2 exact_mv(int qm, int qw, float g, const LUMA_GLOB
   return make_float2(mn, vn);
 }
 
-// New codes of one element (int16 momentum code | uint16 preconditioner << 16).
-__device__ __noinline__ uint32_t exact_codes(int qm, int qw, float g, const LUMA_GLOBAL Grid *old,
-                                             const LUMA_GLOBAL Grid *nw, Hyper h, float um,
-                                             float uw) {
-  const float2 e = exact_mv(qm, qw, g, old, h);
+// New momentum code of one element from its old code (exact path; the same
+// float32 sequence as exact_mv's m' followed by exact_quant_m).
+__device__ __noinline__ int exact_code_m(int qm, float g, const LUMA_GLOBAL Grid *old,
+                                         const LUMA_GLOBAL Grid *nw, Hyper h, float um) {
+  const float m = old ? exact_decode_m(qm, old->dm) : 0.0f;
+  const float mn = h.beta1 * m + h.omb1 * g;
   const Grid G = *nw;
-  const int cm = exact_quant_m(e.x, G, um);
-  const int cw = exact_quant_w(e.y, G, h.eps, uw);
-  return ((uint32_t)cm & 0xFFFFu) | ((uint32_t)cw << 16);
+  return exact_quant_m(mn, G, um);
 }
 
-// Per-wave queue of elements whose fast result is not certified.  Elements
+// New preconditioner code of one element from its old code (exact path).
+__device__ __noinline__ int exact_code_w(int qw, float g, const LUMA_GLOBAL Grid *old,
+                                         const LUMA_GLOBAL Grid *nw, Hyper h, float uw) {
+  const float v = old ? exact_decode_v(qw, old->wmin, old->dw, h.eps) : 0.0f;
+  const float vn = h.beta2 * v + h.omb2 * (g * g);
+  const Grid G = *nw;
+  return exact_quant_w(vn, G, h.eps, uw);
+}
+
+// Per-wave queues of elements whose fast result is not certified.  Elements
 // are appended with ballot/mbcnt (no atomics) and run through the exact path
 // 64 at a time, one per lane, so the exact path runs at full SIMD width.
+// Pass 1 appends up to 8 x 64 entries before it drains its queue; pass 2
+// drains after every 64 appended, so its queues never exceed 127 entries.
 constexpr int kQueueCap = kVec * 64 + 64;
+constexpr int kQueueCap2 = 128;
 
 __device__ __forceinline__ uint32_t lane_id() {
   return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
@@ -515,8 +526,9 @@ struct P2Const {
 };
 
 // One iteration of 8 consecutive elements.  FULL: all 8 valid and 16-byte
-// aligned (vector loads/stores, no masking).  Returns the flags of elements
-// whose codes need the exact path; Q and coarse are kept for the queue.
+// aligned (vector loads/stores, no masking).  Returns which codes need the
+// exact path (bit j: momentum code of element j, bit 8 + j: preconditioner
+// code); Q and coarse are kept for the queues.
 template <int GD, bool INJ, bool SMALL, bool FULL>
 __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, int64_t e0, int n,
                                             uint32_t k0, uint32_t k1, Group8 &Q, U4 &coarse) {
@@ -571,10 +583,7 @@ __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, i
     int qw;
     const bool okw = certified_code(yw - zw0[j], ew, 65535, qw);
     ow[j] = qw;
-    if (FULL)
-      flags |= (okm && okw) ? 0u : (1u << j);
-    else
-      flags |= (!(okm && okw) && j < n) ? (1u << j) : 0u;
+    if (FULL || j < n) flags |= (okm ? 0u : (1u << j)) | (okw ? 0u : (0x100u << j));
   }
   if (FULL) {
     vf4 p0, p1;
@@ -633,30 +642,30 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   C.k8 = B.k8 + hb - C.zoff * C.k7;
   const bool vec_ok = tensor_vec_ok(T);
   const uint32_t lane = lane_id();
-  uint32_t qlen = 0;
-  // Exact codes of a queued element; its fast codes were already stored and
-  // are overwritten (same wavefront, so the stores stay in program order).
-  auto run = [&](uint2 ent) {
+  uint2 *queue_m = queue, *queue_w = queue + kQueueCap2;
+  uint32_t qlen_m = 0, qlen_w = 0;
+  // Queue entry: x = chunk offset | old code << 16, y = the uniform's top 8
+  // bits (Philox; its low 16 bits come from the fine block).  The fast codes
+  // were already stored; the exact ones overwrite them (same wavefront, so
+  // the stores stay in program order).
+  auto uniform = [&](int64_t i, uint32_t top, int which) {
+    const U4 fine = philox_fine_block((uint64_t)i, k0, k1);
+    return (float)((top << 16) | u4_half(fine, 2 * (int)(i & 3) + which)) * 0x1p-24f;
+  };
+  auto run_m = [&](uint2 ent) {
     const int64_t i = beg + (ent.x & 0xFFFFu);
-    const int qmo = (int)(int16_t)(ent.x >> 16);
-    const int qwo = (int)(ent.y & 0xFFFFu);
-    const float g = load_grad(T.grad, i, GD);
-    float um, uw;
-    if (INJ) {
-      um = T.u_m[i];
-      uw = T.u_w[i];
-    } else {
-      const U4 fine = philox_fine_block((uint64_t)i, k0, k1);
-      const int r = (int)(i & 3);
-      um = (float)((((ent.y >> 16) & 0xFFu) << 16) | u4_half(fine, 2 * r)) * 0x1p-24f;
-      uw = (float)(((ent.y >> 24) << 16) | u4_half(fine, 2 * r + 1)) * 0x1p-24f;
-    }
-    const uint32_t codes = exact_codes(qmo, qwo, g, old, nw, h, um, uw);
-    T.q_m[i] = (int16_t)(codes & 0xFFFFu);
-    T.q_w[i] = (int16_t)(codes >> 16);
+    const float um = INJ ? T.u_m[i] : uniform(i, ent.y, 0);
+    T.q_m[i] = (int16_t)exact_code_m((int)(int16_t)(ent.x >> 16), load_grad(T.grad, i, GD), old,
+                                     nw, h, um);
+  };
+  auto run_w = [&](uint2 ent) {
+    const int64_t i = beg + (ent.x & 0xFFFFu);
+    const float uw = INJ ? T.u_w[i] : uniform(i, ent.y, 1);
+    T.q_w[i] = (int16_t)exact_code_w((int)(ent.x >> 16), load_grad(T.grad, i, GD), old, nw, h,
+                                     uw);
   };
   // Every lane runs the same number of iterations (lanes past the end carry
-  // n = 0), so the ballots and the queue length stay uniform across the wave.
+  // n = 0), so the ballots and the queue lengths stay uniform across the wave.
   const int n_it = (int)((end - beg + kThreads * kVec - 1) / (kThreads * kVec));
   for (int it = 0; it < n_it; ++it) {
     const int64_t e0 = beg + ((int64_t)it * kThreads + threadIdx.x) * kVec;
@@ -669,28 +678,39 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
       flags = p2_iter<GD, INJ, SMALL, true>(T, C, e0, n, k0, k1, Q, coarse);
     else
       flags = p2_iter<GD, INJ, SMALL, false>(T, C, e0, n, k0, k1, Q, coarse);
-    if (__ballot(flags != 0)) {
-      const uint32_t off0 = (uint32_t)(e0 - beg);
+    if (!__ballot(flags != 0)) continue;
+    const uint32_t off0 = (uint32_t)(e0 - beg);
 #pragma unroll
-      for (int j = 0; j < kVec; ++j) {
-        const bool f = (flags >> j) & 1u;
-        const uint64_t bm = __ballot(f);
-        if (f) {
-          const uint32_t half = INJ ? 0u : (u4_word(coarse, j >> 1) >> (16 * (j & 1))) & 0xFFFFu;
-          queue[queue_pos(bm, qlen)] =
-              make_uint2((off0 + j) | ((uint32_t)Q.qm[j] << 16), (uint32_t)Q.qw[j] | (half << 16));
+    for (int j = 0; j < kVec; ++j) {
+      const uint32_t bytes = INJ ? 0u : u4_word(coarse, j >> 1) >> (16 * (j & 1));
+      const bool fm = (flags >> j) & 1u;
+      const uint64_t bm = __ballot(fm);
+      if (fm)
+        queue_m[queue_pos(bm, qlen_m)] =
+            make_uint2((off0 + j) | ((uint32_t)Q.qm[j] << 16), bytes & 0xFFu);
+      qlen_m += (uint32_t)__popcll(bm);
+      const bool fw = (flags >> (8 + j)) & 1u;
+      const uint64_t bw = __ballot(fw);
+      if (fw)
+        queue_w[queue_pos(bw, qlen_w)] =
+            make_uint2((off0 + j) | ((uint32_t)Q.qw[j] << 16), (bytes >> 8) & 0xFFu);
+      qlen_w += (uint32_t)__popcll(bw);
+      if (qlen_m >= 64 || qlen_w >= 64) {
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        if (qlen_m >= 64) {
+          qlen_m -= 64;
+          run_m(queue_m[qlen_m + lane]);
         }
-        qlen += (uint32_t)__popcll(bm);
-      }
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      while (qlen >= 64) {
-        qlen -= 64;
-        run(queue[qlen + lane]);
+        if (qlen_w >= 64) {
+          qlen_w -= 64;
+          run_w(queue_w[qlen_w + lane]);
+        }
       }
     }
   }
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  if (lane < qlen) run(queue[lane]);
+  if (lane < qlen_m) run_m(queue_m[lane]);
+  if (lane < qlen_w) run_w(queue_w[lane]);
 }
 
 template <int GD>
@@ -725,7 +745,7 @@ __global__ __launch_bounds__(kThreads) void pass2_fast_kernel(const Tensor *__re
   step_key(base_seed, T.step, T.param_id, k0, k1);
   const bool inj = noise_mode == LUMA_NOISE_INJECTED;
   const bool small = (old == nullptr || old->fast[kXTopM] <= kSmall) && nw->sm <= kSmall;
-  __shared__ uint2 qbuf[kThreads / 64][kQueueCap];
+  __shared__ uint2 qbuf[kThreads / 64][2 * kQueueCap2];
   uint2 *q = qbuf[threadIdx.x >> 6];
   if (T.grad_dtype == LUMA_GRAD_BF16)
     pass2_dispatch<LUMA_GRAD_BF16>(T, h, old, nw, beg, end, k0, k1, inj, small, q);
