@@ -64,6 +64,11 @@ CONFIGS = {
     "llama3_8b": dict(shapes=llama3_8b_shapes, grad=torch.bfloat16, std=1e-3, outliers=1e-3,
                       desc="Llama-3-8B-shaped fp32 param set (291 tensors), bf16 grads "
                            "N(0,1e-3) with 0.1% x100 outliers"),
+    "llama3_8b_hetero": dict(shapes=llama3_8b_shapes, grad=torch.float16, hetero=(1e-7, 1e-1, 5),
+                             restore=True,
+                             desc="Llama-3-8B-shaped fp32 param set (291 tensors), per-tensor grad std "
+                                  "log-uniform in [1e-7, 1e-1], fp16 grads scaled by 2^16 and "
+                                  "unscaled (GradScaler path), stepping from a restored state_dict"),
     "gpt2_small": dict(shapes=gpt2_small_shapes, grad=torch.bfloat16, std=1e-3, outliers=0.0,
                        desc="GPT-2-small-shaped fp32 param list (148 tensors), bf16 grads N(0,1e-3)"),
     "many_small": dict(shapes=many_small_shapes, grad=torch.float32, std=1e-4, outliers=0.0,
@@ -77,11 +82,27 @@ CONFIGS = {
 def make_set(cfg, device):
     shapes = cfg["shapes"]()
     torch.manual_seed(0)
+    stds = None
+    if cfg.get("hetero"):
+        lo, hi, seed = cfg["hetero"]
+        gen = torch.Generator().manual_seed(seed)
+        stds = torch.exp(torch.empty(len(shapes), dtype=torch.float64)
+                         .uniform_(math.log(lo), math.log(hi), generator=gen)).tolist()
     params, grads = [], []
-    for s in shapes:
+    for i, s in enumerate(shapes):
         p = torch.randn(s, device=device) * 0.02
         if len(s) == 1 and cfg["shapes"] is not many_small_shapes:
             p.fill_(1.0)                             # norm weights
+        if stds is not None:
+            # GradScaler: the backward pass produces grads scaled by 2^16 in fp16,
+            # unscale_ multiplies by 2^-16 in fp32 and stores fp16 again
+            g16 = (torch.randn(s, device=device) * (stds[i] * 2.0 ** 16)).half()
+            g = g16.float() * 2.0 ** -16
+            p.requires_grad_(True)
+            p.grad_dtype = None
+            params.append(p)
+            grads.append(g.half())
+            continue
         g = torch.randn(s, device=device) * cfg["std"]
         if cfg.get("outliers"):
             g = torch.where(torch.rand(s, device=device) < cfg["outliers"], g * 100.0, g)
@@ -262,6 +283,14 @@ def main():
     for _ in range(args.warmup):
         opt.step()
     torch.cuda.synchronize()
+    if cfg.get("restore"):
+        # resume from a checkpoint: the timed steps run on a fresh optimizer
+        sd = opt.state_dict()
+        opt = LUMA(params, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01)
+        opt.load_state_dict(sd)
+        del sd
+        opt.step()
+        torch.cuda.synchronize()
     print("bench: warmup done", file=sys.stderr, flush=True)
 
     evs = [torch.cuda.Event(enable_timing=True) for _ in range(4)]

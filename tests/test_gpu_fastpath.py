@@ -9,6 +9,8 @@ Parameters agree within 1e-6 of their scale (the fast AdamW update is not
 bit-matched by design).
 """
 
+import math
+
 import pytest
 import torch
 
@@ -94,3 +96,60 @@ def test_fast_equals_exact_ragged(n):
     for a, b in zip(fast, slow):
         assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
         assert a[2] == b[2] and a[3] == b[3]
+
+
+def _hetero_set(seed=5, n_tensors=12, numel=70001):
+    """Per-tensor grad std log-uniform in [1e-7, 1e-1]; fp16 grads produced the
+    GradScaler way: scale by 2^16, cast to fp16, unscale in fp32, cast back."""
+    g = torch.Generator().manual_seed(seed)
+    stds = torch.exp(torch.empty(n_tensors).uniform_(math.log(1e-7), math.log(1e-1), generator=g))
+    params = [(torch.randn(numel + 13 * i, generator=g) * 0.02) for i in range(n_tensors)]
+
+    def grads(t):
+        gt = torch.Generator().manual_seed(1000 * seed + t)
+        out = []
+        for p, s in zip(params, stds.tolist()):
+            scaled = (torch.randn(p.shape, generator=gt) * s * 2.0 ** 16).half()
+            out.append((scaled.float() * 2.0 ** -16).half())
+        return out
+    return params, grads
+
+
+def _hetero_run(exact):
+    params0, grads = _hetero_set()
+    xs = [p.clone().cuda().requires_grad_(True) for p in params0]
+    for x in xs:
+        x.grad_dtype = None
+    opt = LUMA(xs, lr=1e-3, weight_decay=0.01)
+    opt._base_seed = 0x5EED
+    opt._flags = L.FLAG_EXACT_ONLY if exact else 0
+    for t in range(1, 4):
+        for x, gr in zip(xs, grads(t)):
+            x.grad = gr.cuda()
+        opt.step()
+    # restart from the checkpoint, as a resumed run does
+    sd = opt.state_dict()
+    opt = LUMA(xs, lr=1e-3, weight_decay=0.01)
+    opt.load_state_dict(sd)
+    opt._flags = L.FLAG_EXACT_ONLY if exact else 0
+    out = []
+    for t in range(4, 8):
+        for x, gr in zip(xs, grads(t)):
+            x.grad = gr.cuda()
+        opt.step()
+        st = opt.state_dict()["state"]
+        out.append([(st[i]["Q_m"].cpu(), st[i]["Q_w"].cpu(), st[i]["S_m"], st[i]["S_v"],
+                     xs[i].detach().cpu().clone()) for i in range(len(xs))])
+    return out
+
+
+def test_fast_equals_exact_heterogeneous_fp16_restored():
+    """Heterogeneous-scale workload: fast path == exact path after a restore."""
+    fast, slow = _hetero_run(False), _hetero_run(True)
+    for t, (fs, ss) in enumerate(zip(fast, slow), start=4):
+        for i, (a, b) in enumerate(zip(fs, ss)):
+            assert torch.equal(a[0], b[0]), f"Q_m differs: step {t} tensor {i}"
+            assert torch.equal(a[1], b[1]), f"Q_w differs: step {t} tensor {i}"
+            assert a[2] == b[2] and a[3] == b[3], f"scales differ: step {t} tensor {i}"
+            scale = float(b[4].abs().max())
+            assert float((a[4] - b[4]).abs().max()) <= 1e-6 * scale
