@@ -18,9 +18,11 @@
 // [y - c - h, y - c + h], h = h0 + E + d/8 + slack, holds no integer.
 //
 // Worst-case errors of the gfx950 instructions used, measured over every
-// normal float32 input against float64 (u = 2^-24): v_exp_f32 1.42u,
-// v_log_f32 2.0u * max(|log2 x|, 1), v_sqrt_f32 1.56u, v_rcp_f32 1.54u.
-// The bounds below use 2u for each and a safety factor of 2 on the total.
+// normal float32 input against float64 (u = 2^-24, the unit roundoff):
+// v_exp_f32 1.42u, v_log_f32 2.0u * max(|log2 x|, 1) (absolute, log2
+// units), v_sqrt_f32 1.56u, v_rcp_f32 1.54u.  The pass-2 bounds below are
+// first-order sums of every rounding of both paths (derivations at
+// make_bounds) times a safety factor of 1.25; pass 1 keeps a factor of 2.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -35,7 +37,8 @@ constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kLn2Hi = 0.693145751953125f;       // ln2 with its low 8 bits cleared
 constexpr float kLn2Lo = 1.42860682030941723e-6f;  // ln2 - kLn2Hi
 constexpr float kSmall = 0.125f;  // polynomial regime bound of expm1 / log1p
-constexpr float kSafety = 2.0f;
+constexpr float kSafety = 2.0f;     // pass 1
+constexpr float kSafety2 = 1.25f;   // pass 2
 
 // Indices into Grid::fast, filled by make_fast (finalize) for the new grid.
 enum FastSlot {
@@ -47,11 +50,16 @@ enum FastSlot {
   kXTopM,       // f32(32767 * dm): largest momentum decode argument
   kXTopW,       // f32(65535 * dw): largest preconditioner decode argument
   kW2,          // (1 / w_min)^2: bound on (1/w)^2 of any decoded code
+  kCwHi,        // C = -ln2/dw (double) rounded to 16 significant bits, 0 when delta_w == 0
+  kCwLo,        // f32(C - kCwHi)
+  kWe,          // f32(w_min * eps)
+  kXMin,        // f32(w_min / w_max): smallest w_min * t of an unclamped w
   kFastCount
 };
 
 // expm1 on [0, x_top]: Taylor polynomial x * (1 + x/2 + ... + x^5/720) when
-// x_top <= 1/8 (truncation 0.013u, float32 evaluation < 2.3u), else degree-8
+// x_top <= 1/8 (truncation 0.013u, float32 evaluation < 2.3u; measured max
+// 1.98u), else degree-8
 // Taylor below 0.5 and exp2 - 1 above.
 __device__ __forceinline__ float fast_expm1_small(float x) {
   float c = fmaf(x, 1.0f / 720.0f, 1.0f / 120.0f);
@@ -77,13 +85,14 @@ __device__ __forceinline__ float fast_expm1_general(float x) {
 
 // Relative error of the fast expm1 on [0, x_top] vs the correctly rounded value.
 __device__ __forceinline__ float fast_expm1_relerr(float x_top) {
-  if (x_top <= kSmall) return 4.0f * kU;
+  if (x_top <= kSmall) return 3.0f * kU;
   // exp2 branch: (argument rounding x*u + 2u + 1u for the subtraction) * e^x/(e^x-1) <= 2.55
   return 2.55f * (x_top * kU + 4.0f * kU);
 }
 
 // log1p on [0, a_top]: Taylor polynomial a * (1 - a/2 + ... - a^7/8) when
-// a_top <= 1/8 (truncation 0.11u, float32 evaluation < 2u); else
+// a_top <= 1/8 (truncation 0.11u, float32 evaluation < 2.2u; measured max
+// 1.5u); else
 // 2*atanh(a/(2+a)) (odd series to s^11, s <= 1/5) for a <= 0.5 and
 // ln2*log2(b) + (a - (b - 1))/b, b = RN(1 + a), above (log1p >= 0.4 there,
 // so v_log_f32's absolute error stays a few u relative).
@@ -115,12 +124,7 @@ __device__ __forceinline__ float fast_log1p_general(float a) {
 
 // Relative error bound of the fast log1p on [0, a_top].
 __device__ __forceinline__ float fast_log1p_relerr(float a_top) {
-  return a_top <= kSmall ? 4.0f * kU : 10.0f * kU;
-}
-
-// Largest a / log1p(a) on [0, a_top]: converts |m'| / dm into bins.
-__device__ __forceinline__ float a_over_log1p(float a_top) {
-  return a_top > 0.0f ? (float)((double)a_top / ::log1p((double)a_top)) * 1.01f : 1.01f;
+  return a_top <= kSmall ? 3.0f * kU : 10.0f * kU;
 }
 
 // Fast decode + EMA of one element (functional.py:113-126, 269-275).
@@ -129,30 +133,33 @@ struct FastEma {
   float mn;   // m'
   float vn;   // v'
   float am;   // |m| decoded (for the error bound)
-  float xw;   // preconditioner decode argument
 };
 
+// ndw = -dw; sign = 0x80000000 (both passed in so that callers can keep them
+// in VGPRs).  The preconditioner argument is formed as q * (-dw), which is
+// exactly -(the exact path's float32 q * dw).
+//
 // PRECISE_V: form e^-x with the two-word argument reduction (pass 2, whose
 // parameter update and code bounds use v'); pass 1 only needs the cheaper
 // single exp2, whose error its max-tracking bound covers (x * u term).
 template <bool SMALL_M, bool PRECISE_V>
-__device__ __forceinline__ FastEma fast_ema(int qm, int qw, float g, float dm, float dw,
+__device__ __forceinline__ FastEma fast_ema(int qm, int qw, float g, float dm, float ndw,
                                             float iwmin, float eps, float b1, float omb1,
-                                            float b2, float omb2) {
+                                            float b2, float omb2, uint32_t sign) {
   FastEma r;
   const float qf = (float)qm;
   const float x = fabsf(qf) * dm;
   const float e = SMALL_M ? fast_expm1_small(x) : fast_expm1_general(x);
-  const float m = copysignf(e, qf);
+  const float m = __uint_as_float(__float_as_uint(e) | (__float_as_uint(qf) & sign));
   r.am = e;
-  r.xw = (float)(qw & 0xFFFF) * dw;
+  const float nx = (float)(qw & 0xFFFF) * ndw;
   // w_min / w = e^-x: 2^a with a = RN(-x*log2e), times e^d, where
   // d = -x - a*ln2 is formed with a two-word ln2, so the rounding of the
   // exponent argument does not scale with x.
-  const float a = r.xw * -kLog2e;
+  const float a = nx * kLog2e;
   float ex = __builtin_amdgcn_exp2f(a);
   if (PRECISE_V) {
-    float d = fmaf(a, -kLn2Hi, -r.xw);
+    float d = fmaf(a, -kLn2Hi, nx);
     d = fmaf(a, -kLn2Lo, d);
     ex = fmaf(ex, d, ex);
   }
@@ -170,8 +177,9 @@ __device__ __forceinline__ FastEma fast_ema(int qm, int qw, float g, float dm, f
 
 namespace luma {
 
-// Derived constants of a freshly computed grid (finalize, set_scales, import).
-__device__ inline void make_fast(Grid &g) {
+// Derived constants of a freshly computed grid (finalize, set_scales, import);
+// eps is the group's float32 eps.
+__device__ inline void make_fast(Grid &g, float eps) {
   for (int i = 0; i < 20; ++i) g.fast[i] = 0.0f;
   g.fast[kIdm] = (float)(1.0 / (double)g.dm);
   g.fast[kYTopM] = cr_log1p(g.sm) / g.dm;
@@ -182,19 +190,56 @@ __device__ inline void make_fast(Grid &g) {
   g.fast[kXTopW] = 65535.0f * g.dw;
   const double iw = 1.0 / (double)g.wmin;
   g.fast[kW2] = (float)(iw * iw * (1.0 + 1e-6));
+  if (g.dwpos) {
+    const double c = -0.6931471805599453 / (double)g.dw;
+    int e;
+    const double m = ::frexp(c, &e);
+    const double hi = ::ldexp(::nearbyint(::ldexp(m, 16)), e - 16);
+    g.fast[kCwHi] = (float)hi;
+    g.fast[kCwLo] = (float)(c - hi);
+  }
+  g.fast[kWe] = (float)((double)g.wmin * (double)eps);
+  g.fast[kXMin] = (float)((double)g.wmin / (double)g.wmax);
 }
 
 // Error bounds of one tensor's fast path for one step (built per workgroup).
 struct Bounds {
   // pass 1: |m'_exact| in |m'_fast| * (1 +- dlt_m) +- abs_m, same for v'.
   float dlt_m, abs_m, dlt_v, abs_v;
-  // pass 2: |y_fast - y_exact| <= |m| * k1 + y * k2 + k3 (momentum)
-  //                             <= x_w * k6 + y * k7 + k8 (preconditioner)
-  float k1, k2, k3, k6, k7, k8;
+  // pass 2, in bins: |z_fast - z_exact| <= |m| * k1 + z * k2 + k3 (momentum)
+  //                                      <= A * k7 + k8 (preconditioner)
+  // where z is the bin index plus an offset in (0, 1] and A = e * C_hi.
+  float k1, k2, k3, k7, k8;
 };
 
 // old: grid the codes were written with (null at t = 1); nw: grid of the
 // new scales (null in pass 1).
+//
+// Momentum (first order; a = |m'|, y = log1p(a)/dm).  Decode: the fast
+// expm1 (rho_e) and the exact one (u) differ by (rho_e + u)|m|; the exact
+// path's b1*m rounds once more (u b1 |m|); both EMAs round the sum (u a
+// each; omb1*g is the same float32 product in both).  A change da moves y
+// by da/((1+a) dm), and a/((1+a) log1p a) <= 1, so the EMA terms cost
+// 2u y.  Then the fast log1p (rho_l y), 1/dm's rounding (u y), the exact
+// log1p and division (2u y) and the fused z = L/dm + offset (u (y + 1)):
+//   k1 = b1 (rho_e + 2u) / dm,  k2 = rho_l + 6u,  k3 = u  (times kSafety2).
+//
+// Preconditioner (relative error of x = w_min t against the exact path's
+// 1 / (w / w_min); P = 1/w_old, R = P - eps).  Exact decode rounds exp,
+// w_min*E and 1/W (3u); the fast one has 1/w_min's rounding, exp2 with
+// the two-word reduction and its fma (u + 2.42u): |P_f - P_E| <= 6.42u P.
+// Both round P - eps and r^2.  The EMA, sqrt and t = s + eps propagate
+// the decode error with weight (s/t)(b2 v/v')(P/R) <= 1 (because
+// v' >= b2 v), giving 6.42u + 3.5u (EMA, squaring) + 3.56u (sqrt: 1.56u +
+// u) + u (t) + 2u (1/t, w/w_min) + 2u (fast fma and w_min*eps) = 18.5u
+// at t >= 2 (7.6u at t = 1, where v = 0).  In bins that is rel / dw.  Then
+// y = (e + log2 mant) C with C = -ln2/dw: v_log_f32 on the mantissa (2u
+// log2 units), C's rounding and the product (2u|C|), the fma with C_lo and
+// the sum with the offset (2u|C|), x_min's rounding (u/dw), and the exact
+// path's log and division (2u y <= 2u (A + |C|)):
+//   k7 = 2u,  k8 = (rel + 1 + 4.16 + 1.39) u / dw + 4u  (times kSafety2).
+// LogSR's t(u) is within delta/8 of u, added unscaled; 1e-6 covers the
+// exact path's rounding of p* (a few u) and of 1 - u.
 __device__ inline Bounds make_bounds(const Grid *old, const Grid *nw, float b1, float b2) {
   Bounds B;
   const float rho_x = 2.0f * kU;  // v_exp_f32
@@ -209,19 +254,20 @@ __device__ inline Bounds make_bounds(const Grid *old, const Grid *nw, float b1, 
   B.abs_m = kSafety * b1 * s_old * (rho_e1 + 0.5f * kU) + 1e-37f;
   B.dlt_v = kSafety * 2.5f * kU;
   B.abs_v = kSafety * 2.0f * b2 * w2 * rho_p + 1e-37f;
-  B.k1 = B.k2 = B.k3 = B.k6 = B.k7 = B.k8 = 0.0f;
+  B.k1 = B.k2 = B.k3 = B.k7 = B.k8 = 0.0f;
   if (nw) {
+    const float rho_e = old ? fast_expm1_relerr(old->fast[kXTopM]) : 0.0f;
     const float rho_l = fast_log1p_relerr(nw->sm);
-    const float aol = a_over_log1p(nw->sm);
-    B.k1 = old ? kSafety * b1 * (rho_e1 + 0.5f * kU) * nw->fast[kIdm] : 0.0f;
-    B.k2 = kSafety * (kU * aol + rho_l + 3.0f * kU);
-    B.k3 = nw->dm * 0.125f + 8.0f * kU + 1e-6f;
+    B.k1 = old ? kSafety2 * b1 * (rho_e + 2.0f * kU) * nw->fast[kIdm] : 0.0f;
+    B.k2 = kSafety2 * (rho_l + 6.0f * kU);
+    B.k3 = kSafety2 * kU + nw->dm * 0.125f + 1e-6f;
     if (nw->dwpos) {
       const float idw = 1.0f / nw->dw;
-      B.k6 = 0.0f;
-      B.k7 = kSafety * 4.4f * kU;
-      B.k8 = kSafety * ((old ? rho_x + 13.0f * kU : 8.0f * kU) * idw) + nw->dw * 0.125f +
-             8.0f * kU + 1e-6f;
+      const float rel = old ? 18.5f * kU : 7.6f * kU;
+      B.k7 = kSafety2 * 2.0f * kU;
+      B.k8 = kSafety2 * ((rel + 6.55f * kU) * idw + 4.0f * kU) + nw->dw * 0.125f + 1e-6f;
+    } else {
+      B.k8 = 1e-6f;
     }
   }
   return B;

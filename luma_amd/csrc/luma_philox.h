@@ -69,6 +69,29 @@ LUMA_HD U4 philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uin
   return o;
 }
 
+#if defined(__HIPCC__)
+// Device variant with the multipliers passed in (callers keep them, and the
+// key, in VGPRs; see in_vgpr in luma_step.hip).
+__device__ __forceinline__ U4 philox4x32_10_v(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3,
+                                              uint32_t k0, uint32_t k1, uint32_t m0,
+                                              uint32_t m1) {
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const uint64_t p0 = (uint64_t)m0 * c0;
+    const uint64_t p1 = (uint64_t)m1 * c2;
+    const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0;
+    const uint32_t n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1;
+    c0 = n0;
+    c1 = (uint32_t)p1;
+    c2 = n2;
+    c3 = (uint32_t)p0;
+    k0 += kPhiloxW0;
+    k1 += kPhiloxW1;
+  }
+  return U4{c0, c1, c2, c3};
+}
+#endif
+
 // Counter-block indices for element e (see the header comment).
 LUMA_HD U4 philox_coarse_block(uint64_t e, uint32_t k0, uint32_t k1) {
   const uint64_t b = e >> 3;

@@ -165,7 +165,7 @@ __global__ __launch_bounds__(64) void finalize_kernel(const Tensor *__restrict__
     s.s_m[par] = s_m;
     s.s_v[par] = s_v;
     make_grid(s_m, s_v, hypers[T.hyper].eps_d, s.grid[par]);
-    make_fast(s.grid[par]);
+    make_fast(s.grid[par], hypers[T.hyper].eps);
   }
 }
 
@@ -332,6 +332,18 @@ __device__ __noinline__ int exact_code_w(int qw, float g, const LUMA_GLOBAL Grid
 constexpr int kQueueCap = kVec * 64 + 64;
 constexpr int kQueueCap2 = 128;
 
+// Keeps a wave-uniform value in a VGPR.  On gfx950 a VALU instruction with
+// an SGPR source operand issues at about half the rate of one whose sources
+// are VGPRs, inline constants or literals (measured: 0.95 vs 1.5-1.8 wave
+// instructions per clock per CU), so the streaming loops read their
+// per-tensor constants from VGPRs.  The empty asm makes the value opaque,
+// which stops the compiler from re-reading it from the SGPR.
+template <typename V>
+__device__ __forceinline__ V in_vgpr(V x) {
+  asm("" : "+v"(x));
+  return x;
+}
+
 __device__ __forceinline__ uint32_t lane_id() {
   return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
 }
@@ -375,16 +387,21 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 // Fast |m'| and v' of 8 consecutive elements as float bit patterns (for
 // non-negative floats the unsigned order is the float order, with every NaN
 // above +Inf); invalid elements of a partial group give 0.
+// Constants of the pass-1 loop, kept in VGPRs (see in_vgpr).
+struct P1Const {
+  float dm, ndw, iwmin, eps, b1, omb1, b2, omb2;
+  uint32_t sign;
+};
+
 template <int GD, bool SMALL, bool FULL>
-__device__ __forceinline__ void p1_iter(const Tensor &T, const DecodeK &D, const Hyper &h,
-                                        int64_t e0, int n, uint32_t (&am)[kVec],
-                                        uint32_t (&av)[kVec]) {
+__device__ __forceinline__ void p1_iter(const Tensor &T, const P1Const &K, int64_t e0, int n,
+                                        uint32_t (&am)[kVec], uint32_t (&av)[kVec]) {
   Group8 G;
   load_group<GD>(T, e0, n, FULL, G);
 #pragma unroll
   for (int j = 0; j < kVec; ++j) {
-    const FastEma f = fast_ema<SMALL, false>(G.qm[j], G.qw[j], G.g[j], D.dm, D.dw, D.iwmin,
-                                             D.eps, h.beta1, h.omb1, h.beta2, h.omb2);
+    const FastEma f = fast_ema<SMALL, false>(G.qm[j], G.qw[j], G.g[j], K.dm, K.ndw, K.iwmin,
+                                             K.eps, K.b1, K.omb1, K.b2, K.omb2, K.sign);
     am[j] = __float_as_uint(f.mn) & 0x7FFFFFFFu;
     av[j] = __float_as_uint(f.vn) & 0x7FFFFFFFu;
     if (!FULL && j >= n) am[j] = av[j] = 0u;
@@ -403,6 +420,16 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
                                 uint32_t *queue) {
   const Bounds B = make_bounds((const Grid *)old, nullptr, h.beta1, h.beta2);
   const DecodeK D = decode_consts(old, h.eps);
+  P1Const K;
+  K.dm = in_vgpr(D.dm);
+  K.ndw = in_vgpr(-D.dw);
+  K.iwmin = in_vgpr(D.iwmin);
+  K.eps = in_vgpr(D.eps);
+  K.b1 = in_vgpr(h.beta1);
+  K.omb1 = in_vgpr(h.omb1);
+  K.b2 = in_vgpr(h.beta2);
+  K.omb2 = in_vgpr(h.omb2);
+  K.sign = in_vgpr(0x80000000u);
   const bool vec_ok = tensor_vec_ok(T);
   const float lo_m = 1.0f - B.dlt_m, hi_m = 1.0f / (1.0f + B.dlt_m);
   const float lo_v = 1.0f - B.dlt_v, hi_v = 1.0f / (1.0f + B.dlt_v);
@@ -427,9 +454,9 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     const int n = rem <= 0 ? 0 : (rem < kVec ? (int)rem : kVec);
     uint32_t am[kVec], av[kVec];
     if (vec_ok && n == kVec)
-      p1_iter<GD, SMALL, true>(T, D, h, e0, n, am, av);
+      p1_iter<GD, SMALL, true>(T, K, e0, n, am, av);
     else
-      p1_iter<GD, SMALL, false>(T, D, h, e0, n, am, av);
+      p1_iter<GD, SMALL, false>(T, K, e0, n, am, av);
     const uint32_t im = max(max(max(am[0], am[1]), max(am[2], am[3])),
                             max(max(am[4], am[5]), max(am[6], am[7])));
     const uint32_t iv = max(max(max(av[0], av[1]), max(av[2], av[3])),
@@ -502,28 +529,76 @@ __global__ __launch_bounds__(kThreads) void pass1_fast_kernel(const Tensor *__re
   }
 }
 
-// Certified LogSR decision (see luma_fast.h).  z = y + 1 - c, where c is
-// the middle of the uniform's interval; e bounds |y - y_exact| plus the
-// interval's half width.  The code is floor(z) clamped to [0, kmax]; it is
-// certain when [z - e, z + e] holds no integer.
-__device__ __forceinline__ bool certified_code(float z, float e, int kmax, int &q) {
-  const float fl = floorf(z);
-  const float fr = z - fl;
-  q = (int)__builtin_amdgcn_fmed3f(fl, 0.0f, (float)kmax);
-  return fabsf(fr - 0.5f) + e < 0.5f;
+// Certified LogSR decision (see luma_fast.h): with z = y + 1 - c, c the
+// middle of the uniform's interval, the code is floor(z); it is certain
+// when [z - e, z + e] holds no integer, e bounding |z - z_exact| plus the
+// interval's half width.  Given h = 0.5 - e, returns 1 when not certain:
+// the sign bit of max(h - |fract(z) - 0.5|, -1), so that NaN counts as
+// uncertain (fmax drops it) -- computed without compares, whose lane-mask
+// results cost more than plain VALU on gfx950.
+__device__ __forceinline__ uint32_t unsure(float z, float h) {
+  const float d = fmaxf(h - fabsf(__builtin_amdgcn_fractf(z) - 0.5f), -1.0f);
+  return __float_as_uint(d) >> 31;
 }
 
 // Per-tensor constants of pass 2.
 struct P2Const {
   DecodeK D;
+  uint32_t pk0, pk1, pm0, pm1;  // Philox key and multipliers
+  float ndw;                    // -dw of the old grid (decode)
+  float nk1, nk2, hk3, nk7, hk8;   // -k1, -k2, 0.5 - k3, -k7, 0.5 - k8
   float b1, omb1, b2, omb2, decay, neg_eta, eps;
-  float isbc2;            // 1 / sqrt(bc2)
-  float idm, ytop_m;      // momentum: 1/dm, largest y (+ zoff)
-  float nl2dw, ytop_w;    // preconditioner: -ln2/dw, largest y (+ zoff)
-  float wmin_n;
-  float zoff;             // 1 - center of a Philox bucket offset (or 1 when injected)
+  float isbc2;              // 1 / sqrt(bc2)
+  float idm;                // momentum: 1/dm
+  float cf, ch, cl;         // preconditioner: C = -ln2/dw as float, 16-bit head, tail
+  float wmin_n, we, xmin;   // new w_min, w_min * eps, w_min / w_max
+  float zoff;               // 1 - half width of a Philox bucket (1 when injected)
   float k1, k2, k3, k7, k8;
+  float kmax_m, kmax_w;     // 32767, 65535
+  uint32_t sign;            // 0x80000000
 };
+
+// Moves every constant of the loop into VGPRs (see in_vgpr).
+__device__ __forceinline__ void launder(P2Const &C) {
+  C.D.dm = in_vgpr(C.D.dm);
+  C.D.dw = in_vgpr(C.D.dw);
+  C.D.iwmin = in_vgpr(C.D.iwmin);
+  C.D.eps = in_vgpr(C.D.eps);
+  C.pk0 = in_vgpr(C.pk0);
+  C.pk1 = in_vgpr(C.pk1);
+  C.pm0 = in_vgpr(C.pm0);
+  C.pm1 = in_vgpr(C.pm1);
+  C.b1 = in_vgpr(C.b1);
+  C.omb1 = in_vgpr(C.omb1);
+  C.b2 = in_vgpr(C.b2);
+  C.omb2 = in_vgpr(C.omb2);
+  C.decay = in_vgpr(C.decay);
+  C.neg_eta = in_vgpr(C.neg_eta);
+  C.eps = in_vgpr(C.eps);
+  C.isbc2 = in_vgpr(C.isbc2);
+  C.idm = in_vgpr(C.idm);
+  C.cf = in_vgpr(C.cf);
+  C.ch = in_vgpr(C.ch);
+  C.cl = in_vgpr(C.cl);
+  C.wmin_n = in_vgpr(C.wmin_n);
+  C.we = in_vgpr(C.we);
+  C.xmin = in_vgpr(C.xmin);
+  C.zoff = in_vgpr(C.zoff);
+  C.k1 = in_vgpr(C.k1);
+  C.k2 = in_vgpr(C.k2);
+  C.k3 = in_vgpr(C.k3);
+  C.k7 = in_vgpr(C.k7);
+  C.k8 = in_vgpr(C.k8);
+  C.kmax_m = in_vgpr(C.kmax_m);
+  C.ndw = in_vgpr(C.ndw);
+  C.nk1 = in_vgpr(C.nk1);
+  C.nk2 = in_vgpr(C.nk2);
+  C.hk3 = in_vgpr(C.hk3);
+  C.nk7 = in_vgpr(C.nk7);
+  C.hk8 = in_vgpr(C.hk8);
+  C.kmax_w = in_vgpr(C.kmax_w);
+  C.sign = in_vgpr(C.sign);
+}
 
 // One iteration of 8 consecutive elements.  FULL: all 8 valid and 16-byte
 // aligned (vector loads/stores, no masking).  Returns which codes need the
@@ -543,47 +618,55 @@ __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, i
 #pragma unroll
     for (int j = 0; j < kVec; ++j) p[j] = j < n ? T.param[e0 + j] : 0.0f;
   }
-  // uniform interval centers, already subtracted from the 1 + y offset
+  // offsets zoff - (lower end of the uniform's interval): z = y + offset
+  float zmu_m[kVec], zmu_w[kVec];
   if (INJ) {
 #pragma unroll
     for (int j = 0; j < kVec; ++j) {
-      zm0[j] = (FULL || j < n) ? T.u_m[e0 + j] : 0.5f;
-      zw0[j] = (FULL || j < n) ? T.u_w[e0 + j] : 0.5f;
+      zmu_m[j] = C.zoff - ((FULL || j < n) ? T.u_m[e0 + j] : 0.5f);
+      zmu_w[j] = C.zoff - ((FULL || j < n) ? T.u_w[e0 + j] : 0.5f);
     }
   } else {
-    coarse = philox_coarse_block((uint64_t)e0, k0, k1);
+    const uint64_t b = (uint64_t)e0 >> 3;   // coarse block of elements e0 .. e0+7
+    coarse = philox4x32_10_v((uint32_t)b, (uint32_t)(b >> 32), 0u, 0u, C.pk0, C.pk1, C.pm0, C.pm1);
 #pragma unroll
     for (int j = 0; j < kVec; ++j) {
-      zm0[j] = (float)u4_byte(coarse, 2 * j) * (1.0f / 256.0f);
-      zw0[j] = (float)u4_byte(coarse, 2 * j + 1) * (1.0f / 256.0f);
+      zmu_m[j] = fmaf((float)u4_byte(coarse, 2 * j), -1.0f / 256.0f, C.zoff);
+      zmu_w[j] = fmaf((float)u4_byte(coarse, 2 * j + 1), -1.0f / 256.0f, C.zoff);
     }
   }
   int om[kVec], ow[kVec];
   uint32_t flags = 0;
 #pragma unroll
   for (int j = 0; j < kVec; ++j) {
-    const FastEma f = fast_ema<SMALL, true>(Q.qm[j], Q.qw[j], Q.g[j], C.D.dm, C.D.dw, C.D.iwmin,
-                                            C.D.eps, C.b1, C.omb1, C.b2, C.omb2);
+    const FastEma f = fast_ema<SMALL, true>(Q.qm[j], Q.qw[j], Q.g[j], C.D.dm, C.ndw, C.D.iwmin,
+                                            C.D.eps, C.b1, C.omb1, C.b2, C.omb2, C.sign);
     const float s = __builtin_amdgcn_sqrtf(f.vn);
     // AdamW update (functional.py:278-279), within 1e-6 of the exact path
     const float den = fmaf(s, C.isbc2, C.eps);
     p[j] = fmaf(p[j], C.decay, (C.neg_eta * f.mn) * __builtin_amdgcn_rcpf(den));
-    // momentum code
-    const float a = fabsf(f.mn);
-    const float L = SMALL ? fast_log1p_small(a) : fast_log1p_general(a);
-    const float ym = fminf(fmaf(L, C.idm, C.zoff), C.ytop_m);
-    const float em = fmaf(f.am, C.k1, fmaf(ym, C.k2, C.k3));
-    int qm;
-    const bool okm = certified_code(ym - zm0[j], em, 32767, qm);
-    om[j] = f.mn < 0.0f ? -qm : qm;
-    // preconditioner code (delta_w = 0 gives nl2dw = 0: y = 0)
-    const float t = s + C.eps;
-    const float yw = fminf(fmaf(__builtin_amdgcn_logf(C.wmin_n * t), C.nl2dw, C.zoff), C.ytop_w);
-    const float ew = fmaf(yw, C.k7, C.k8);
-    int qw;
-    const bool okw = certified_code(yw - zw0[j], ew, 65535, qw);
-    ow[j] = qw;
-    if (FULL || j < n) flags |= (okm ? 0u : (1u << j)) | (okw ? 0u : (0x100u << j));
+    // momentum code: z = log1p(|m'|)/dm + offset.  |m'| <= S_m' exactly, so
+    // the exact path's clamp is inactive; the code's sign is m''s.
+    const float am = in_vgpr(fabsf(f.mn));   // one v_and, not an |.| modifier per fma
+    const float L = SMALL ? fast_log1p_small(am) : fast_log1p_general(am);
+    const float zm = fmaf(L, C.idm, zmu_m[j]);
+    const float hm = fmaf(f.am, C.nk1, fmaf(zm, C.nk2, C.hk3));    // 0.5 - e
+    om[j] = (int)__uint_as_float(
+        __float_as_uint(__builtin_amdgcn_fmed3f(floorf(zm), 0.0f, C.kmax_m)) |
+        (__float_as_uint(f.mn) & C.sign));
+    // preconditioner code: x = w_min t, clamped to the exact path's w range;
+    // y = -log2(x) ln2/dw = (e + log2 mant) C, with e C exact (16-bit C_hi)
+    // so that only O(|C|) terms round.  delta_w = 0 gives C = 0: code 0.
+    const float x = __builtin_amdgcn_fmed3f(fmaf(s, C.wmin_n, C.we), C.xmin, 1.0f);
+    const float ef = (float)__builtin_amdgcn_frexp_expf(x);
+    const float l2 = __builtin_amdgcn_logf(__builtin_amdgcn_frexp_mantf(x));
+    const float A = ef * C.ch;
+    const float zw = fmaf(l2, C.cf, fmaf(ef, C.cl, __builtin_amdgcn_fractf(A) + zmu_w[j]));
+    const float hw = fmaf(A, C.nk7, C.hk8);                        // 0.5 - e
+    ow[j] = (int)__builtin_amdgcn_fmed3f(floorf(A) + floorf(zw), 0.0f, C.kmax_w);
+    // uncertain when 0.5 - e - |fract(z) - 0.5| < 0 or NaN: its sign bit
+    const uint32_t um = unsure(zm, hm), uw = unsure(zw, hw);
+    if (FULL || j < n) flags |= (um << j) | (uw << (8 + j));
   }
   if (FULL) {
     vf4 p0, p1;
@@ -618,51 +701,66 @@ __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, i
 template <int GD, bool INJ, bool SMALL>
 __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOBAL Grid *old,
                                 const LUMA_GLOBAL Grid *nw, int64_t beg, int64_t end,
-                                uint32_t k0, uint32_t k1, uint2 *queue) {
+                                uint32_t k0, uint32_t k1, uint4 *queue) {
   const Bounds B = make_bounds((const Grid *)old, (const Grid *)nw, h.beta1, h.beta2);
   P2Const C;
   C.D = decode_consts(old, h.eps);
   C.b1 = h.beta1; C.omb1 = h.omb1; C.b2 = h.beta2; C.omb2 = h.omb2;
   C.decay = h.decay; C.neg_eta = h.neg_eta; C.eps = h.eps;
   C.isbc2 = (float)(1.0 / ::sqrt((double)h.bc2));
-  // y is formed as y + zoff, zoff = 1 - (half width of the uniform's interval),
-  // so that z = y + zoff - u_low has floor(z) = the LogSR code.
+  // z = y + zoff - u_low has floor(z) = the LogSR code when u is known to
+  // lie in [u_low, u_low + 2 hb): zoff = 1 - hb (Philox: 1/256 buckets).
   const float hb = INJ ? 0.0f : 1.0f / 512.0f;
   C.zoff = 1.0f - hb;
   C.idm = nw->fast[kIdm];
-  C.ytop_m = nw->fast[kYTopM] + C.zoff;
-  C.nl2dw = nw->fast[kNl2dw];
-  C.ytop_w = nw->fast[kYTopW] + C.zoff;
+  C.cf = nw->fast[kNl2dw];
+  C.ch = nw->fast[kCwHi];
+  C.cl = nw->fast[kCwLo];
   C.wmin_n = nw->wmin;
-  // the bounds were derived for y; y + zoff adds at most one rounding (u * y)
+  C.we = nw->fast[kWe];
+  C.xmin = nw->fast[kXMin];
   C.k1 = B.k1;
-  C.k2 = B.k2 + kSafety * kU;
-  C.k3 = B.k3 + hb - C.zoff * C.k2;
-  C.k7 = B.k7 + kSafety * kU;
-  C.k8 = B.k8 + hb - C.zoff * C.k7;
+  C.k2 = B.k2;
+  C.k3 = B.k3 + hb;
+  C.k7 = B.k7;
+  C.k8 = B.k8 + hb;
+  C.kmax_m = 32767.0f;
+  C.kmax_w = 65535.0f;
+  C.sign = 0x80000000u;
+  C.pk0 = k0;
+  C.pk1 = k1;
+  C.pm0 = kPhiloxM0;
+  C.pm1 = kPhiloxM1;
+  C.ndw = -C.D.dw;
+  C.nk1 = -C.k1;
+  C.nk2 = -C.k2;
+  C.hk3 = 0.5f - C.k3;
+  C.nk7 = -C.k7;
+  C.hk8 = 0.5f - C.k8;
+  launder(C);
   const bool vec_ok = tensor_vec_ok(T);
   const uint32_t lane = lane_id();
-  uint2 *queue_m = queue, *queue_w = queue + kQueueCap2;
+  uint4 *queue_m = queue, *queue_w = queue + kQueueCap2;
   uint32_t qlen_m = 0, qlen_w = 0;
   // Queue entry: x = chunk offset | old code << 16, y = the uniform's top 8
-  // bits (Philox; its low 16 bits come from the fine block).  The fast codes
-  // were already stored; the exact ones overwrite them (same wavefront, so
-  // the stores stay in program order).
+  // bits (Philox; its low 16 bits come from the fine block), z = the
+  // gradient as float32 bits (no second read of HBM).  The fast codes were
+  // already stored; the exact ones overwrite them (same wavefront, so the
+  // stores stay in program order).
   auto uniform = [&](int64_t i, uint32_t top, int which) {
     const U4 fine = philox_fine_block((uint64_t)i, k0, k1);
     return (float)((top << 16) | u4_half(fine, 2 * (int)(i & 3) + which)) * 0x1p-24f;
   };
-  auto run_m = [&](uint2 ent) {
+  auto run_m = [&](uint4 ent) {
     const int64_t i = beg + (ent.x & 0xFFFFu);
     const float um = INJ ? T.u_m[i] : uniform(i, ent.y, 0);
-    T.q_m[i] = (int16_t)exact_code_m((int)(int16_t)(ent.x >> 16), load_grad(T.grad, i, GD), old,
+    T.q_m[i] = (int16_t)exact_code_m((int)(int16_t)(ent.x >> 16), __uint_as_float(ent.z), old,
                                      nw, h, um);
   };
-  auto run_w = [&](uint2 ent) {
+  auto run_w = [&](uint4 ent) {
     const int64_t i = beg + (ent.x & 0xFFFFu);
     const float uw = INJ ? T.u_w[i] : uniform(i, ent.y, 1);
-    T.q_w[i] = (int16_t)exact_code_w((int)(ent.x >> 16), load_grad(T.grad, i, GD), old, nw, h,
-                                     uw);
+    T.q_w[i] = (int16_t)exact_code_w((int)(ent.x >> 16), __uint_as_float(ent.z), old, nw, h, uw);
   };
   // Every lane runs the same number of iterations (lanes past the end carry
   // n = 0), so the ballots and the queue lengths stay uniform across the wave.
@@ -686,14 +784,15 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
       const bool fm = (flags >> j) & 1u;
       const uint64_t bm = __ballot(fm);
       if (fm)
-        queue_m[queue_pos(bm, qlen_m)] =
-            make_uint2((off0 + j) | ((uint32_t)Q.qm[j] << 16), bytes & 0xFFu);
+        queue_m[queue_pos(bm, qlen_m)] = make_uint4((off0 + j) | ((uint32_t)Q.qm[j] << 16),
+                                                    bytes & 0xFFu, __float_as_uint(Q.g[j]), 0u);
       qlen_m += (uint32_t)__popcll(bm);
       const bool fw = (flags >> (8 + j)) & 1u;
       const uint64_t bw = __ballot(fw);
       if (fw)
-        queue_w[queue_pos(bw, qlen_w)] =
-            make_uint2((off0 + j) | ((uint32_t)Q.qw[j] << 16), (bytes >> 8) & 0xFFu);
+        queue_w[queue_pos(bw, qlen_w)] = make_uint4((off0 + j) | ((uint32_t)Q.qw[j] << 16),
+                                                    (bytes >> 8) & 0xFFu, __float_as_uint(Q.g[j]),
+                                                    0u);
       qlen_w += (uint32_t)__popcll(bw);
       if (qlen_m >= 64 || qlen_w >= 64) {
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -718,7 +817,7 @@ __device__ __forceinline__ void pass2_dispatch(const Tensor &T, const Hyper &h,
                                                const LUMA_GLOBAL Grid *old,
                                                const LUMA_GLOBAL Grid *nw, int64_t beg,
                                                int64_t end, uint32_t k0, uint32_t k1, bool inj,
-                                               bool small, uint2 *q) {
+                                               bool small, uint4 *q) {
   if (inj) {
     if (small) pass2_fast_body<GD, true, true>(T, h, old, nw, beg, end, k0, k1, q);
     else pass2_fast_body<GD, true, false>(T, h, old, nw, beg, end, k0, k1, q);
@@ -745,8 +844,8 @@ __global__ __launch_bounds__(kThreads) void pass2_fast_kernel(const Tensor *__re
   step_key(base_seed, T.step, T.param_id, k0, k1);
   const bool inj = noise_mode == LUMA_NOISE_INJECTED;
   const bool small = (old == nullptr || old->fast[kXTopM] <= kSmall) && nw->sm <= kSmall;
-  __shared__ uint2 qbuf[kThreads / 64][2 * kQueueCap2];
-  uint2 *q = qbuf[threadIdx.x >> 6];
+  __shared__ uint4 qbuf[kThreads / 64][2 * kQueueCap2];
+  uint4 *q = qbuf[threadIdx.x >> 6];
   if (T.grad_dtype == LUMA_GRAD_BF16)
     pass2_dispatch<LUMA_GRAD_BF16>(T, h, old, nw, beg, end, k0, k1, inj, small, q);
   else if (T.grad_dtype == LUMA_GRAD_F16)
@@ -769,7 +868,7 @@ __global__ void set_scales_kernel(Slot *__restrict__ slots, const LumaScaleInit 
   s.s_m[par] = it.s_m;
   s.s_v[par] = it.s_v;
   make_grid(it.s_m, it.s_v, it.eps, s.grid[par]);
-  make_fast(s.grid[par]);
+  make_fast(s.grid[par], (float)it.eps);
 }
 
 __global__ void get_scales_kernel(const Slot *__restrict__ slots, const int32_t *__restrict__ idx,
@@ -832,7 +931,7 @@ __global__ __launch_bounds__(64) void quant_finalize_kernel(const float *__restr
     s.s_m[par] = py_max((double)am, 1e-9);
     s.s_v[par] = py_max((double)av, 0.0);
     make_grid(s.s_m[par], s.s_v[par], eps, s.grid[par]);
-    make_fast(s.grid[par]);
+    make_fast(s.grid[par], (float)eps);
   }
 }
 
