@@ -548,7 +548,7 @@ struct P2Const {
   float ndw;                    // -dw of the old grid (decode)
   float nk1, nk2, hk3, nk7, hk8;   // -k1, -k2, 0.5 - k3, -k7, 0.5 - k8
   float b1, omb1, b2, omb2, decay, neg_eta, eps;
-  float isbc2;              // 1 / sqrt(bc2)
+  float isbc2, eps_u;       // 1 / (sqrt(bc2) (-eta)), eps / (-eta)
   float idm;                // momentum: 1/dm
   float cf, ch, cl;         // preconditioner: C = -ln2/dw as float, 16-bit head, tail
   float wmin_n, we, xmin;   // new w_min, w_min * eps, w_min / w_max
@@ -576,6 +576,7 @@ __device__ __forceinline__ void launder(P2Const &C) {
   C.neg_eta = in_vgpr(C.neg_eta);
   C.eps = in_vgpr(C.eps);
   C.isbc2 = in_vgpr(C.isbc2);
+  C.eps_u = in_vgpr(C.eps_u);
   C.idm = in_vgpr(C.idm);
   C.cf = in_vgpr(C.cf);
   C.ch = in_vgpr(C.ch);
@@ -642,9 +643,10 @@ __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, i
     const FastEma f = fast_ema<SMALL, true>(Q.qm[j], Q.qw[j], Q.g[j], C.D.dm, C.ndw, C.D.iwmin,
                                             C.D.eps, C.b1, C.omb1, C.b2, C.omb2, C.sign);
     const float s = __builtin_amdgcn_sqrtf(f.vn);
-    // AdamW update (functional.py:278-279), within 1e-6 of the exact path
-    const float den = fmaf(s, C.isbc2, C.eps);
-    p[j] = fmaf(p[j], C.decay, (C.neg_eta * f.mn) * __builtin_amdgcn_rcpf(den));
+    // AdamW update (functional.py:278-279), within 1e-6 of the exact path:
+    // p*decay + m' / ((sqrt(v')/sqrt(bc2) + eps) / (-eta))
+    const float den = fmaf(s, C.isbc2, C.eps_u);
+    p[j] = fmaf(p[j], C.decay, f.mn * __builtin_amdgcn_rcpf(den));
     // momentum code: z = log1p(|m'|)/dm + offset.  |m'| <= S_m' exactly, so
     // the exact path's clamp is inactive; the code's sign is m''s.
     const float am = in_vgpr(fabsf(f.mn));   // one v_and, not an |.| modifier per fma
@@ -707,7 +709,14 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   C.D = decode_consts(old, h.eps);
   C.b1 = h.beta1; C.omb1 = h.omb1; C.b2 = h.beta2; C.omb2 = h.omb2;
   C.decay = h.decay; C.neg_eta = h.neg_eta; C.eps = h.eps;
-  C.isbc2 = (float)(1.0 / ::sqrt((double)h.bc2));
+  // the update's denominator divided by -eta (lr = 0: an infinite
+  // denominator, so the update term is exactly 0)
+  {
+    const double ne = (double)h.neg_eta;
+    const double isb = 1.0 / ::sqrt((double)h.bc2);
+    C.isbc2 = ne != 0.0 ? (float)(isb / ne) : 0.0f;
+    C.eps_u = ne != 0.0 ? (float)((double)h.eps / ne) : INFINITY;
+  }
   // z = y + zoff - u_low has floor(z) = the LogSR code when u is known to
   // lie in [u_low, u_low + 2 hb): zoff = 1 - hb (Philox: 1/256 buckets).
   const float hb = INJ ? 0.0f : 1.0f / 512.0f;
