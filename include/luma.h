@@ -6,6 +6,13 @@
  * each entry point returns 0 on success or a nonzero status whose text is
  * available from luma_last_error().
  *
+ * Every per-step quantity lives in device memory: each tensor's step count,
+ * scales and grids sit in its slot, and the step-dependent scalars are
+ * derived on the device from the param group's hyper-parameters.  A launch
+ * sequence captured into a HIP graph therefore advances correctly on every
+ * replay (the reference keeps its step counter on the device for the same
+ * reason, optimizer.py:382-387).
+ *
  * What each entry point replaces in the reference (IgorYashch/LUMA 0.1.0):
  *
  *   luma_step          -- the per-parameter loop body of LUMA.step for all
@@ -15,14 +22,20 @@
  *                         i.e. the Triton pipelines luma_triton_init_step /
  *                         luma_triton_step (triton_kernel.py:409-492).
  *   luma_step_profiled -- luma_step with event records between its launches.
+ *   luma_step_tensor   -- one tensor, no device tables: the per-tensor
+ *                         functional ops luma_triton_step /
+ *                         luma_triton_init_step (triton_kernel.py:409-492).
  *   luma_set_scales    -- the scale half of load_state_dict /
  *                         _init_triton_buffers (optimizer.py:146-183,341-387).
- *   luma_get_scales    -- the S_m / S_v read-back of state_dict
+ *   luma_get_scales    -- the S_m / S_v / step read-back of state_dict
  *                         (optimizer.py:119-144).
  *   luma_decode        -- the decode of export_adamw_state
  *                         (optimizer.py:231-235, functional.py:113-126).
  *   luma_quantize      -- the quantisation of import_adamw_state
  *                         (optimizer.py:304-321, functional.py:133-176).
+ *   luma_hyper_rows    -- the step-dependent scalars of functional.py:209-213,
+ *                         262-264, 278 as the device derives them (for
+ *                         checking against the host's double arithmetic).
  *   luma_philox4x32    -- host-side Philox4x32-10 block function used by the
  *                         stochastic rounding (Salmon et al., SC'11); the
  *                         reference's Triton path draws from tl.rand
@@ -38,13 +51,17 @@
 extern "C" {
 #endif
 
-#define LUMA_ABI_VERSION 1
+#define LUMA_ABI_VERSION 2
 
 /* Elements per chunk-table entry (one workgroup's share of a tensor). */
 #define LUMA_CHUNK_ELEMS 32768
 
-/* Bytes of one opaque scale slot (per-tensor persistent state). */
-#define LUMA_SLOT_BYTES 256
+/*
+ * Bytes of one slot: a tensor's persistent device state (step count, S_m,
+ * S_v, grids).  A fresh slot must be zero-filled (step count 0: the next
+ * step is the reference's init step).  16-byte aligned.
+ */
+#define LUMA_SLOT_BYTES 512
 
 /* Gradient element types. */
 #define LUMA_GRAD_F32 0
@@ -58,7 +75,7 @@ extern "C" {
 /* luma_step flags. */
 #define LUMA_FLAG_EXACT_ONLY 1 /* take the exact per-element path everywhere */
 
-/* One parameter tensor taking part in a step (array in device memory). */
+/* One parameter tensor taking part in a step. */
 typedef struct LumaTensor {
   float *param;         /* device f32 [numel], updated in place            */
   const void *grad;     /* device f32 / bf16 / f16 [numel]                  */
@@ -66,13 +83,13 @@ typedef struct LumaTensor {
   int16_t *q_w;         /* device [numel] uint16 preconditioner codes       */
   const float *u_m;     /* device [numel] injected uniforms, or NULL        */
   const float *u_w;     /* device [numel] injected uniforms, or NULL        */
+  void *slot;           /* device, LUMA_SLOT_BYTES: this tensor's state     */
   int64_t numel;        /* elements                                          */
-  int64_t step;         /* this update's step number t (1 = first update)   */
   int64_t param_id;     /* position of the parameter in param_groups order  */
   int32_t grad_dtype;   /* LUMA_GRAD_*                                       */
-  int32_t hyper;        /* index into the LumaHyper table                    */
-  int32_t slot;         /* index into the scale-slot table                   */
+  int32_t group;        /* index into the LumaGroup table                    */
   int32_t first_chunk;  /* index of this tensor's first LumaChunk            */
+  int32_t reserved;     /* 0                                                 */
 } LumaTensor;
 
 /* Chunk c of a tensor covers elements [c*LUMA_CHUNK_ELEMS, min(numel, (c+1)*LUMA_CHUNK_ELEMS)). */
@@ -82,36 +99,34 @@ typedef struct LumaChunk {
 } LumaChunk;
 
 /*
- * Per (param group, step) coefficients.  The caller computes them in double
- * exactly as the reference does and rounds each to float32 once:
- * beta1 = f32(b1), omb1 = f32(1 - b1), beta2 = f32(b2), omb2 = f32(1 - b2),
- * decay = f32(1 - wd*lr), neg_eta = f32(-(lr / (1 - b1^t))),
- * bc2 = f32(1 - b2^t), eps = f32(eps); eps_d is eps itself.
+ * A param group's hyper-parameters as the Python doubles the reference holds
+ * (optimizer.py:80-92).  Per step the device derives, exactly as the
+ * reference's double arithmetic and each rounded once to float32:
+ * beta1, 1 - beta1, beta2, 1 - beta2, 1 - weight_decay*lr,
+ * -(lr / (1 - beta1^t)), 1 - beta2^t and eps, where beta^t is the correctly
+ * rounded power (Python's ** agrees with it after the float32 rounding).
  */
-typedef struct LumaHyper {
-  float beta1, omb1, beta2, omb2;
-  float decay, neg_eta, bc2, eps;
-  double eps_d;
-} LumaHyper;
+typedef struct LumaGroup {
+  double lr, beta1, beta2, eps, weight_decay;
+  double reserved; /* 0 */
+} LumaGroup;
 
 typedef struct LumaStepArgs {
   const LumaTensor *tensors; /* device */
   int32_t n_tensors;
   int32_t n_chunks;
   const LumaChunk *chunks;   /* device */
-  const LumaHyper *hypers;   /* device */
-  void *slots;               /* device, LUMA_SLOT_BYTES per slot, zero-initialised */
-  float *partials;           /* device workspace, 2 floats per chunk */
+  const LumaGroup *groups;   /* device */
+  float *partials;           /* device workspace, luma_workspace_bytes(n_chunks) */
   uint64_t base_seed;        /* LUMA._base_seed as its two's-complement bits */
   int32_t noise_mode;        /* LUMA_NOISE_* */
   int32_t flags;             /* LUMA_FLAG_* */
 } LumaStepArgs;
 
-/* One scale-slot write (array in device memory). */
+/* One slot write (array in device memory). */
 typedef struct LumaScaleInit {
-  int32_t slot;
-  int32_t pad;
-  int64_t step;  /* the tensor's current step count t (parity selects the buffer) */
+  void *slot;    /* device slot */
+  int64_t step;  /* the tensor's step count t */
   double s_m;    /* S_m as stored by the reference (>= 1e-9) */
   double s_v;    /* S_v (>= 0) */
   double eps;    /* the group's eps */
@@ -122,18 +137,21 @@ const char *luma_last_error(void);
 
 /*
  * Struct sizes as compiled, for binding checks: LumaTensor, LumaChunk,
- * LumaHyper, LumaScaleInit, LumaStepArgs, slot bytes, LUMA_CHUNK_ELEMS, 0.
+ * LumaGroup, LumaScaleInit, LumaStepArgs, slot bytes, LUMA_CHUNK_ELEMS, 0.
  */
 void luma_layout(int32_t out[8]);
 
-/* Bytes of workspace luma_step needs for n_chunks chunks. */
+/* Bytes of workspace luma_step / luma_step_tensor / luma_quantize need for n_chunks chunks. */
 size_t luma_workspace_bytes(int32_t n_chunks);
 
 /*
  * One optimizer step for every tensor in the table: pass 1 (decode + EMA +
- * per-chunk maxima), per-tensor finalize (new S_m/S_v and grid in float64),
- * pass 2 (re-decode + EMA + AdamW update + LogSR re-quantisation).  Three
- * kernel launches on `stream` (a hipStream_t), no host synchronisation.
+ * per-chunk maxima), per-tensor finalize (new S_m/S_v and grid in float64,
+ * step count + 1, step scalars), pass 2 (re-decode + EMA + AdamW update +
+ * LogSR re-quantisation).  A tensor whose slot holds step count 0 takes the
+ * init step.  Three kernel launches on `stream` (a hipStream_t), no host
+ * synchronisation; no device table is written, so the sequence may be
+ * captured into a HIP graph and replayed.
  */
 int luma_step(const LumaStepArgs *args, void *stream);
 
@@ -144,31 +162,47 @@ int luma_step(const LumaStepArgs *args, void *stream);
  */
 int luma_step_profiled(const LumaStepArgs *args, void *stream, void *const events[4]);
 
-/* Write S_m/S_v of n slots (items: device array) and derive their grids. */
-int luma_set_scales(void *slots, const LumaScaleInit *items, int32_t n, void *stream);
+/*
+ * luma_step for one tensor with no device tables: *tensor and *group are
+ * host structs read during the call (tensor->first_chunk is ignored);
+ * `partials` needs luma_workspace_bytes(ceil(numel / LUMA_CHUNK_ELEMS)).
+ */
+int luma_step_tensor(const LumaTensor *tensor, const LumaGroup *group, float *partials,
+                     uint64_t base_seed, int32_t noise_mode, int32_t flags, void *stream);
 
-/* Read S_m/S_v of n (slot, step) pairs into out[2*i], out[2*i+1] (device doubles). */
-int luma_get_scales(const void *slots, const int32_t *slot_idx, const int64_t *steps,
-                    int32_t n, double *out, void *stream);
+/* Write step count, S_m and S_v of n slots (items: device array) and derive their grids. */
+int luma_set_scales(const LumaScaleInit *items, int32_t n, void *stream);
 
 /*
- * Decode one tensor's codes into float32 m (exp_avg) and v (exp_avg_sq) using
- * the scales of (slot, step) and the group's eps.
+ * Read n slots (slots: device array of slot pointers): S_m, S_v into
+ * scales[2*i], scales[2*i+1] and the step count into steps[i] (device).
  */
-int luma_decode(const int16_t *q_m, const int16_t *q_w, int64_t numel, const void *slots,
-                int32_t slot, int64_t step, double eps, float *m_out, float *v_out,
-                void *stream);
+int luma_get_scales(void *const *slots, int32_t n, double *scales, int64_t *steps, void *stream);
+
+/*
+ * Decode one tensor's codes into float32 m (exp_avg) and v (exp_avg_sq) on
+ * the grid of the slot's current step, with the group's eps.
+ */
+int luma_decode(const int16_t *q_m, const int16_t *q_w, int64_t numel, const void *slot,
+                double eps, float *m_out, float *v_out, void *stream);
 
 /*
  * Quantise given float32 m, v (clamped at 0) into codes with fresh scales
- * S_m = max(max|m|, 1e-9), S_v = max(max v, 0), stored into (slot, step).
- * Uniforms: Philox keyed by seed (noise_mode 0) or u_m/u_w (noise_mode 1).
- * `partials` needs luma_workspace_bytes(ceil(numel / LUMA_CHUNK_ELEMS)).
+ * S_m = max(max|m|, 1e-9), S_v = max(max v, 0), stored into the slot with
+ * step count `step`.  Uniforms: Philox keyed by seed (noise_mode 0) or
+ * u_m/u_w (noise_mode 1).  `partials` needs
+ * luma_workspace_bytes(ceil(numel / LUMA_CHUNK_ELEMS)).
  */
 int luma_quantize(const float *m, const float *v, int64_t numel, int16_t *q_m, int16_t *q_w,
-                  void *slots, int32_t slot, int64_t step, double eps, uint64_t seed,
-                  int32_t noise_mode, const float *u_m, const float *u_w, float *partials,
-                  void *stream);
+                  void *slot, int64_t step, double eps, uint64_t seed, int32_t noise_mode,
+                  const float *u_m, const float *u_w, float *partials, void *stream);
+
+/*
+ * The step scalars the device derives for steps t0 .. t0+n-1 of *group (a
+ * host struct): 8 floats per step into out (device): beta1, 1-beta1, beta2,
+ * 1-beta2, decay, -eta, bc2, eps.
+ */
+int luma_hyper_rows(const LumaGroup *group, int64_t t0, int32_t n, float *out, void *stream);
 
 /* Host: one Philox4x32-10 block. */
 void luma_philox4x32(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);

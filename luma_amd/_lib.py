@@ -17,8 +17,8 @@ LIB_NAME = "libluma_hip.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 
 CHUNK_ELEMS = 32768          # LUMA_CHUNK_ELEMS
-SLOT_BYTES = 256             # LUMA_SLOT_BYTES
-ABI_VERSION = 1              # LUMA_ABI_VERSION
+SLOT_BYTES = 512             # LUMA_SLOT_BYTES
+ABI_VERSION = 2              # LUMA_ABI_VERSION
 
 GRAD_F32, GRAD_BF16, GRAD_F16 = 0, 1, 2
 NOISE_PHILOX, NOISE_INJECTED = 0, 1
@@ -26,20 +26,20 @@ FLAG_EXACT_ONLY = 1
 
 TENSOR_DTYPE = np.dtype([
     ("param", "<u8"), ("grad", "<u8"), ("q_m", "<u8"), ("q_w", "<u8"),
-    ("u_m", "<u8"), ("u_w", "<u8"),
-    ("numel", "<i8"), ("step", "<i8"), ("param_id", "<i8"),
-    ("grad_dtype", "<i4"), ("hyper", "<i4"), ("slot", "<i4"), ("first_chunk", "<i4"),
+    ("u_m", "<u8"), ("u_w", "<u8"), ("slot", "<u8"),
+    ("numel", "<i8"), ("param_id", "<i8"),
+    ("grad_dtype", "<i4"), ("group", "<i4"), ("first_chunk", "<i4"), ("reserved", "<i4"),
 ])
 CHUNK_DTYPE = np.dtype([("tensor", "<i4"), ("index", "<i4")])
-HYPER_DTYPE = np.dtype([
-    ("beta1", "<f4"), ("omb1", "<f4"), ("beta2", "<f4"), ("omb2", "<f4"),
-    ("decay", "<f4"), ("neg_eta", "<f4"), ("bc2", "<f4"), ("eps", "<f4"),
-    ("eps_d", "<f8"),
+GROUP_DTYPE = np.dtype([
+    ("lr", "<f8"), ("beta1", "<f8"), ("beta2", "<f8"), ("eps", "<f8"),
+    ("weight_decay", "<f8"), ("reserved", "<f8"),
 ])
 SCALE_INIT_DTYPE = np.dtype([
-    ("slot", "<i4"), ("pad", "<i4"), ("step", "<i8"),
-    ("s_m", "<f8"), ("s_v", "<f8"), ("eps", "<f8"),
+    ("slot", "<u8"), ("step", "<i8"), ("s_m", "<f8"), ("s_v", "<f8"), ("eps", "<f8"),
 ])
+# luma_hyper_rows output columns
+HYPER_ROW_FIELDS = ("beta1", "omb1", "beta2", "omb2", "decay", "neg_eta", "bc2", "eps")
 
 
 class StepArgs(ctypes.Structure):
@@ -48,8 +48,7 @@ class StepArgs(ctypes.Structure):
         ("n_tensors", ctypes.c_int32),
         ("n_chunks", ctypes.c_int32),
         ("chunks", ctypes.c_void_p),
-        ("hypers", ctypes.c_void_p),
-        ("slots", ctypes.c_void_p),
+        ("groups", ctypes.c_void_p),
         ("partials", ctypes.c_void_p),
         ("base_seed", ctypes.c_uint64),
         ("noise_mode", ctypes.c_int32),
@@ -72,13 +71,16 @@ _SIGNATURES = {
     "luma_step": (ctypes.c_int, [ctypes.POINTER(StepArgs), _VP]),
     "luma_step_profiled": (ctypes.c_int, [ctypes.POINTER(StepArgs), _VP,
                                           ctypes.POINTER(ctypes.c_void_p)]),
-    "luma_set_scales": (ctypes.c_int, [_VP, _VP, ctypes.c_int32, _VP]),
-    "luma_get_scales": (ctypes.c_int, [_VP, _VP, _VP, ctypes.c_int32, _VP, _VP]),
-    "luma_decode": (ctypes.c_int, [_VP, _VP, ctypes.c_int64, _VP, ctypes.c_int32, ctypes.c_int64,
-                                   ctypes.c_double, _VP, _VP, _VP]),
-    "luma_quantize": (ctypes.c_int, [_VP, _VP, ctypes.c_int64, _VP, _VP, _VP, ctypes.c_int32,
-                                     ctypes.c_int64, ctypes.c_double, ctypes.c_uint64,
-                                     ctypes.c_int32, _VP, _VP, _VP, _VP]),
+    "luma_step_tensor": (ctypes.c_int, [_VP, _VP, _VP, ctypes.c_uint64, ctypes.c_int32,
+                                        ctypes.c_int32, _VP]),
+    "luma_set_scales": (ctypes.c_int, [_VP, ctypes.c_int32, _VP]),
+    "luma_get_scales": (ctypes.c_int, [_VP, ctypes.c_int32, _VP, _VP, _VP]),
+    "luma_decode": (ctypes.c_int, [_VP, _VP, ctypes.c_int64, _VP, ctypes.c_double, _VP, _VP,
+                                   _VP]),
+    "luma_quantize": (ctypes.c_int, [_VP, _VP, ctypes.c_int64, _VP, _VP, _VP, ctypes.c_int64,
+                                     ctypes.c_double, ctypes.c_uint64, ctypes.c_int32, _VP, _VP,
+                                     _VP, _VP]),
+    "luma_hyper_rows": (ctypes.c_int, [_VP, ctypes.c_int64, ctypes.c_int32, _VP, _VP]),
     "luma_philox4x32": (None, [ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint32),
                                ctypes.POINTER(ctypes.c_uint32)]),
 }
@@ -108,7 +110,7 @@ def load(path: str = LIB_PATH):
 def check_layout(lib) -> None:
     out = (ctypes.c_int32 * 8)()
     lib.luma_layout(out)
-    want = [TENSOR_DTYPE.itemsize, CHUNK_DTYPE.itemsize, HYPER_DTYPE.itemsize,
+    want = [TENSOR_DTYPE.itemsize, CHUNK_DTYPE.itemsize, GROUP_DTYPE.itemsize,
             SCALE_INIT_DTYPE.itemsize, ctypes.sizeof(StepArgs), SLOT_BYTES, CHUNK_ELEMS]
     got = list(out)[:7]
     if got != want:

@@ -15,7 +15,10 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
+
+#include "luma_hyper.h"
 
 namespace luma {
 
@@ -37,19 +40,22 @@ struct Grid {
 };
 static_assert(sizeof(Grid) == 112, "grid layout");
 
-// Persistent per-tensor state: scales and grids, double-buffered by step parity.
+// Persistent per-tensor state (one LUMA_SLOT_BYTES buffer per tensor): the
+// step count, scales and grids double-buffered by step parity, and the
+// scalars of the latest step.  Step t writes s_m/s_v/grid[t & 1]; its
+// decode reads grid[(t - 1) & 1].
 struct Slot {
+  int64_t step;    // completed steps (0: no state yet, the next step is t = 1)
+  int64_t reserved;
   double s_m[2];
   double s_v[2];
+  Hyper hyp;       // scalars of step `step` (written by the step's finalize)
   Grid grid[2];
+  uint8_t pad[LUMA_SLOT_BYTES - 88 - 2 * sizeof(Grid)];
 };
-static_assert(sizeof(Slot) == 256, "slot layout");
-
-struct Hyper {
-  float beta1, omb1, beta2, omb2;
-  float decay, neg_eta, bc2, eps;
-  double eps_d;
-};
+static_assert(sizeof(Hyper) == 40, "hyper layout");
+static_assert(offsetof(Slot, grid) == 88, "slot layout");
+static_assert(sizeof(Slot) == LUMA_SLOT_BYTES, "slot layout");
 
 __device__ __forceinline__ float cr_expm1(float x) { return (float)::expm1((double)x); }
 __device__ __forceinline__ float cr_exp(float x) { return (float)::exp((double)x); }

@@ -27,7 +27,6 @@ constexpr int kThreads = 256;     // 4 wave64 per workgroup
 constexpr int kVec = 8;           // consecutive elements per thread per iteration
 constexpr int64_t kChunk = LUMA_CHUNK_ELEMS;
 static_assert(kChunk % (kThreads * kVec) == 0, "chunk must be a whole number of iterations");
-static_assert(sizeof(LumaHyper) == sizeof(Hyper), "hyper layout");
 
 // Device view of LumaTensor.  The pointer fields are declared in the global
 // address space so loads and stores through them compile to global_* (not
@@ -47,15 +46,52 @@ struct Tensor {
   LUMA_GLOBAL int16_t *q_w;
   const LUMA_GLOBAL float *u_m;
   const LUMA_GLOBAL float *u_w;
+  LUMA_GLOBAL Slot *slot;
   int64_t numel;
-  int64_t step;
   int64_t param_id;
   int32_t grad_dtype;
-  int32_t hyper;
-  int32_t slot;
+  int32_t group;
   int32_t first_chunk;
+  int32_t reserved;
 };
 static_assert(sizeof(Tensor) == sizeof(LumaTensor), "tensor layout");
+
+// Where a launch finds its tensors: the device tables of luma_step, or (when
+// `tensors` is null) the single tensor and group passed by value by
+// luma_step_tensor, whose chunks are then the workgroups in order.
+struct StepSrc {
+  const Tensor *tensors;
+  const LumaChunk *chunks;
+  const LumaGroup *groups;
+  Tensor one;
+  LumaGroup group;
+};
+
+// The chunk of this workgroup: its tensor, group and chunk index.
+__device__ __forceinline__ void chunk_job(const StepSrc &src, Tensor &T, LumaGroup &g,
+                                          int64_t &index) {
+  if (src.tensors) {
+    const LumaChunk c = src.chunks[blockIdx.x];
+    T = src.tensors[c.tensor];
+    g = src.groups[T.group];
+    index = c.index;
+  } else {
+    T = src.one;
+    g = src.group;
+    index = blockIdx.x;
+  }
+}
+
+// The tensor of this workgroup (one workgroup per tensor).
+__device__ __forceinline__ void tensor_job(const StepSrc &src, Tensor &T, LumaGroup &g) {
+  if (src.tensors) {
+    T = src.tensors[blockIdx.x];
+    g = src.groups[T.group];
+  } else {
+    T = src.one;
+    g = src.group;
+  }
+}
 
 __device__ __forceinline__ float load_grad(const LUMA_GLOBAL void *g, int64_t i, int dt) {
   if (dt == LUMA_GRAD_F32) return ((const LUMA_GLOBAL float *)g)[i];
@@ -110,16 +146,17 @@ __device__ __forceinline__ void element_ema(const Tensor &T, const Hyper &h, con
   exact_ema(m, v, g, h, mn, vn);
 }
 
-__global__ __launch_bounds__(kThreads) void pass1_exact_kernel(const Tensor *__restrict__ tensors,
-                                                         const LumaChunk *__restrict__ chunks,
-                                                         const Hyper *__restrict__ hypers,
-                                                         const Slot *__restrict__ slots,
-                                                         float *__restrict__ partials) {
-  const LumaChunk c = chunks[blockIdx.x];
-  const Tensor T = tensors[c.tensor];
-  const Hyper h = hypers[T.hyper];
-  const Grid *old = T.step >= 2 ? &slots[T.slot].grid[(T.step - 1) & 1] : nullptr;
-  const int64_t beg = (int64_t)c.index * kChunk;
+__global__ __launch_bounds__(kThreads) void pass1_exact_kernel(StepSrc src,
+                                                               float *__restrict__ partials) {
+  Tensor T;
+  LumaGroup grp;
+  int64_t ci;
+  chunk_job(src, T, grp, ci);
+  const Hyper h = group_hyper(grp);
+  // this step is t = step + 1; its decode reads the grid of step t - 1
+  const int64_t prev = T.slot->step;
+  const Grid *old = prev >= 1 ? (const Grid *)&T.slot->grid[prev & 1] : nullptr;
+  const int64_t beg = ci * kChunk;
   const int64_t end = beg + kChunk < T.numel ? beg + kChunk : T.numel;
 
   float am = 0.0f, av = 0.0f;
@@ -143,11 +180,11 @@ __global__ __launch_bounds__(kThreads) void pass1_exact_kernel(const Tensor *__r
 // S' = max(max, floor) with Python's max() semantics (a NaN maximum stays NaN).
 __device__ __forceinline__ double py_max(double a, double floor_) { return floor_ > a ? floor_ : a; }
 
-__global__ __launch_bounds__(64) void finalize_kernel(const Tensor *__restrict__ tensors,
-                                                      const Hyper *__restrict__ hypers,
-                                                      Slot *__restrict__ slots,
+__global__ __launch_bounds__(64) void finalize_kernel(StepSrc src,
                                                       const float *__restrict__ partials) {
-  const Tensor T = tensors[blockIdx.x];
+  Tensor T;
+  LumaGroup grp;
+  tensor_job(src, T, grp);
   const int nch = (int)((T.numel + kChunk - 1) / kChunk);
   float am = 0.0f, av = 0.0f;
   for (int i = threadIdx.x; i < nch; i += 64) {
@@ -160,30 +197,36 @@ __global__ __launch_bounds__(64) void finalize_kernel(const Tensor *__restrict__
   if (threadIdx.x == 0) {
     const double s_m = py_max((double)am, 1e-9);  // SCALE_FLOOR_M (config.py:25)
     const double s_v = py_max((double)av, 0.0);
-    Slot &s = slots[T.slot];
-    const int par = (int)(T.step & 1);
+    LUMA_GLOBAL Slot &s = *T.slot;
+    const int64_t t = s.step + 1;
+    const int par = (int)(t & 1);
+    const Hyper h = step_hyper(grp, t);
     s.s_m[par] = s_m;
     s.s_v[par] = s_v;
-    make_grid(s_m, s_v, hypers[T.hyper].eps_d, s.grid[par]);
-    make_fast(s.grid[par], hypers[T.hyper].eps);
+    Grid g;
+    make_grid(s_m, s_v, grp.eps, g);
+    make_fast(g, h.eps);
+    s.grid[par] = g;
+    s.hyp = h;
+    s.step = t;
   }
 }
 
-__global__ __launch_bounds__(kThreads) void pass2_exact_kernel(const Tensor *__restrict__ tensors,
-                                                         const LumaChunk *__restrict__ chunks,
-                                                         const Hyper *__restrict__ hypers,
-                                                         const Slot *__restrict__ slots,
-                                                         uint64_t base_seed, int noise_mode) {
-  const LumaChunk c = chunks[blockIdx.x];
-  const Tensor T = tensors[c.tensor];
-  const Hyper h = hypers[T.hyper];
-  const Slot &S = slots[T.slot];
-  const Grid *old = T.step >= 2 ? &S.grid[(T.step - 1) & 1] : nullptr;
-  const Grid G = S.grid[T.step & 1];
-  const int64_t beg = (int64_t)c.index * kChunk;
+__global__ __launch_bounds__(kThreads) void pass2_exact_kernel(StepSrc src, uint64_t base_seed,
+                                                               int noise_mode) {
+  Tensor T;
+  LumaGroup grp;
+  int64_t ci;
+  chunk_job(src, T, grp, ci);
+  const Slot &S = *(const Slot *)T.slot;
+  const int64_t t = S.step;   // advanced by finalize
+  const Hyper h = S.hyp;
+  const Grid *old = t >= 2 ? &S.grid[(t - 1) & 1] : nullptr;
+  const Grid G = S.grid[t & 1];
+  const int64_t beg = ci * kChunk;
   const int64_t end = beg + kChunk < T.numel ? beg + kChunk : T.numel;
   uint32_t k0, k1;
-  step_key(base_seed, T.step, T.param_id, k0, k1);
+  step_key(base_seed, t, T.param_id, k0, k1);
 
   for (int64_t e0 = beg + (int64_t)threadIdx.x * kVec; e0 < end; e0 += (int64_t)kThreads * kVec) {
     U4 coarse{}, fine0{}, fine1{};
@@ -496,17 +539,17 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   }
 }
 
-__global__ __launch_bounds__(kThreads) void pass1_fast_kernel(const Tensor *__restrict__ tensors,
-                                                              const LumaChunk *__restrict__ chunks,
-                                                              const Hyper *__restrict__ hypers,
-                                                              const Slot *__restrict__ slots,
+__global__ __launch_bounds__(kThreads) void pass1_fast_kernel(StepSrc src,
                                                               float *__restrict__ partials) {
-  const LumaChunk c = chunks[blockIdx.x];
-  const Tensor T = tensors[c.tensor];
-  const Hyper h = hypers[T.hyper];
-  const LUMA_GLOBAL Grid *old =
-      T.step >= 2 ? (const LUMA_GLOBAL Grid *)&slots[T.slot].grid[(T.step - 1) & 1] : nullptr;
-  const int64_t beg = (int64_t)c.index * kChunk;
+  Tensor T;
+  LumaGroup grp;
+  int64_t ci;
+  chunk_job(src, T, grp, ci);
+  const Hyper h = group_hyper(grp);
+  // this step is t = step + 1; its decode reads the grid of step t - 1
+  const int64_t prev = T.slot->step;
+  const LUMA_GLOBAL Grid *old = prev >= 1 ? &T.slot->grid[prev & 1] : nullptr;
+  const int64_t beg = ci * kChunk;
   const int64_t end = beg + kChunk < T.numel ? beg + kChunk : T.numel;
   const bool small = old == nullptr || old->fast[kXTopM] <= kSmall;
   __shared__ uint32_t qbuf[kThreads / 64][kQueueCap];
@@ -836,21 +879,21 @@ __device__ __forceinline__ void pass2_dispatch(const Tensor &T, const Hyper &h,
   }
 }
 
-__global__ __launch_bounds__(kThreads) void pass2_fast_kernel(const Tensor *__restrict__ tensors,
-                                                              const LumaChunk *__restrict__ chunks,
-                                                              const Hyper *__restrict__ hypers,
-                                                              const Slot *__restrict__ slots,
-                                                              uint64_t base_seed, int noise_mode) {
-  const LumaChunk c = chunks[blockIdx.x];
-  const Tensor T = tensors[c.tensor];
-  const Hyper h = hypers[T.hyper];
-  const LUMA_GLOBAL Slot *S = (const LUMA_GLOBAL Slot *)&slots[T.slot];
-  const LUMA_GLOBAL Grid *old = T.step >= 2 ? &S->grid[(T.step - 1) & 1] : nullptr;
-  const LUMA_GLOBAL Grid *nw = &S->grid[T.step & 1];
-  const int64_t beg = (int64_t)c.index * kChunk;
+__global__ __launch_bounds__(kThreads) void pass2_fast_kernel(StepSrc src, uint64_t base_seed,
+                                                              int noise_mode) {
+  Tensor T;
+  LumaGroup grp;
+  int64_t ci;
+  chunk_job(src, T, grp, ci);
+  const LUMA_GLOBAL Slot *S = T.slot;
+  const int64_t t = S->step;   // advanced by finalize
+  const Hyper h = S->hyp;
+  const LUMA_GLOBAL Grid *old = t >= 2 ? &S->grid[(t - 1) & 1] : nullptr;
+  const LUMA_GLOBAL Grid *nw = &S->grid[t & 1];
+  const int64_t beg = ci * kChunk;
   const int64_t end = beg + kChunk < T.numel ? beg + kChunk : T.numel;
   uint32_t k0, k1;
-  step_key(base_seed, T.step, T.param_id, k0, k1);
+  step_key(base_seed, t, T.param_id, k0, k1);
   const bool inj = noise_mode == LUMA_NOISE_INJECTED;
   const bool small = (old == nullptr || old->fast[kXTopM] <= kSmall) && nw->sm <= kSmall;
   __shared__ uint4 qbuf[kThreads / 64][2 * kQueueCap2];
@@ -867,37 +910,44 @@ __global__ __launch_bounds__(kThreads) void pass2_fast_kernel(const Tensor *__re
 //  Scale slots, decode (export) and quantise (import)
 // ---------------------------------------------------------------------------
 
-__global__ void set_scales_kernel(Slot *__restrict__ slots, const LumaScaleInit *__restrict__ items,
-                                  int n) {
+// Writes the state of one slot: step count t, the scales of step t and its grid.
+__device__ void write_slot(Slot &s, int64_t t, double s_m, double s_v, double eps) {
+  const int par = (int)(t & 1);
+  s.s_m[par] = s_m;
+  s.s_v[par] = s_v;
+  make_grid(s_m, s_v, eps, s.grid[par]);
+  make_fast(s.grid[par], (float)eps);
+  s.step = t;
+}
+
+__global__ void set_scales_kernel(const LumaScaleInit *__restrict__ items, int n) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const LumaScaleInit it = items[i];
-  Slot &s = slots[it.slot];
-  const int par = (int)(it.step & 1);
-  s.s_m[par] = it.s_m;
-  s.s_v[par] = it.s_v;
-  make_grid(it.s_m, it.s_v, it.eps, s.grid[par]);
-  make_fast(s.grid[par], (float)it.eps);
+  write_slot(*static_cast<Slot *>(it.slot), it.step, it.s_m, it.s_v, it.eps);
 }
 
-__global__ void get_scales_kernel(const Slot *__restrict__ slots, const int32_t *__restrict__ idx,
-                                  const int64_t *__restrict__ steps, int n, double *__restrict__ out) {
+__global__ void get_scales_kernel(void *const *__restrict__ slots, int n,
+                                  double *__restrict__ scales, int64_t *__restrict__ steps) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  const Slot &s = slots[idx[i]];
-  const int par = (int)(steps[i] & 1);
-  out[2 * i] = s.s_m[par];
-  out[2 * i + 1] = s.s_v[par];
+  const Slot &s = *static_cast<const Slot *>(slots[i]);
+  const int par = (int)(s.step & 1);
+  scales[2 * i] = s.s_m[par];
+  scales[2 * i + 1] = s.s_v[par];
+  steps[i] = s.step;
 }
 
 __global__ __launch_bounds__(kThreads) void decode_kernel(const int16_t *__restrict__ q_m,
                                                           const int16_t *__restrict__ q_w,
-                                                          int64_t n, const Slot *__restrict__ slots,
-                                                          int slot, int par, double eps,
-                                                          float *__restrict__ m_out,
+                                                          int64_t n, const Slot *__restrict__ slot,
+                                                          double eps, float *__restrict__ m_out,
                                                           float *__restrict__ v_out) {
   __shared__ Grid g;
-  if (threadIdx.x == 0) make_grid(slots[slot].s_m[par], slots[slot].s_v[par], eps, g);
+  if (threadIdx.x == 0) {
+    const int par = (int)(slot->step & 1);
+    make_grid(slot->s_m[par], slot->s_v[par], eps, g);
+  }
   __syncthreads();
   const float epsf = (float)eps;
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
@@ -926,8 +976,8 @@ __global__ __launch_bounds__(kThreads) void quant_max_kernel(const float *__rest
 }
 
 __global__ __launch_bounds__(64) void quant_finalize_kernel(const float *__restrict__ partials,
-                                                            int nch, Slot *__restrict__ slots,
-                                                            int slot, int par, double eps) {
+                                                            int nch, Slot *__restrict__ slot,
+                                                            int64_t step, double eps) {
   float am = 0.0f, av = 0.0f;
   for (int i = threadIdx.x; i < nch; i += 64) {
     am = nan_max(am, partials[2 * i]);
@@ -935,24 +985,18 @@ __global__ __launch_bounds__(64) void quant_finalize_kernel(const float *__restr
   }
   am = wave_max(am);
   av = wave_max(av);
-  if (threadIdx.x == 0) {
-    Slot &s = slots[slot];
-    s.s_m[par] = py_max((double)am, 1e-9);
-    s.s_v[par] = py_max((double)av, 0.0);
-    make_grid(s.s_m[par], s.s_v[par], eps, s.grid[par]);
-    make_fast(s.grid[par], (float)eps);
-  }
+  if (threadIdx.x == 0) write_slot(*slot, step, py_max((double)am, 1e-9), py_max((double)av, 0.0), eps);
 }
 
 __global__ __launch_bounds__(kThreads) void quant_kernel(const float *__restrict__ m,
                                                          const float *__restrict__ v, int64_t n,
                                                          int16_t *__restrict__ q_m,
                                                          int16_t *__restrict__ q_w,
-                                                         const Slot *__restrict__ slots, int slot,
-                                                         int par, double eps, uint64_t seed,
+                                                         const Slot *__restrict__ slot, int par,
+                                                         double eps, uint64_t seed,
                                                          int noise_mode, const float *__restrict__ u_m,
                                                          const float *__restrict__ u_w) {
-  const Grid G = slots[slot].grid[par];
+  const Grid G = slot->grid[par];
   const float epsf = (float)eps;
   const uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
   const int64_t beg = (int64_t)blockIdx.x * kChunk;
@@ -981,6 +1025,22 @@ __global__ __launch_bounds__(kThreads) void quant_kernel(const float *__restrict
       q_w[i] = (int16_t)(uint16_t)exact_quant_w(v[i], G, epsf, uw);
     }
   }
+}
+
+// Step scalars of steps t0 .. t0+n-1 (luma_hyper_rows).
+__global__ void hyper_rows_kernel(LumaGroup g, int64_t t0, int n, float *__restrict__ out) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const Hyper h = step_hyper(g, t0 + i);
+  float *o = out + 8 * (int64_t)i;
+  o[0] = h.beta1;
+  o[1] = h.omb1;
+  o[2] = h.beta2;
+  o[3] = h.omb2;
+  o[4] = h.decay;
+  o[5] = h.neg_eta;
+  o[6] = h.bc2;
+  o[7] = h.eps;
 }
 
 }  // namespace luma
@@ -1017,7 +1077,7 @@ size_t luma_workspace_bytes(int32_t n_chunks) { return (size_t)(n_chunks > 0 ? n
 void luma_layout(int32_t out[8]) {
   out[0] = (int32_t)sizeof(LumaTensor);
   out[1] = (int32_t)sizeof(LumaChunk);
-  out[2] = (int32_t)sizeof(LumaHyper);
+  out[2] = (int32_t)sizeof(LumaGroup);
   out[3] = (int32_t)sizeof(LumaScaleInit);
   out[4] = (int32_t)sizeof(LumaStepArgs);
   out[5] = (int32_t)sizeof(Slot);
@@ -1025,43 +1085,51 @@ void luma_layout(int32_t out[8]) {
   out[7] = 0;
 }
 
-static int step_impl(const LumaStepArgs *a, void *stream, void *const *events) {
-  if (!a) return fail("luma_step: null args");
-  if (a->n_tensors <= 0 || a->n_chunks <= 0) return 0;
-  if (!a->tensors || !a->chunks || !a->hypers || !a->slots || !a->partials)
-    return fail("luma_step: null table pointer");
-  if (a->noise_mode != LUMA_NOISE_PHILOX && a->noise_mode != LUMA_NOISE_INJECTED)
+// The three launches of one step over `n_chunks` chunks of `n_tensors`
+// tensors, with optional event records between them.
+static int launch_step(const StepSrc &src, int32_t n_tensors, int32_t n_chunks, float *partials,
+                       uint64_t base_seed, int32_t noise_mode, int32_t flags, hipStream_t s,
+                       void *const *events) {
+  if (noise_mode != LUMA_NOISE_PHILOX && noise_mode != LUMA_NOISE_INJECTED)
     return fail("luma_step: unknown noise_mode");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const Tensor *T = reinterpret_cast<const Tensor *>(a->tensors);
-  const Hyper *H = reinterpret_cast<const Hyper *>(a->hypers);
-  Slot *S = static_cast<Slot *>(a->slots);
   auto mark = [&](int i) -> int {
     if (!events || !events[i]) return 0;
     const hipError_t e = hipEventRecord(static_cast<hipEvent_t>(events[i]), s);
     return e == hipSuccess ? 0 : fail("luma_step: event record", e);
   };
   if (int r = mark(0)) return r;
-  const bool exact = (a->flags & LUMA_FLAG_EXACT_ONLY) != 0;
+  const bool exact = (flags & LUMA_FLAG_EXACT_ONLY) != 0;
   if (exact)
-    hipLaunchKernelGGL(pass1_exact_kernel, dim3(a->n_chunks), dim3(kThreads), 0, s, T, a->chunks,
-                       H, S, a->partials);
+    hipLaunchKernelGGL(pass1_exact_kernel, dim3(n_chunks), dim3(kThreads), 0, s, src, partials);
   else
-    hipLaunchKernelGGL(pass1_fast_kernel, dim3(a->n_chunks), dim3(kThreads), 0, s, T, a->chunks,
-                       H, S, a->partials);
+    hipLaunchKernelGGL(pass1_fast_kernel, dim3(n_chunks), dim3(kThreads), 0, s, src, partials);
   if (int r = check_launch("luma_step: pass 1 launch")) return r;
   if (int r = mark(1)) return r;
-  hipLaunchKernelGGL(finalize_kernel, dim3(a->n_tensors), dim3(64), 0, s, T, H, S, a->partials);
+  hipLaunchKernelGGL(finalize_kernel, dim3(n_tensors), dim3(64), 0, s, src,
+                     (const float *)partials);
   if (int r = check_launch("luma_step: finalize launch")) return r;
   if (int r = mark(2)) return r;
   if (exact)
-    hipLaunchKernelGGL(pass2_exact_kernel, dim3(a->n_chunks), dim3(kThreads), 0, s, T, a->chunks,
-                       H, S, a->base_seed, a->noise_mode);
+    hipLaunchKernelGGL(pass2_exact_kernel, dim3(n_chunks), dim3(kThreads), 0, s, src, base_seed,
+                       (int)noise_mode);
   else
-    hipLaunchKernelGGL(pass2_fast_kernel, dim3(a->n_chunks), dim3(kThreads), 0, s, T, a->chunks,
-                       H, S, a->base_seed, a->noise_mode);
+    hipLaunchKernelGGL(pass2_fast_kernel, dim3(n_chunks), dim3(kThreads), 0, s, src, base_seed,
+                       (int)noise_mode);
   if (int r = check_launch("luma_step: pass 2 launch")) return r;
   return mark(3);
+}
+
+static int step_impl(const LumaStepArgs *a, void *stream, void *const *events) {
+  if (!a) return fail("luma_step: null args");
+  if (a->n_tensors <= 0 || a->n_chunks <= 0) return 0;
+  if (!a->tensors || !a->chunks || !a->groups || !a->partials)
+    return fail("luma_step: null table pointer");
+  StepSrc src{};
+  src.tensors = reinterpret_cast<const Tensor *>(a->tensors);
+  src.chunks = a->chunks;
+  src.groups = a->groups;
+  return launch_step(src, a->n_tensors, a->n_chunks, a->partials, a->base_seed, a->noise_mode,
+                     a->flags, static_cast<hipStream_t>(stream), events);
 }
 
 int luma_step(const LumaStepArgs *a, void *stream) { return step_impl(a, stream, nullptr); }
@@ -1070,42 +1138,58 @@ int luma_step_profiled(const LumaStepArgs *a, void *stream, void *const events[4
   return step_impl(a, stream, events);
 }
 
-int luma_set_scales(void *slots, const LumaScaleInit *items, int32_t n, void *stream) {
+int luma_step_tensor(const LumaTensor *tensor, const LumaGroup *group, float *partials,
+                     uint64_t base_seed, int32_t noise_mode, int32_t flags, void *stream) {
+  if (!tensor || !group) return fail("luma_step_tensor: null tensor or group");
+  if (tensor->numel <= 0) return 0;
+  if (!tensor->param || !tensor->grad || !tensor->q_m || !tensor->q_w || !tensor->slot ||
+      !partials)
+    return fail("luma_step_tensor: null pointer");
+  if (noise_mode == LUMA_NOISE_INJECTED && (!tensor->u_m || !tensor->u_w))
+    return fail("luma_step_tensor: injected noise needs u_m and u_w");
+  const int64_t nch = (tensor->numel + kChunk - 1) / kChunk;
+  if (nch > 0x7fffffff) return fail("luma_step_tensor: tensor too large");
+  StepSrc src{};
+  memcpy(&src.one, tensor, sizeof(Tensor));
+  src.one.first_chunk = 0;
+  src.group = *group;
+  return launch_step(src, 1, (int32_t)nch, partials, base_seed, noise_mode, flags,
+                     static_cast<hipStream_t>(stream), nullptr);
+}
+
+int luma_set_scales(const LumaScaleInit *items, int32_t n, void *stream) {
   if (n <= 0) return 0;
-  if (!slots || !items) return fail("luma_set_scales: null pointer");
+  if (!items) return fail("luma_set_scales: null pointer");
   hipLaunchKernelGGL(set_scales_kernel, dim3((n + 63) / 64), dim3(64), 0,
-                     static_cast<hipStream_t>(stream), static_cast<Slot *>(slots), items, n);
+                     static_cast<hipStream_t>(stream), items, n);
   return check_launch("luma_set_scales: launch");
 }
 
-int luma_get_scales(const void *slots, const int32_t *slot_idx, const int64_t *steps, int32_t n,
-                    double *out, void *stream) {
+int luma_get_scales(void *const *slots, int32_t n, double *scales, int64_t *steps, void *stream) {
   if (n <= 0) return 0;
-  if (!slots || !slot_idx || !steps || !out) return fail("luma_get_scales: null pointer");
+  if (!slots || !scales || !steps) return fail("luma_get_scales: null pointer");
   hipLaunchKernelGGL(get_scales_kernel, dim3((n + 63) / 64), dim3(64), 0,
-                     static_cast<hipStream_t>(stream), static_cast<const Slot *>(slots), slot_idx,
-                     steps, n, out);
+                     static_cast<hipStream_t>(stream), slots, n, scales, steps);
   return check_launch("luma_get_scales: launch");
 }
 
-int luma_decode(const int16_t *q_m, const int16_t *q_w, int64_t numel, const void *slots,
-                int32_t slot, int64_t step, double eps, float *m_out, float *v_out, void *stream) {
+int luma_decode(const int16_t *q_m, const int16_t *q_w, int64_t numel, const void *slot,
+                double eps, float *m_out, float *v_out, void *stream) {
   if (numel <= 0) return 0;
-  if (!q_m || !q_w || !slots || !m_out || !v_out) return fail("luma_decode: null pointer");
+  if (!q_m || !q_w || !slot || !m_out || !v_out) return fail("luma_decode: null pointer");
   int64_t blocks = (numel + kThreads * 8 - 1) / (kThreads * 8);
   if (blocks > 65536) blocks = 65536;
   hipLaunchKernelGGL(decode_kernel, dim3((unsigned)blocks), dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream), q_m, q_w, numel,
-                     static_cast<const Slot *>(slots), slot, (int)(step & 1), eps, m_out, v_out);
+                     static_cast<const Slot *>(slot), eps, m_out, v_out);
   return check_launch("luma_decode: launch");
 }
 
 int luma_quantize(const float *m, const float *v, int64_t numel, int16_t *q_m, int16_t *q_w,
-                  void *slots, int32_t slot, int64_t step, double eps, uint64_t seed,
-                  int32_t noise_mode, const float *u_m, const float *u_w, float *partials,
-                  void *stream) {
+                  void *slot, int64_t step, double eps, uint64_t seed, int32_t noise_mode,
+                  const float *u_m, const float *u_w, float *partials, void *stream) {
   if (numel <= 0) return 0;
-  if (!m || !v || !q_m || !q_w || !slots || !partials) return fail("luma_quantize: null pointer");
+  if (!m || !v || !q_m || !q_w || !slot || !partials) return fail("luma_quantize: null pointer");
   if (noise_mode == LUMA_NOISE_INJECTED && (!u_m || !u_w))
     return fail("luma_quantize: injected noise needs u_m and u_w");
   if (noise_mode != LUMA_NOISE_PHILOX && noise_mode != LUMA_NOISE_INJECTED)
@@ -1113,17 +1197,26 @@ int luma_quantize(const float *m, const float *v, int64_t numel, int16_t *q_m, i
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t nch = (numel + kChunk - 1) / kChunk;
   if (nch > 0x7fffffff) return fail("luma_quantize: tensor too large");
-  Slot *S = static_cast<Slot *>(slots);
+  Slot *S = static_cast<Slot *>(slot);
   const int par = (int)(step & 1);
   hipLaunchKernelGGL(quant_max_kernel, dim3((unsigned)nch), dim3(kThreads), 0, s, m, v, numel,
                      partials);
   if (int r = check_launch("luma_quantize: max launch")) return r;
-  hipLaunchKernelGGL(quant_finalize_kernel, dim3(1), dim3(64), 0, s, partials, (int)nch, S, slot,
-                     par, eps);
+  hipLaunchKernelGGL(quant_finalize_kernel, dim3(1), dim3(64), 0, s, partials, (int)nch, S, step,
+                     eps);
   if (int r = check_launch("luma_quantize: finalize launch")) return r;
   hipLaunchKernelGGL(quant_kernel, dim3((unsigned)nch), dim3(kThreads), 0, s, m, v, numel, q_m, q_w,
-                     S, slot, par, eps, seed, noise_mode, u_m, u_w);
+                     (const Slot *)S, par, eps, seed, noise_mode, u_m, u_w);
   return check_launch("luma_quantize: launch");
+}
+
+int luma_hyper_rows(const LumaGroup *group, int64_t t0, int32_t n, float *out, void *stream) {
+  if (n <= 0) return 0;
+  if (!group || !out) return fail("luma_hyper_rows: null pointer");
+  if (t0 < 1) return fail("luma_hyper_rows: steps start at 1");
+  hipLaunchKernelGGL(hyper_rows_kernel, dim3((n + 255) / 256), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), *group, t0, n, out);
+  return check_launch("luma_hyper_rows: launch");
 }
 
 void luma_philox4x32(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]) {

@@ -5,10 +5,17 @@ Same public surface as the reference (src/luma_optimizer/optimizer.py:39-524):
 ``state_dict()`` / ``load_state_dict()``, ``export_adamw_state()``,
 ``import_adamw_state()`` and ``_base_seed``.  Per parameter the state holds
 ``step``, ``param_id``, ``Q_m`` and ``Q_w`` (int16, the parameter's shape);
-``S_m`` / ``S_v`` live in device scale slots and appear in ``state_dict()``.
+the step count, ``S_m`` and ``S_v`` live on the device in the parameter's
+slot (a private 512-byte buffer, the counterpart of the reference's
+``_step_tensor`` / ``_new_grid``, optimizer.py:341-387) and appear in
+``state_dict()``.
 
 One ``step()`` is one multi-tensor launch sequence on the current stream
-(luma_step in include/luma.h) with no host synchronisation.  The stochastic
+(luma_step in include/luma.h) with no host synchronisation.  Every per-step
+quantity is derived on the device, so ``step()`` can be captured into a CUDA
+(HIP) graph after one eager step and replayed: each replay is one more step.
+``state[p]["step"]`` counts eager calls; ``state_dict()`` and
+``export_adamw_state()`` read the device counts (and refresh it).  The stochastic
 rounding draws come from Philox4x32-10 keyed by the reference's per-step seed
 ``((t << 32) | 2*param_id) ^ _base_seed`` (functional.py:99-106), or from
 uniforms injected with ``inject_noise`` (used to compare against the
@@ -46,32 +53,25 @@ def _ptr(t: Optional[torch.Tensor]) -> int:
 
 
 class _Engine:
-    """Device-side tables of one optimizer: scale slots, chunk plan, uploads."""
+    """Device-side tables of one optimizer: tensor, chunk and group tables and
+    the chunk-maxima workspace.  Tables are uploaded only when their contents
+    change, so a step whose parameters, gradients and hyper-parameters are
+    those of the previous step launches with no host-to-device copy (and may
+    be captured into a CUDA/HIP graph)."""
 
     def __init__(self, device: torch.device):
         self.lib = L.load()
         self.device = device
-        self.n_slots = 0
-        self.slots = torch.zeros(64 * L.SLOT_BYTES, dtype=torch.uint8, device=device)
-        self._plan_key = None
-        self._chunks = None
-        self._first_chunk = None
+        self._tensor_key = None      # bytes of the uploaded tensor table
+        self._d_tensors = None
+        self._d_chunks = None
+        self._n_chunks = 0
+        self._group_key = None
+        self._d_groups = None
         self._partials = None
+        self._captured = []          # tables that a captured graph may read
         # torch.cuda.Event x4 (already recorded once) -> per-kernel timing
         self.profile_events = None
-
-    # -- slots --------------------------------------------------------------
-    def reset_slots(self):
-        self.n_slots = 0
-
-    def new_slot(self) -> int:
-        cap = self.slots.numel() // L.SLOT_BYTES
-        if self.n_slots >= cap:
-            grown = torch.zeros(2 * cap * L.SLOT_BYTES, dtype=torch.uint8, device=self.device)
-            grown[: self.slots.numel()].copy_(self.slots)
-            self.slots = grown
-        self.n_slots += 1
-        return self.n_slots - 1
 
     # -- helpers ------------------------------------------------------------
     def _stream(self) -> int:
@@ -81,57 +81,73 @@ class _Engine:
         host = torch.from_numpy(arr.view(np.uint8).reshape(-1)).pin_memory()
         return host.to(self.device, non_blocking=True)
 
-    def workspace(self, n_chunks: int) -> torch.Tensor:
-        need = max(2 * n_chunks, 2)
-        if self._partials is None or self._partials.numel() < need:
-            self._partials = torch.empty(need, dtype=torch.float32, device=self.device)
-        return self._partials
+    def new_slots(self, n: int):
+        """n zero-filled slots (step count 0) as views of one allocation."""
+        block = torch.zeros((n, L.SLOT_BYTES), dtype=torch.uint8, device=self.device)
+        return list(block.unbind(0))
 
-    def _plan(self, numels: Tuple[int, ...]):
-        if numels != self._plan_key:
-            nch = (np.asarray(numels, dtype=np.int64) + L.CHUNK_ELEMS - 1) // L.CHUNK_ELEMS
-            total = int(nch.sum())
-            if total >= 2**31:
-                raise ValueError("LUMA: too many chunks for one launch")
-            first = np.zeros(len(numels), dtype=np.int64)
-            np.cumsum(nch[:-1], out=first[1:])
-            ch = np.empty(total, dtype=L.CHUNK_DTYPE)
-            ch["tensor"] = np.repeat(np.arange(len(numels), dtype=np.int32), nch)
-            ch["index"] = np.arange(total, dtype=np.int64) - np.repeat(first, nch)
-            self._chunks = self._upload(ch)
-            self._first_chunk = first.astype(np.int32)
-            self._n_chunks = total
-            self._plan_key = numels
-        return self._chunks, self._first_chunk, self._n_chunks
+    @staticmethod
+    def _capture_error(what: str) -> RuntimeError:
+        return RuntimeError(
+            f"LUMA.step() under graph capture: {what} changed since the last eager step(). "
+            "Run one eager step() with the same parameters, gradient tensors and "
+            "hyper-parameters before capturing.")
 
     # -- entry points -------------------------------------------------------
-    def step(self, rows, hypers: np.ndarray, base_seed: int, noise_mode: int, flags: int = 0):
-        """rows: list of (param, grad, q_m, q_w, u_m, u_w, step, param_id, grad_code,
-        hyper_idx, slot)."""
+    def step(self, rows, groups: np.ndarray, base_seed: int, noise_mode: int, flags: int = 0):
+        """rows: list of (param, grad, q_m, q_w, u_m, u_w, slot, param_id, grad_code, group)."""
+        capturing = torch.cuda.is_current_stream_capturing()
         n = len(rows)
-        numels = tuple(r[0].numel() for r in rows)
-        chunks, first, n_chunks = self._plan(numels)
-        tt = np.empty(n, dtype=L.TENSOR_DTYPE)
+        numels = np.fromiter((r[0].numel() for r in rows), dtype=np.int64, count=n)
+        nch = (numels + L.CHUNK_ELEMS - 1) // L.CHUNK_ELEMS
+        first = np.zeros(n, dtype=np.int64)
+        np.cumsum(nch[:-1], out=first[1:])
+        n_chunks = int(nch.sum())
+        if n_chunks >= 2**31:
+            raise ValueError("LUMA: too many chunks for one launch")
+        tt = np.zeros(n, dtype=L.TENSOR_DTYPE)
         tt["param"] = [r[0].data_ptr() for r in rows]
         tt["grad"] = [r[1].data_ptr() for r in rows]
         tt["q_m"] = [r[2].data_ptr() for r in rows]
         tt["q_w"] = [r[3].data_ptr() for r in rows]
         tt["u_m"] = [_ptr(r[4]) for r in rows]
         tt["u_w"] = [_ptr(r[5]) for r in rows]
+        tt["slot"] = [r[6].data_ptr() for r in rows]
         tt["numel"] = numels
-        tt["step"] = [r[6] for r in rows]
         tt["param_id"] = [r[7] for r in rows]
         tt["grad_dtype"] = [r[8] for r in rows]
-        tt["hyper"] = [r[9] for r in rows]
-        tt["slot"] = [r[10] for r in rows]
+        tt["group"] = [r[9] for r in rows]
         tt["first_chunk"] = first
-        d_tensors = self._upload(tt)
-        d_hypers = self._upload(hypers)
-        partials = self.workspace(n_chunks)
+        key = tt.tobytes()
+        if key != self._tensor_key:
+            if capturing:
+                raise self._capture_error("the parameter or gradient set")
+            ch = np.empty(n_chunks, dtype=L.CHUNK_DTYPE)
+            ch["tensor"] = np.repeat(np.arange(n, dtype=np.int32), nch)
+            ch["index"] = np.arange(n_chunks, dtype=np.int64) - np.repeat(first, nch)
+            self._d_chunks = self._upload(ch)
+            self._d_tensors = self._upload(tt)
+            self._n_chunks = n_chunks
+            self._tensor_key = key
+        gkey = groups.tobytes()
+        if gkey != self._group_key:
+            if capturing:
+                raise self._capture_error("a param group's hyper-parameters")
+            self._d_groups = self._upload(groups)
+            self._group_key = gkey
+        need = max(2 * n_chunks, 2)
+        if self._partials is None or self._partials.numel() < need:
+            if capturing:
+                raise self._capture_error("the chunk count")
+            self._partials = torch.empty(need, dtype=torch.float32, device=self.device)
+        if capturing:
+            tables = (self._d_tensors, self._d_chunks, self._d_groups, self._partials)
+            if not self._captured or any(x is not y for x, y in zip(self._captured[-1], tables)):
+                self._captured.append(tables)
         args = L.StepArgs(
-            tensors=d_tensors.data_ptr(), n_tensors=n, n_chunks=n_chunks,
-            chunks=chunks.data_ptr(), hypers=d_hypers.data_ptr(),
-            slots=self.slots.data_ptr(), partials=partials.data_ptr(),
+            tensors=self._d_tensors.data_ptr(), n_tensors=n, n_chunks=n_chunks,
+            chunks=self._d_chunks.data_ptr(), groups=self._d_groups.data_ptr(),
+            partials=self._partials.data_ptr(),
             base_seed=base_seed & _MASK64, noise_mode=noise_mode, flags=flags)
         if self.profile_events is None:
             L.check(self.lib.luma_step(ctypes.byref(args), self._stream()), "luma_step")
@@ -141,44 +157,42 @@ class _Engine:
                     "luma_step_profiled")
 
     def set_scales(self, items):
-        """items: list of (slot, step, S_m, S_v, eps)."""
+        """items: list of (slot tensor, step, S_m, S_v, eps)."""
         arr = np.zeros(len(items), dtype=L.SCALE_INIT_DTYPE)
-        arr["slot"] = [i[0] for i in items]
+        arr["slot"] = [i[0].data_ptr() for i in items]
         arr["step"] = [i[1] for i in items]
         arr["s_m"] = [i[2] for i in items]
         arr["s_v"] = [i[3] for i in items]
         arr["eps"] = [i[4] for i in items]
         d = self._upload(arr)
-        L.check(self.lib.luma_set_scales(self.slots.data_ptr(), d.data_ptr(), len(items),
-                                         self._stream()), "luma_set_scales")
+        L.check(self.lib.luma_set_scales(d.data_ptr(), len(items), self._stream()),
+                "luma_set_scales")
 
-    def get_scales(self, slots, steps):
-        """Returns a list of (S_m, S_v) Python floats (synchronises)."""
+    def get_scales(self, slots):
+        """Returns a list of (step, S_m, S_v) as Python numbers (synchronises)."""
         n = len(slots)
-        d_idx = self._upload(np.asarray(slots, dtype=np.int32))
-        d_steps = self._upload(np.asarray(steps, dtype=np.int64))
-        out = torch.empty(2 * n, dtype=torch.float64, device=self.device)
-        L.check(self.lib.luma_get_scales(self.slots.data_ptr(), d_idx.data_ptr(),
-                                         d_steps.data_ptr(), n, out.data_ptr(), self._stream()),
-                "luma_get_scales")
-        vals = out.cpu().tolist()
-        return [(vals[2 * i], vals[2 * i + 1]) for i in range(n)]
+        d_ptrs = self._upload(np.asarray([s.data_ptr() for s in slots], dtype=np.uint64))
+        scales = torch.empty(2 * n, dtype=torch.float64, device=self.device)
+        steps = torch.empty(n, dtype=torch.int64, device=self.device)
+        L.check(self.lib.luma_get_scales(d_ptrs.data_ptr(), n, scales.data_ptr(),
+                                         steps.data_ptr(), self._stream()), "luma_get_scales")
+        sc = scales.cpu().tolist()
+        st = steps.cpu().tolist()
+        return [(st[i], sc[2 * i], sc[2 * i + 1]) for i in range(n)]
 
-    def decode(self, q_m, q_w, slot, step, eps, m_out, v_out):
+    def decode(self, q_m, q_w, slot, eps, m_out, v_out):
         L.check(self.lib.luma_decode(q_m.data_ptr(), q_w.data_ptr(), q_m.numel(),
-                                     self.slots.data_ptr(), slot, step, float(eps),
-                                     m_out.data_ptr(), v_out.data_ptr(), self._stream()),
-                "luma_decode")
+                                     slot.data_ptr(), float(eps), m_out.data_ptr(),
+                                     v_out.data_ptr(), self._stream()), "luma_decode")
 
     def quantize(self, m, v, q_m, q_w, slot, step, eps, seed, noise_mode, u_m, u_w):
         n = m.numel()
         nch = (n + L.CHUNK_ELEMS - 1) // L.CHUNK_ELEMS
         ws = torch.empty(max(2 * nch, 2), dtype=torch.float32, device=self.device)
         L.check(self.lib.luma_quantize(m.data_ptr(), v.data_ptr(), n, q_m.data_ptr(),
-                                       q_w.data_ptr(), self.slots.data_ptr(), slot, step,
-                                       float(eps), seed & _MASK64, noise_mode, _ptr(u_m),
-                                       _ptr(u_w), ws.data_ptr(), self._stream()),
-                "luma_quantize")
+                                       q_w.data_ptr(), slot.data_ptr(), step, float(eps),
+                                       seed & _MASK64, noise_mode, _ptr(u_m), _ptr(u_w),
+                                       ws.data_ptr(), self._stream()), "luma_quantize")
 
 
 class LUMA(Optimizer):
@@ -263,32 +277,38 @@ class LUMA(Optimizer):
             out.append(u)
         return out[0], out[1]
 
-    @staticmethod
-    def _hyper_row(group, t: int):
-        b1, b2 = group["betas"]
-        lr, wd, eps = group["lr"], group["weight_decay"], group["eps"]
-        bc1 = 1.0 - b1 ** t       # functional.py:209,262 (1 - b1 at t = 1)
-        bc2 = 1.0 - b2 ** t
-        eta = lr / bc1
-        return (b1, 1.0 - b1, b2, 1.0 - b2, 1.0 - wd * lr, -eta, bc2, eps, eps)
+    def _group_table(self) -> np.ndarray:
+        """Hyper-parameters of every param group as the Python doubles the
+        reference computes with (optimizer.py:80-92); the device derives the
+        per-step scalars from them."""
+        arr = np.zeros(len(self.param_groups), dtype=L.GROUP_DTYPE)
+        for i, g in enumerate(self.param_groups):
+            b1, b2 = g["betas"]
+            arr[i] = (float(g["lr"]), float(b1), float(b2), float(g["eps"]),
+                      float(g["weight_decay"]), 0.0)
+        return arr
 
     # ------------------------------------------------------------------
     #  Checkpoint: portable save / load  (optimizer.py:119-183)
     # ------------------------------------------------------------------
+    def _read_slots(self, states):
+        """Device step counts and scales of the given states (one sync); also
+        refreshes each state's host ``step``."""
+        vals = self._engine.get_scales([s["_slot"] for s in states])
+        for s, (step, _, _) in zip(states, vals):
+            s["step"] = step
+        return vals
+
     def state_dict(self) -> dict:
         raw = super().state_dict()
-        keys, slots, steps = [], [], []
-        for idx, s in raw["state"].items():
-            if "_slot" in s:
-                keys.append(idx)
-                slots.append(s["_slot"])
-                steps.append(s["step"])
+        keys = [idx for idx, s in raw["state"].items() if "_slot" in s]
+        vals = self._read_slots([raw["state"][k] for k in keys]) if keys else []
         clean = {idx: {k: v for k, v in s.items() if not k.startswith("_")}
                  for idx, s in raw["state"].items()}
-        if keys:
-            for idx, (sm, sv) in zip(keys, self._engine.get_scales(slots, steps)):
-                clean[idx]["S_m"] = sm
-                clean[idx]["S_v"] = sv
+        for idx, (step, sm, sv) in zip(keys, vals):
+            clean[idx]["step"] = step
+            clean[idx]["S_m"] = sm
+            clean[idx]["S_v"] = sv
         raw["state"] = clean
         raw["_base_seed"] = self._base_seed
         return raw
@@ -320,12 +340,12 @@ class LUMA(Optimizer):
         if not pending:
             return
         engine = self._get_engine(pending[0][1].device)
-        engine.reset_slots()
         items = []
-        for _, param, state, eps in pending:
+        for (_, param, state, eps), slot in zip(pending, engine.new_slots(len(pending))):
             self._get_engine(param.device)
-            state["_slot"] = engine.new_slot()
-            items.append((state["_slot"], state["step"], float(state.pop("S_m")),
+            state["_slot"] = slot
+            state["step"] = int(state["step"])
+            items.append((slot, state["step"], float(state.pop("S_m")),
                           float(state.pop("S_v")), eps))
         engine.set_scales(items)
 
@@ -338,6 +358,10 @@ class LUMA(Optimizer):
             for p in group["params"]:
                 param_to_idx[id(p)] = len(param_to_idx)
         adamw_state: dict = {}
+        live = [self.state[p] for g in self.param_groups for p in g["params"]
+                if "_slot" in self.state[p]]
+        if live:
+            self._read_slots(live)
         for group in self.param_groups:
             eps = group["eps"]
             for p in group["params"]:
@@ -348,7 +372,7 @@ class LUMA(Optimizer):
                 engine = self._get_engine(param.device)
                 exp_avg = torch.empty_like(param, dtype=torch.float32)
                 exp_avg_sq = torch.empty_like(param, dtype=torch.float32)
-                engine.decode(state["Q_m"], state["Q_w"], state["_slot"], state["step"], eps,
+                engine.decode(state["Q_m"], state["Q_w"], state["_slot"], eps,
                               exp_avg, exp_avg_sq)
                 adamw_state[param_to_idx[id(p)]] = {
                     "step": torch.tensor(float(state["step"])),
@@ -386,7 +410,7 @@ class LUMA(Optimizer):
             q_m = torch.empty_like(param, dtype=torch.int16)
             q_w = torch.empty_like(param, dtype=torch.int16)
             state = self.state[p]
-            slot = state["_slot"] if "_slot" in state else engine.new_slot()
+            slot = state["_slot"] if "_slot" in state else engine.new_slots(1)[0]
             u_m, u_w = self._take_noise(p, param)
             seed = make_step_seed(self._base_seed, 0, idx)   # optimizer.py:315-317
             engine.quantize(m, v, q_m, q_w, slot, step, group["eps"], seed, noise_mode, u_m, u_w)
@@ -400,6 +424,9 @@ class LUMA(Optimizer):
     # ------------------------------------------------------------------
     #  Main entry point  (optimizer.py:413-524)
     # ------------------------------------------------------------------
+    # Not traced by dynamo: under torch.compile the call is a graph break and
+    # runs as is (table bookkeeping in Python, then three kernel launches).
+    @torch.compiler.disable
     @torch.no_grad()
     def step(self, closure=None):
         loss = None
@@ -437,22 +464,24 @@ class LUMA(Optimizer):
 
         engine = self._get_engine(work[0][2].device)
         noise_mode = L.NOISE_INJECTED if self._noise is not None else L.NOISE_PHILOX
-        hyper_index: Dict[Tuple[int, int], int] = {}
-        hyper_rows = []
-        rows = []
+        capturing = torch.cuda.is_current_stream_capturing()
+        fresh = [self.state[w[1]] for w in work if "_slot" not in self.state[w[1]]]
+        if fresh:
+            if capturing:
+                raise engine._capture_error("the set of parameters with optimizer state")
+            for state, slot in zip(fresh, engine.new_slots(len(fresh))):
+                state["_slot"] = slot
+        rows, states = [], []
         for gi, p, param, grad, pidx in work:
-            engine_dev = self._get_engine(param.device)  # noqa: F841  (one device)
+            self._get_engine(param.device)   # one device for all parameters
             state = self.state[p]
-            if len(state) == 0:
+            if "step" not in state:
                 state["step"] = 0
                 state["param_id"] = pidx
-            state["step"] += 1
-            t = state["step"]
-            if t == 1 or "Q_m" not in state:
+            states.append(state)
+            if "Q_m" not in state:
                 state["Q_m"] = torch.empty_like(param, dtype=torch.int16)
                 state["Q_w"] = torch.empty_like(param, dtype=torch.int16)
-            if "_slot" not in state:
-                state["_slot"] = engine.new_slot()
             code = _GRAD_CODES.get(grad.dtype)
             if code is None:
                 grad = grad.float()
@@ -461,17 +490,12 @@ class LUMA(Optimizer):
                 grad = grad.to(param.device)
             if grad.stride() != param.stride() or not _is_dense(grad):
                 grad = torch.empty_like(param, dtype=grad.dtype).copy_(grad)
-            key = (gi, t)
-            if key not in hyper_index:
-                hyper_index[key] = len(hyper_rows)
-                hyper_rows.append(self._hyper_row(self.param_groups[gi], t))
             u_m, u_w = self._take_noise(p, param)
-            rows.append((param, grad, state["Q_m"], state["Q_w"], u_m, u_w, t,
-                         state["param_id"], code, hyper_index[key], state["_slot"]))
-        hypers = np.array(hyper_rows, dtype=np.float64)
-        harr = np.empty(len(hyper_rows), dtype=L.HYPER_DTYPE)
-        for j, name in enumerate(L.HYPER_DTYPE.names):
-            harr[name] = hypers[:, j]
-        engine.step(rows, harr, self._base_seed, noise_mode, self._flags)
+            rows.append((param, grad, state["Q_m"], state["Q_w"], u_m, u_w, state["_slot"],
+                         state["param_id"], code, gi))
+        engine.step(rows, self._group_table(), self._base_seed, noise_mode, self._flags)
+        # host count of step() calls; the kernels use the slot's device count
+        for state in states:
+            state["step"] += 1
         self._noise = None
         return loss

@@ -137,16 +137,6 @@ def test_sparse_grad_rejected():
         opt.step()
 
 
-def test_hyper_row_matches_reference_scalars():
-    """Coefficients are the reference's double expressions (functional.py:209-214,262-279)."""
-    g = {"betas": (0.9, 0.999), "lr": 1e-3, "weight_decay": 0.01, "eps": 1e-8}
-    row = LUMA._hyper_row(g, 7)
-    assert row == (0.9, 1.0 - 0.9, 0.999, 1.0 - 0.999, 1.0 - 0.01 * 1e-3,
-                   -(1e-3 / (1.0 - 0.9 ** 7)), 1.0 - 0.999 ** 7, 1e-8, 1e-8)
-    row1 = LUMA._hyper_row(g, 1)
-    assert row1[5] == -(1e-3 / (1.0 - 0.9)) and row1[6] == 1.0 - 0.999
-
-
 def test_package_exports():
     assert luma_amd.__all__ == ["LUMA", "get_kernel_config"]
     assert "CHUNK_ELEMS" in luma_amd.get_kernel_config()
