@@ -229,6 +229,61 @@ def traffic_report(config, kernel, fetch_csv, write_csv, copy_fetch_csv, copy_wr
     print("\n".join(lines))
 
 
+def stats_report(config, trace_csv, bench_json, out):
+    """Write the kernel-time summary of a `rocprofv3 --kernel-trace --stats` run of
+    bench.py: per LUMA kernel, the average over every launch and over the
+    steady-state launches (all but the first, the init step), next to the
+    bench's own HIP-event averages from the same run."""
+    import csv
+    durs = {}
+    with open(trace_csv) as f:
+        rows = list(csv.DictReader(f))
+    for r in sorted(rows, key=lambda r: int(r["Start_Timestamp"])):
+        name = r["Kernel_Name"]
+        if name.startswith("luma::"):
+            key = name.split("(")[0]
+            durs.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e6)
+    total = sum((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e6 for r in rows)
+    bench = None
+    with open(bench_json) as f:
+        for line in f:
+            if line.startswith("{"):
+                bench = json.loads(line)
+    cfg = CONFIGS[config]
+    n_params = sum(math.prod(s) for s in cfg["shapes"]())
+    lines = [
+        f"# Kernel time of the LUMA step on {config} ({n_params} params, {len(cfg['shapes']())} tensors, "
+        f"{str(cfg['grad']).replace('torch.', '')} grads)",
+        "",
+        "Commands (MI355X, one GPU):",
+        f"    rocprofv3 --kernel-trace --stats --output-format csv -d <dir> -o kt -- python bench.py --config {config} "
+        f"--steps {bench['steps']} --warmup {bench['warmup']} --no-cpu > <bench.json>",
+        f"    python bench.py --stats-report {config} <dir>/.../kt_kernel_trace.csv <bench.json> <out.md>",
+        "",
+        f"{bench['warmup'] + bench['steps']} launches of each kernel: {bench['warmup']} warm-up + "
+        f"{bench['steps']} timed steps; the first is the init step (t = 1).",
+        "",
+        "| kernel | launches | avg ms (all) | avg ms (t >= 2) | min ms | max ms | % of GPU time | bench HIP events ms |",
+        "|---|---|---|---|---|---|---|---|",
+    ]
+    ev = {"luma::pass1_fast_kernel": "luma_pass1", "luma::finalize_kernel": "luma_finalize",
+          "luma::pass2_fast_kernel": "luma_pass2"}
+    for key in sorted(durs, key=lambda k: -sum(durs[k])):
+        d = durs[key]
+        ss = d[1:] or d
+        bev = bench["kernel_ms"].get(ev.get(key, ""), None)
+        lines.append(f"| `{key}` | {len(d)} | {sum(d) / len(d):.3f} | {sum(ss) / len(ss):.3f} | "
+                     f"{min(d):.3f} | {max(d):.3f} | {100 * sum(d) / total:.2f} | "
+                     f"{'' if bev is None else f'{bev:.3f}'} |")
+    lines += ["",
+              f"Step time in the same run (bench wall clock): {bench['ms_per_step']:.3f} ms; "
+              f"{bench['value']} Gparams/s.",
+              "Kernels not listed are torch's synthetic-data set-up outside the timed region."]
+    with open(out, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def read_traffic(config, kernel):
     path = os.path.join(TRAFFIC_DIR, f"{kernel.replace('::', '_')}_{config}_traffic.md")
     try:
@@ -256,9 +311,14 @@ def main():
                     metavar=("CONFIG", "KERNEL", "FETCH_CSV", "WRITE_CSV", "COPY_FETCH_CSV",
                              "COPY_WRITE_CSV", "OUT"),
                     help="summarise rocprofv3 FETCH_SIZE/WRITE_SIZE runs into OUT")
+    ap.add_argument("--stats-report", nargs=4, metavar=("CONFIG", "TRACE_CSV", "BENCH_JSON", "OUT"),
+                    help="summarise a rocprofv3 --kernel-trace --stats run of bench.py into OUT")
     args = ap.parse_args()
     if args.traffic_report:
         traffic_report(*args.traffic_report)
+        return
+    if args.stats_report:
+        stats_report(*args.stats_report)
         return
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
