@@ -368,12 +368,14 @@ __device__ __noinline__ int exact_code_w(int qw, float g, const LUMA_GLOBAL Grid
 }
 
 // Per-wave queues of elements whose fast result is not certified.  Elements
-// are appended with ballot/mbcnt (no atomics) and run through the exact path
+// are appended without atomics (pass 1: ballot/mbcnt per element slot;
+// pass 2: one wave prefix sum per iteration) and run through the exact path
 // 64 at a time, one per lane, so the exact path runs at full SIMD width.
-// Pass 1 appends up to 8 x 64 entries before it drains its queue; pass 2
-// drains after every 64 appended, so its queues never exceed 127 entries.
+// Pass 1 appends up to 8 x 64 entries before it drains its queue.  Pass 2
+// drains below 64 after every iteration and appends at most 192 in one
+// (more is handled in place), so its queues never exceed 255 entries.
 constexpr int kQueueCap = kVec * 64 + 64;
-constexpr int kQueueCap2 = 128;
+constexpr int kQueueCap2 = 256;
 
 // Keeps a wave-uniform value in a VGPR.  On gfx950 a VALU instruction with
 // an SGPR source operand issues at about half the rate of one whose sources
@@ -570,6 +572,32 @@ __global__ __launch_bounds__(kThreads) void pass1_fast_kernel(StepSrc src,
     partials[2 * (int64_t)blockIdx.x] = exm;
     partials[2 * (int64_t)blockIdx.x + 1] = exv;
   }
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave (all lanes active): three
+// row shifts of the original value, shifts by 4 and 8 within rows, then
+// broadcasts of lanes 15 and 31 into the rows above (the GCN DPP scan).
+__device__ __forceinline__ uint32_t wave_scan_incl(uint32_t x) {
+  const int x0 = (int)x;
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, x0, 0x111, 0xf, 0xf, true);       // row_shr:1
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, x0, 0x112, 0xf, 0xf, true);       // row_shr:2
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, x0, 0x113, 0xf, 0xf, true);       // row_shr:3
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xf, 0xe, true);   // row_shr:4, lanes 4-15
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xf, 0xc, true);   // row_shr:8, lanes 8-15
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xa, 0xf, false);  // row_bcast:15, rows 1, 3
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xc, 0xf, false);  // row_bcast:31, rows 2, 3
+  return x;
+}
+
+// a[k] for a per-lane index k in 0..7, as a select tree (no indexed
+// register access).
+template <typename T>
+__device__ __forceinline__ T sel8(const T (&a)[kVec], uint32_t k) {
+  const bool b0 = (k & 1u) != 0, b1 = (k & 2u) != 0, b2 = (k & 4u) != 0;
+  const T x01 = b0 ? a[1] : a[0], x23 = b0 ? a[3] : a[2];
+  const T x45 = b0 ? a[5] : a[4], x67 = b0 ? a[7] : a[6];
+  const T y03 = b1 ? x23 : x01, y47 = b1 ? x67 : x45;
+  return b2 ? y47 : y03;
 }
 
 // Certified LogSR decision (see luma_fast.h): with z = y + 1 - c, c the
@@ -830,33 +858,58 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
       flags = p2_iter<GD, INJ, SMALL, false>(T, C, e0, n, k0, k1, Q, coarse);
     if (!__ballot(flags != 0)) continue;
     const uint32_t off0 = (uint32_t)(e0 - beg);
-#pragma unroll
-    for (int j = 0; j < kVec; ++j) {
-      const uint32_t bytes = INJ ? 0u : u4_word(coarse, j >> 1) >> (16 * (j & 1));
-      const bool fm = (flags >> j) & 1u;
-      const uint64_t bm = __ballot(fm);
-      if (fm)
-        queue_m[queue_pos(bm, qlen_m)] = make_uint4((off0 + j) | ((uint32_t)Q.qm[j] << 16),
-                                                    bytes & 0xFFu, __float_as_uint(Q.g[j]), 0u);
-      qlen_m += (uint32_t)__popcll(bm);
-      const bool fw = (flags >> (8 + j)) & 1u;
-      const uint64_t bw = __ballot(fw);
-      if (fw)
-        queue_w[queue_pos(bw, qlen_w)] = make_uint4((off0 + j) | ((uint32_t)Q.qw[j] << 16),
-                                                    (bytes >> 8) & 0xFFu, __float_as_uint(Q.g[j]),
-                                                    0u);
-      qlen_w += (uint32_t)__popcll(bw);
-      if (qlen_m >= 64 || qlen_w >= 64) {
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        if (qlen_m >= 64) {
-          qlen_m -= 64;
-          run_m(queue_m[qlen_m + lane]);
-        }
-        if (qlen_w >= 64) {
-          qlen_w -= 64;
-          run_w(queue_w[qlen_w + lane]);
-        }
+    // queue positions: a wave prefix sum of (momentum count | preconditioner
+    // count << 16) gives each lane its first slot in both queues
+    const uint32_t fm = flags & 0xFFu, fw = flags >> 8;
+    const uint32_t cnt = (uint32_t)__builtin_popcount(fm) | ((uint32_t)__builtin_popcount(fw) << 16);
+    const uint32_t incl = wave_scan_incl(cnt);
+    const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+    const uint32_t excl = incl - cnt;
+    const uint32_t tot_m = tot & 0xFFFFu, tot_w = tot >> 16;
+    // queue entry of code k (element off0 + k): its top uniform byte is byte
+    // 2k (momentum) or 2k + 1 (preconditioner) of the coarse block, in word k/2
+    auto entry = [&](uint32_t k, int code, uint32_t byte_shift) {
+      const uint32_t w01 = (k & 2u) ? coarse.y : coarse.x, w23 = (k & 2u) ? coarse.w : coarse.z;
+      const uint32_t wd = (k & 4u) ? w23 : w01;
+      const uint32_t byte = INJ ? 0u : (wd >> (16u * (k & 1u) + byte_shift)) & 0xFFu;
+      return make_uint4((off0 + k) | ((uint32_t)code << 16), byte, __float_as_uint(sel8(Q.g, k)),
+                        0u);
+    };
+    if (qlen_m + tot_m <= (uint32_t)kQueueCap2) {
+      uint32_t pos = qlen_m + (excl & 0xFFFFu);
+      for (uint32_t f = fm; f != 0u; f &= f - 1u) {
+        const uint32_t k = (uint32_t)__builtin_ctz(f);
+        queue_m[pos++] = entry(k, sel8(Q.qm, k), 0u);
       }
+      qlen_m += tot_m;
+    } else {
+      // more than the queue holds (only when most codes are uncertain): in place
+      for (uint32_t f = fm; f != 0u; f &= f - 1u) {
+        const uint32_t k = (uint32_t)__builtin_ctz(f);
+        run_m(entry(k, sel8(Q.qm, k), 0u));
+      }
+    }
+    if (qlen_w + tot_w <= (uint32_t)kQueueCap2) {
+      uint32_t pos = qlen_w + (excl >> 16);
+      for (uint32_t f = fw; f != 0u; f &= f - 1u) {
+        const uint32_t k = (uint32_t)__builtin_ctz(f);
+        queue_w[pos++] = entry(k, sel8(Q.qw, k), 8u);
+      }
+      qlen_w += tot_w;
+    } else {
+      for (uint32_t f = fw; f != 0u; f &= f - 1u) {
+        const uint32_t k = (uint32_t)__builtin_ctz(f);
+        run_w(entry(k, sel8(Q.qw, k), 8u));
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    while (qlen_m >= 64) {
+      qlen_m -= 64;
+      run_m(queue_m[qlen_m + lane]);
+    }
+    while (qlen_w >= 64) {
+      qlen_w -= 64;
+      run_w(queue_w[qlen_w + lane]);
     }
   }
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");

@@ -25,6 +25,7 @@ reference's own draws).
 from __future__ import annotations
 
 import ctypes
+import operator
 from typing import Dict, Optional, Tuple
 
 import numpy as np
@@ -63,6 +64,7 @@ class _Engine:
         self.lib = L.load()
         self.device = device
         self._tensor_key = None      # bytes of the uploaded tensor table
+        self._numel_key = None       # bytes of its numel column (chunk table)
         self._d_tensors = None
         self._d_chunks = None
         self._n_chunks = 0
@@ -94,18 +96,18 @@ class _Engine:
             "hyper-parameters before capturing.")
 
     # -- entry points -------------------------------------------------------
-    def step(self, rows, groups: np.ndarray, base_seed: int, noise_mode: int, flags: int = 0):
-        """rows: list of (param, grad, q_m, q_w, u_m, u_w, slot, param_id, grad_code, group)."""
-        capturing = torch.cuda.is_current_stream_capturing()
+    @staticmethod
+    def table(rows) -> np.ndarray:
+        """Tensor table of rows: (param, grad, q_m, q_w, u_m, u_w, slot, param_id,
+        grad_code, group) per tensor, chunks numbered consecutively."""
         n = len(rows)
+        tt = np.zeros(n, dtype=L.TENSOR_DTYPE)
         numels = np.fromiter((r[0].numel() for r in rows), dtype=np.int64, count=n)
         nch = (numels + L.CHUNK_ELEMS - 1) // L.CHUNK_ELEMS
         first = np.zeros(n, dtype=np.int64)
         np.cumsum(nch[:-1], out=first[1:])
-        n_chunks = int(nch.sum())
-        if n_chunks >= 2**31:
+        if int(nch.sum()) >= 2**31:
             raise ValueError("LUMA: too many chunks for one launch")
-        tt = np.zeros(n, dtype=L.TENSOR_DTYPE)
         tt["param"] = [r[0].data_ptr() for r in rows]
         tt["grad"] = [r[1].data_ptr() for r in rows]
         tt["q_m"] = [r[2].data_ptr() for r in rows]
@@ -118,17 +120,33 @@ class _Engine:
         tt["grad_dtype"] = [r[8] for r in rows]
         tt["group"] = [r[9] for r in rows]
         tt["first_chunk"] = first
+        return tt
+
+    def launch(self, tt: np.ndarray, groups: np.ndarray, base_seed: int, noise_mode: int,
+               flags: int = 0):
+        """One step over the tensors of table tt (luma_step), uploading only the
+        tables whose contents changed since the previous launch."""
+        capturing = torch.cuda.is_current_stream_capturing()
+        n = len(tt)
         key = tt.tobytes()
         if key != self._tensor_key:
             if capturing:
                 raise self._capture_error("the parameter or gradient set")
-            ch = np.empty(n_chunks, dtype=L.CHUNK_DTYPE)
-            ch["tensor"] = np.repeat(np.arange(n, dtype=np.int32), nch)
-            ch["index"] = np.arange(n_chunks, dtype=np.int64) - np.repeat(first, nch)
-            self._d_chunks = self._upload(ch)
+            numels = tt["numel"]
+            nkey = numels.tobytes()
+            if nkey != self._numel_key:
+                nch = (numels + L.CHUNK_ELEMS - 1) // L.CHUNK_ELEMS
+                n_chunks = int(nch.sum())
+                ch = np.empty(n_chunks, dtype=L.CHUNK_DTYPE)
+                ch["tensor"] = np.repeat(np.arange(n, dtype=np.int32), nch)
+                ch["index"] = (np.arange(n_chunks, dtype=np.int64)
+                               - np.repeat(tt["first_chunk"].astype(np.int64), nch))
+                self._d_chunks = self._upload(ch)
+                self._n_chunks = n_chunks
+                self._numel_key = nkey
             self._d_tensors = self._upload(tt)
-            self._n_chunks = n_chunks
             self._tensor_key = key
+        n_chunks = self._n_chunks
         gkey = groups.tobytes()
         if gkey != self._group_key:
             if capturing:
@@ -195,6 +213,65 @@ class _Engine:
                                        ws.data_ptr(), self._stream()), "luma_quantize")
 
 
+class _Plan:
+    """The tensor table of the previous step, for re-use.
+
+    A step may re-use it when the parameter list is the same objects, the
+    same parameters have a gradient, and every gradient is a plain dense
+    tensor of the planned dtype, strides and device.  Then only the gradient
+    and parameter pointers are re-read (about 1 us per tensor, against the
+    full per-parameter bookkeeping), and nothing is uploaded unless they
+    moved.  Invalidated by load_state_dict, import_adamw_state and
+    add_param_group.
+    """
+
+    __slots__ = ("all_params", "has_grad", "work_idx", "params", "grads", "gdtypes", "strides",
+                 "device_index", "states", "tt")
+
+    def __init__(self, param_groups, work, rows, states, tt):
+        self.all_params = [p for g in param_groups for p in g["params"]]
+        self.has_grad = [p.grad is not None for p in self.all_params]
+        self.work_idx = [w[4] for w in work]
+        self.params = [r[0] for r in rows]
+        self.grads = [r[1] for r in rows]
+        self.gdtypes = [g.dtype for g in self.grads]
+        self.strides = [g.stride() for g in self.grads]
+        self.device_index = self.params[0].get_device()
+        self.states = states
+        self.tt = tt
+
+    @staticmethod
+    def usable(work, rows) -> bool:
+        """Whether the step just built from `work` can be re-used: every
+        gradient went in as the parameter's own .grad tensor (no dtype or
+        layout conversion, no DTensor unwrapping)."""
+        return all(type(w[1]) is torch.nn.Parameter or type(w[1]) is torch.Tensor
+                   for w in work) and all(
+            r[1] is w[1].grad and type(r[1]) is torch.Tensor for w, r in zip(work, rows))
+
+    def refresh(self, param_groups) -> bool:
+        flat = [p for g in param_groups for p in g["params"]]
+        if len(flat) != len(self.all_params) or not all(map(operator.is_, flat, self.all_params)):
+            return False
+        grads = [p.grad for p in flat]
+        if [g is not None for g in grads] != self.has_grad:
+            return False
+        wg = [grads[i] for i in self.work_idx]
+        dev = self.device_index
+        for i, (g, old) in enumerate(zip(wg, self.grads)):
+            if g is old:
+                continue
+            if (type(g) is not torch.Tensor or g.dtype is not self.gdtypes[i]
+                    or g.stride() != self.strides[i] or g.get_device() != dev):
+                return False
+        self.grads = wg
+        n = len(wg)
+        self.tt["grad"] = np.fromiter(map(torch.Tensor.data_ptr, wg), dtype=np.uint64, count=n)
+        self.tt["param"] = np.fromiter(map(torch.Tensor.data_ptr, self.params), dtype=np.uint64,
+                                       count=n)
+        return True
+
+
 class LUMA(Optimizer):
     r"""LUMA: Log-space Unbiased Momentum AdamW on the MI355X HIP backend.
 
@@ -233,6 +310,7 @@ class LUMA(Optimizer):
         self._engine: Optional[_Engine] = None
         self._noise: Optional[Dict[int, Tuple[torch.Tensor, torch.Tensor]]] = None
         self._flags = 0
+        self._plan: Optional[_Plan] = None
 
     # ------------------------------------------------------------------
     #  Helpers
@@ -313,7 +391,12 @@ class LUMA(Optimizer):
         raw["_base_seed"] = self._base_seed
         return raw
 
+    def add_param_group(self, param_group: dict) -> None:
+        self._plan = None
+        super().add_param_group(param_group)
+
     def load_state_dict(self, state_dict: dict) -> None:
+        self._plan = None
         self._base_seed = state_dict.get("_base_seed", self._base_seed)
         super().load_state_dict(state_dict)
         pending = []
@@ -387,6 +470,7 @@ class LUMA(Optimizer):
         return {"state": adamw_state, "param_groups": param_groups}
 
     def import_adamw_state(self, adamw_sd: dict) -> None:
+        self._plan = None
         all_params = []
         group_of = {}
         for group in self.param_groups:
@@ -433,6 +517,15 @@ class LUMA(Optimizer):
         if closure is not None:
             with torch.enable_grad():
                 loss = closure()
+
+        plan = self._plan
+        if plan is not None and self._noise is None and plan.refresh(self.param_groups):
+            self._engine.launch(plan.tt, self._group_table(), self._base_seed, L.NOISE_PHILOX,
+                                self._flags)
+            for state in plan.states:
+                state["step"] += 1
+            return loss
+        self._plan = None
 
         work = []
         param_idx = 0
@@ -493,9 +586,12 @@ class LUMA(Optimizer):
             u_m, u_w = self._take_noise(p, param)
             rows.append((param, grad, state["Q_m"], state["Q_w"], u_m, u_w, state["_slot"],
                          state["param_id"], code, gi))
-        engine.step(rows, self._group_table(), self._base_seed, noise_mode, self._flags)
+        tt = engine.table(rows)
+        engine.launch(tt, self._group_table(), self._base_seed, noise_mode, self._flags)
         # host count of step() calls; the kernels use the slot's device count
         for state in states:
             state["step"] += 1
+        if noise_mode == L.NOISE_PHILOX and _Plan.usable(work, rows):
+            self._plan = _Plan(self.param_groups, work, rows, states, tt)
         self._noise = None
         return loss
