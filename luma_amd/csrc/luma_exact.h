@@ -127,13 +127,41 @@ __device__ __forceinline__ float exact_log_sr(float y, float delta, float z, flo
   return clamp_t(q, 0.0f, kmax);
 }
 
+// LogSR up to its decision: the code is qhi when u < p, else qlo (the same
+// float32 operations as exact_log_sr, for callers that know u only to an
+// interval).
+__device__ __forceinline__ void exact_log_sr_pair(float y, float delta, float z, float kmax,
+                                                  float &p, float &qlo, float &qhi) {
+  const float k = floorf(y);
+  const float fr = y - k;
+  p = cr_expm1(fr * delta) / z;
+  qlo = clamp_t(k + 0.0f, 0.0f, kmax);
+  qhi = clamp_t(k + 1.0f, 0.0f, kmax);
+}
+
+// The momentum code's sign and int16 conversion (functional.py:146-150).
+__device__ __forceinline__ int signed_code_m(float mc, float q) {
+  const float s = mc > 0.0f ? q : (mc < 0.0f ? -q : (mc != mc ? mc : 0.0f));
+  return (int)s;
+}
+
 // Quantise m (functional.py:133-150).
 __device__ __forceinline__ int exact_quant_m(float mn, const Grid &g, float u) {
   const float mc = clamp_t(mn, -g.sm, g.sm);
   const float y = cr_log1p(fabsf(mc)) / g.dm;
   const float q = exact_log_sr(y, g.dm, g.zm, u, kKM);
-  const float s = mc > 0.0f ? q : (mc < 0.0f ? -q : (mc != mc ? mc : 0.0f));
-  return (int)s;
+  return signed_code_m(mc, q);
+}
+
+// exact_quant_m before the draw: codes for u >= p (lo) and u < p (hi).
+__device__ __forceinline__ void exact_quant_m_pair(float mn, const Grid &g, float &p, int &lo,
+                                                   int &hi) {
+  const float mc = clamp_t(mn, -g.sm, g.sm);
+  const float y = cr_log1p(fabsf(mc)) / g.dm;
+  float qlo, qhi;
+  exact_log_sr_pair(y, g.dm, g.zm, kKM, p, qlo, qhi);
+  lo = signed_code_m(mc, qlo);
+  hi = signed_code_m(mc, qhi);
 }
 
 // Quantise v (functional.py:153-176); returns the uint16 code in [0, 65535].
@@ -145,6 +173,24 @@ __device__ __forceinline__ int exact_quant_w(float vn, const Grid &g, float eps,
   const float y = cr_log(wc / g.wmin) / g.dw;
   const float q = exact_log_sr(y, g.dw, g.zw, u, kKW);
   return (int)q;
+}
+
+// exact_quant_w before the draw: codes for u >= p (lo) and u < p (hi).
+__device__ __forceinline__ void exact_quant_w_pair(float vn, const Grid &g, float eps, float &p,
+                                                   int &lo, int &hi) {
+  if (!g.dwpos) {
+    p = 0.0f;
+    lo = hi = 0;
+    return;
+  }
+  const float vc = (vn != vn || vn > 0.0f) ? vn : 0.0f;
+  const float w = 1.0f / (cr_sqrt(vc) + eps);
+  const float wc = clamp_t(w, g.wmin, g.wmax);
+  const float y = cr_log(wc / g.wmin) / g.dw;
+  float qlo, qhi;
+  exact_log_sr_pair(y, g.dw, g.zw, kKW, p, qlo, qhi);
+  lo = (int)qlo;
+  hi = (int)qhi;
 }
 
 }  // namespace luma

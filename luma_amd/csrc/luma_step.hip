@@ -348,23 +348,50 @@ __device__ __noinline__ float2 exact_mv(int qm, int qw, float g, const LUMA_GLOB
   return make_float2(mn, vn);
 }
 
-// New momentum code of one element from its old code (exact path; the same
-// float32 sequence as exact_mv's m' followed by exact_quant_m).
-__device__ __noinline__ int exact_code_m(int qm, float g, const LUMA_GLOBAL Grid *old,
-                                         const LUMA_GLOBAL Grid *nw, Hyper h, float um) {
+// New code of one element before its draw (exact path): the 16-bit code
+// when the uniform u >= p (lo) and when u < p (hi), and p.  Returned packed
+// in one 64-bit value (lo | hi << 16 | bits(p) << 32) so that the call
+// needs no stack.
+struct CodePair {
+  int lo, hi;
+  float p;
+};
+
+__device__ __forceinline__ uint64_t pack_pair(int lo, int hi, float p) {
+  return (uint64_t)(((uint32_t)lo & 0xFFFFu) | ((uint32_t)hi << 16)) |
+         ((uint64_t)__float_as_uint(p) << 32);
+}
+
+__device__ __forceinline__ CodePair unpack_pair(uint64_t v) {
+  CodePair c;
+  c.lo = (int)(v & 0xFFFFu);
+  c.hi = (int)((v >> 16) & 0xFFFFu);
+  c.p = __uint_as_float((uint32_t)(v >> 32));
+  return c;
+}
+
+// Momentum: the same float32 sequence as exact_mv's m' then exact_quant_m.
+__device__ __noinline__ uint64_t exact_pair_m(int qm, float g, const LUMA_GLOBAL Grid *old,
+                                              const LUMA_GLOBAL Grid *nw, Hyper h) {
   const float m = old ? exact_decode_m(qm, old->dm) : 0.0f;
   const float mn = h.beta1 * m + h.omb1 * g;
   const Grid G = *nw;
-  return exact_quant_m(mn, G, um);
+  float p;
+  int lo, hi;
+  exact_quant_m_pair(mn, G, p, lo, hi);
+  return pack_pair(lo, hi, p);
 }
 
-// New preconditioner code of one element from its old code (exact path).
-__device__ __noinline__ int exact_code_w(int qw, float g, const LUMA_GLOBAL Grid *old,
-                                         const LUMA_GLOBAL Grid *nw, Hyper h, float uw) {
+// Preconditioner: exact_mv's v' then exact_quant_w.
+__device__ __noinline__ uint64_t exact_pair_w(int qw, float g, const LUMA_GLOBAL Grid *old,
+                                              const LUMA_GLOBAL Grid *nw, Hyper h) {
   const float v = old ? exact_decode_v(qw, old->wmin, old->dw, h.eps) : 0.0f;
   const float vn = h.beta2 * v + h.omb2 * (g * g);
   const Grid G = *nw;
-  return exact_quant_w(vn, G, h.eps, uw);
+  float p;
+  int lo, hi;
+  exact_quant_w_pair(vn, G, h.eps, p, lo, hi);
+  return pack_pair(lo, hi, p);
 }
 
 // Per-wave queues of elements whose fast result is not certified.  Elements
@@ -827,20 +854,32 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   // gradient as float32 bits (no second read of HBM).  The fast codes were
   // already stored; the exact ones overwrite them (same wavefront, so the
   // stores stay in program order).
-  auto uniform = [&](int64_t i, uint32_t top, int which) {
-    const U4 fine = philox_fine_block((uint64_t)i, k0, k1);
-    return (float)((top << 16) | u4_half(fine, 2 * (int)(i & 3) + which)) * 0x1p-24f;
+  // The code is c.hi when u < c.p.  With Philox the top 8 bits of u are
+  // known: u lies in [top/256, (top + 1)/256 - 2^-24], which decides unless
+  // c.p falls inside (then the fine block gives the low 16 bits).
+  auto below = [&](float p, int64_t i, uint32_t top, int which) -> bool {  // u < p
+    const float lo = (float)(top << 16) * 0x1p-24f;
+    const float hi = (float)((top << 16) | 0xFFFFu) * 0x1p-24f;
+    bool b = p > hi;                  // u <= hi < p
+    if (p > lo && !b) {               // else u >= lo >= p (a NaN p also: false)
+      const U4 fine = philox_fine_block((uint64_t)i, k0, k1);
+      b = (float)((top << 16) | u4_half(fine, 2 * (int)(i & 3) + which)) * 0x1p-24f < p;
+    }
+    return b;
   };
   auto run_m = [&](uint4 ent) {
     const int64_t i = beg + (ent.x & 0xFFFFu);
-    const float um = INJ ? T.u_m[i] : uniform(i, ent.y, 0);
-    T.q_m[i] = (int16_t)exact_code_m((int)(int16_t)(ent.x >> 16), __uint_as_float(ent.z), old,
-                                     nw, h, um);
+    const CodePair c =
+        unpack_pair(exact_pair_m((int)(int16_t)(ent.x >> 16), __uint_as_float(ent.z), old, nw, h));
+    const bool b = INJ ? T.u_m[i] < c.p : below(c.p, i, ent.y, 0);
+    T.q_m[i] = (int16_t)(b ? c.hi : c.lo);
   };
   auto run_w = [&](uint4 ent) {
     const int64_t i = beg + (ent.x & 0xFFFFu);
-    const float uw = INJ ? T.u_w[i] : uniform(i, ent.y, 1);
-    T.q_w[i] = (int16_t)exact_code_w((int)(ent.x >> 16), __uint_as_float(ent.z), old, nw, h, uw);
+    const CodePair c =
+        unpack_pair(exact_pair_w((int)(ent.x >> 16), __uint_as_float(ent.z), old, nw, h));
+    const bool b = INJ ? T.u_w[i] < c.p : below(c.p, i, ent.y, 1);
+    T.q_w[i] = (int16_t)(b ? c.hi : c.lo);
   };
   // Every lane runs the same number of iterations (lanes past the end carry
   // n = 0), so the ballots and the queue lengths stay uniform across the wave.
