@@ -20,7 +20,10 @@
  *                         src/luma_optimizer/functional.py:183-228) and
  *                         luma_update_step (t >= 2, functional.py:231-298),
  *                         i.e. the Triton pipelines luma_triton_init_step /
- *                         luma_triton_step (triton_kernel.py:409-492).
+ *                         luma_triton_step (triton_kernel.py:409-492); with
+ *                         LumaScaling, also GradScaler's unscale_ and
+ *                         skip-on-overflow around it (the reference runs
+ *                         them outside the optimizer).
  *   luma_step_profiled -- luma_step with event records between its launches.
  *   luma_step_tensor   -- one tensor, no device tables: the per-tensor
  *                         functional ops luma_triton_step /
@@ -51,7 +54,7 @@
 extern "C" {
 #endif
 
-#define LUMA_ABI_VERSION 2
+#define LUMA_ABI_VERSION 3
 
 /* Elements per chunk-table entry (one workgroup's share of a tensor). */
 #define LUMA_CHUNK_ELEMS 32768
@@ -111,6 +114,23 @@ typedef struct LumaGroup {
   double reserved; /* 0 */
 } LumaGroup;
 
+/*
+ * Mixed-precision scaling (torch.amp.GradScaler's contract for optimizers
+ * that unscale inside their step, `_step_supports_amp_scaling`):
+ *   grad_scale -- device float32 scalar, or NULL.  The gradients hold
+ *                 scale * g; each element is unscaled exactly as
+ *                 GradScaler.unscale_ would store it:
+ *                 dtype(f32(grad) * f32(1 / (double)scale)), rounded to
+ *                 nearest even in the gradient's own dtype.
+ *   found_inf  -- device float32 scalar, or NULL.  Nonzero: the whole step
+ *                 does nothing (parameters, codes, scales and step counts
+ *                 unchanged), with no host synchronisation.
+ */
+typedef struct LumaScaling {
+  const float *grad_scale;
+  const float *found_inf;
+} LumaScaling;
+
 typedef struct LumaStepArgs {
   const LumaTensor *tensors; /* device */
   int32_t n_tensors;
@@ -121,6 +141,7 @@ typedef struct LumaStepArgs {
   uint64_t base_seed;        /* LUMA._base_seed as its two's-complement bits */
   int32_t noise_mode;        /* LUMA_NOISE_* */
   int32_t flags;             /* LUMA_FLAG_* */
+  LumaScaling scaling;       /* both NULL: unscaled gradients, always step */
 } LumaStepArgs;
 
 /* One slot write (array in device memory). */
@@ -163,12 +184,14 @@ int luma_step(const LumaStepArgs *args, void *stream);
 int luma_step_profiled(const LumaStepArgs *args, void *stream, void *const events[4]);
 
 /*
- * luma_step for one tensor with no device tables: *tensor and *group are
- * host structs read during the call (tensor->first_chunk is ignored);
+ * luma_step for one tensor with no device tables: *tensor, *group and
+ * *scaling (may be NULL) are host structs read during the call
+ * (tensor->first_chunk is ignored);
  * `partials` needs luma_workspace_bytes(ceil(numel / LUMA_CHUNK_ELEMS)).
  */
 int luma_step_tensor(const LumaTensor *tensor, const LumaGroup *group, float *partials,
-                     uint64_t base_seed, int32_t noise_mode, int32_t flags, void *stream);
+                     uint64_t base_seed, int32_t noise_mode, int32_t flags,
+                     const LumaScaling *scaling, void *stream);
 
 /* Write step count, S_m and S_v of n slots (items: device array) and derive their grids. */
 int luma_set_scales(const LumaScaleInit *items, int32_t n, void *stream);

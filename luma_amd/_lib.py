@@ -18,7 +18,7 @@ LIB_PATH = os.path.join(HERE, LIB_NAME)
 
 CHUNK_ELEMS = 32768          # LUMA_CHUNK_ELEMS
 SLOT_BYTES = 512             # LUMA_SLOT_BYTES
-ABI_VERSION = 2              # LUMA_ABI_VERSION
+ABI_VERSION = 3              # LUMA_ABI_VERSION
 
 GRAD_F32, GRAD_BF16, GRAD_F16 = 0, 1, 2
 NOISE_PHILOX, NOISE_INJECTED = 0, 1
@@ -42,6 +42,11 @@ SCALE_INIT_DTYPE = np.dtype([
 HYPER_ROW_FIELDS = ("beta1", "omb1", "beta2", "omb2", "decay", "neg_eta", "bc2", "eps")
 
 
+class Scaling(ctypes.Structure):
+    """LumaScaling: GradScaler's scale and found_inf device scalars (or NULL)."""
+    _fields_ = [("grad_scale", ctypes.c_void_p), ("found_inf", ctypes.c_void_p)]
+
+
 class StepArgs(ctypes.Structure):
     _fields_ = [
         ("tensors", ctypes.c_void_p),
@@ -53,6 +58,7 @@ class StepArgs(ctypes.Structure):
         ("base_seed", ctypes.c_uint64),
         ("noise_mode", ctypes.c_int32),
         ("flags", ctypes.c_int32),
+        ("scaling", Scaling),
     ]
 
 
@@ -72,7 +78,7 @@ _SIGNATURES = {
     "luma_step_profiled": (ctypes.c_int, [ctypes.POINTER(StepArgs), _VP,
                                           ctypes.POINTER(ctypes.c_void_p)]),
     "luma_step_tensor": (ctypes.c_int, [_VP, _VP, _VP, ctypes.c_uint64, ctypes.c_int32,
-                                        ctypes.c_int32, _VP]),
+                                        ctypes.c_int32, ctypes.POINTER(Scaling), _VP]),
     "luma_set_scales": (ctypes.c_int, [_VP, ctypes.c_int32, _VP]),
     "luma_get_scales": (ctypes.c_int, [_VP, ctypes.c_int32, _VP, _VP, _VP]),
     "luma_decode": (ctypes.c_int, [_VP, _VP, ctypes.c_int64, _VP, ctypes.c_double, _VP, _VP,

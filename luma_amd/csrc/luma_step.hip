@@ -65,7 +65,45 @@ struct StepSrc {
   const LumaGroup *groups;
   Tensor one;
   LumaGroup group;
+  LumaScaling scaling;
 };
+
+// GradScaler's found_inf: a nonzero value makes the whole step a no-op.
+__device__ __forceinline__ bool skip_step(const StepSrc &src) {
+  return src.scaling.found_inf != nullptr && *src.scaling.found_inf != 0.0f;
+}
+
+// f32(1 / (double)scale), as GradScaler computes the inverse scale.
+__device__ __forceinline__ float inv_scale(const StepSrc &src) {
+  return src.scaling.grad_scale ? (float)(1.0 / (double)*src.scaling.grad_scale) : 1.0f;
+}
+
+// A scaled gradient element as GradScaler.unscale_ stores it: the float32
+// product with the inverse scale, rounded to nearest even in the gradient's
+// own dtype (a NaN becomes the canonical bfloat16 NaN, as torch's cast does).
+__device__ __forceinline__ float round_bf16(float x) {
+  if (x != x) return __uint_as_float(0x7FC00000u);
+  const uint32_t u = __float_as_uint(x);
+  return __uint_as_float((u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u);
+}
+
+template <int GD>
+__device__ __forceinline__ float unscale(float g, float inv) {
+  float x = g * inv;
+  // Round the product to float32 first, as torch does: left alone, the
+  // compiler fuses the product and the half conversion into one
+  // v_fma_mixlo_f16, which rounds once instead of twice.
+  asm("" : "+v"(x));
+  if (GD == LUMA_GRAD_F32) return x;
+  if (GD == LUMA_GRAD_F16) return __half2float(__float2half_rn(x));
+  return round_bf16(x);
+}
+
+__device__ __forceinline__ float unscale_rt(float g, float inv, int dt) {
+  if (dt == LUMA_GRAD_F32) return unscale<LUMA_GRAD_F32>(g, inv);
+  if (dt == LUMA_GRAD_F16) return unscale<LUMA_GRAD_F16>(g, inv);
+  return unscale<LUMA_GRAD_BF16>(g, inv);
+}
 
 // The chunk of this workgroup: its tensor, group and chunk index.
 __device__ __forceinline__ void chunk_job(const StepSrc &src, Tensor &T, LumaGroup &g,
@@ -136,8 +174,10 @@ __device__ __forceinline__ void block_max2(float &a, float &b) {
 
 // m', v' of element i of tensor T (exact path).
 __device__ __forceinline__ void element_ema(const Tensor &T, const Hyper &h, const Grid *old,
-                                            int64_t i, float &mn, float &vn) {
-  const float g = load_grad(T.grad, i, T.grad_dtype);
+                                            int64_t i, bool scaled, float inv, float &mn,
+                                            float &vn) {
+  float g = load_grad(T.grad, i, T.grad_dtype);
+  if (scaled) g = unscale_rt(g, inv, T.grad_dtype);
   float m = 0.0f, v = 0.0f;
   if (old) {  // t >= 2: decode the stored codes on the old grid
     m = exact_decode_m(T.q_m[i], old->dm);
@@ -148,11 +188,14 @@ __device__ __forceinline__ void element_ema(const Tensor &T, const Hyper &h, con
 
 __global__ __launch_bounds__(kThreads) void pass1_exact_kernel(StepSrc src,
                                                                float *__restrict__ partials) {
+  if (skip_step(src)) return;
   Tensor T;
   LumaGroup grp;
   int64_t ci;
   chunk_job(src, T, grp, ci);
   const Hyper h = group_hyper(grp);
+  const bool scaled = src.scaling.grad_scale != nullptr;
+  const float inv = inv_scale(src);
   // this step is t = step + 1; its decode reads the grid of step t - 1
   const int64_t prev = T.slot->step;
   const Grid *old = prev >= 1 ? (const Grid *)&T.slot->grid[prev & 1] : nullptr;
@@ -165,7 +208,7 @@ __global__ __launch_bounds__(kThreads) void pass1_exact_kernel(StepSrc src,
       const int64_t i = e0 + j;
       if (i >= end) break;
       float mn, vn;
-      element_ema(T, h, old, i, mn, vn);
+      element_ema(T, h, old, i, scaled, inv, mn, vn);
       am = nan_max(am, fabsf(mn));
       av = nan_max(av, vn);
     }
@@ -182,6 +225,7 @@ __device__ __forceinline__ double py_max(double a, double floor_) { return floor
 
 __global__ __launch_bounds__(64) void finalize_kernel(StepSrc src,
                                                       const float *__restrict__ partials) {
+  if (skip_step(src)) return;
   Tensor T;
   LumaGroup grp;
   tensor_job(src, T, grp);
@@ -214,10 +258,13 @@ __global__ __launch_bounds__(64) void finalize_kernel(StepSrc src,
 
 __global__ __launch_bounds__(kThreads) void pass2_exact_kernel(StepSrc src, uint64_t base_seed,
                                                                int noise_mode) {
+  if (skip_step(src)) return;
   Tensor T;
   LumaGroup grp;
   int64_t ci;
   chunk_job(src, T, grp, ci);
+  const bool scaled = src.scaling.grad_scale != nullptr;
+  const float inv = inv_scale(src);
   const Slot &S = *(const Slot *)T.slot;
   const int64_t t = S.step;   // advanced by finalize
   const Hyper h = S.hyp;
@@ -239,7 +286,7 @@ __global__ __launch_bounds__(kThreads) void pass2_exact_kernel(StepSrc src, uint
       const int64_t i = e0 + j;
       if (i >= end) break;
       float mn, vn;
-      element_ema(T, h, old, i, mn, vn);
+      element_ema(T, h, old, i, scaled, inv, mn, vn);
       T.param[i] = exact_param_update(T.param[i], mn, vn, h);
       float um, uw;
       if (noise_mode == LUMA_NOISE_PHILOX) {
@@ -462,14 +509,24 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 // Constants of the pass-1 loop, kept in VGPRs (see in_vgpr).
 struct P1Const {
   float dm, ndw, iwmin, eps, b1, omb1, b2, omb2;
+  float inv;   // inverse gradient scale (SCALED)
   uint32_t sign;
 };
 
-template <int GD, bool SMALL, bool FULL>
+// Unscales a group's gradients in place (SCALED launches only).
+template <int GD, bool SCALED>
+__device__ __forceinline__ void unscale_group(Group8 &G, float inv) {
+  if (!SCALED) return;
+#pragma unroll
+  for (int j = 0; j < kVec; ++j) G.g[j] = unscale<GD>(G.g[j], inv);
+}
+
+template <int GD, bool SMALL, bool SCALED, bool FULL>
 __device__ __forceinline__ void p1_iter(const Tensor &T, const P1Const &K, int64_t e0, int n,
                                         uint32_t (&am)[kVec], uint32_t (&av)[kVec]) {
   Group8 G;
   load_group<GD>(T, e0, n, FULL, G);
+  unscale_group<GD, SCALED>(G, K.inv);
 #pragma unroll
   for (int j = 0; j < kVec; ++j) {
     const FastEma f = fast_ema<SMALL, false>(G.qm[j], G.qw[j], G.g[j], K.dm, K.ndw, K.iwmin,
@@ -486,9 +543,9 @@ __device__ __forceinline__ void p1_iter(const Tensor &T, const P1Const &K, int64
 // whose fast value is below the threshold cannot be the exact maximum; the
 // others (in practice a few per chunk) go through the wave's queue to the
 // exact path.
-template <int GD, bool SMALL>
+template <int GD, bool SMALL, bool SCALED>
 __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOBAL Grid *old,
-                                int64_t beg, int64_t end, float &exm, float &exv,
+                                float inv, int64_t beg, int64_t end, float &exm, float &exv,
                                 uint32_t *queue) {
   const Bounds B = make_bounds((const Grid *)old, nullptr, h.beta1, h.beta2);
   const DecodeK D = decode_consts(old, h.eps);
@@ -501,6 +558,7 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   K.omb1 = in_vgpr(h.omb1);
   K.b2 = in_vgpr(h.beta2);
   K.omb2 = in_vgpr(h.omb2);
+  K.inv = in_vgpr(inv);
   K.sign = in_vgpr(0x80000000u);
   const bool vec_ok = tensor_vec_ok(T);
   const float lo_m = 1.0f - B.dlt_m, hi_m = 1.0f / (1.0f + B.dlt_m);
@@ -513,7 +571,9 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   uint32_t qlen = 0;
   auto run = [&](uint32_t off) {
     const int64_t i = beg + off;
-    const float2 e = exact_mv(T.q_m[i], (int)(uint16_t)T.q_w[i], load_grad(T.grad, i, GD), old, h);
+    float g = load_grad(T.grad, i, GD);
+    if (SCALED) g = unscale<GD>(g, inv);
+    const float2 e = exact_mv(T.q_m[i], (int)(uint16_t)T.q_w[i], g, old, h);
     exm = nan_max(exm, fabsf(e.x));
     exv = nan_max(exv, e.y);
   };
@@ -526,9 +586,9 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     const int n = rem <= 0 ? 0 : (rem < kVec ? (int)rem : kVec);
     uint32_t am[kVec], av[kVec];
     if (vec_ok && n == kVec)
-      p1_iter<GD, SMALL, true>(T, K, e0, n, am, av);
+      p1_iter<GD, SMALL, SCALED, true>(T, K, e0, n, am, av);
     else
-      p1_iter<GD, SMALL, false>(T, K, e0, n, am, av);
+      p1_iter<GD, SMALL, SCALED, false>(T, K, e0, n, am, av);
     const uint32_t im = max(max(max(am[0], am[1]), max(am[2], am[3])),
                             max(max(am[4], am[5]), max(am[6], am[7])));
     const uint32_t iv = max(max(max(av[0], av[1]), max(av[2], av[3])),
@@ -568,8 +628,23 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   }
 }
 
+template <int GD>
+__device__ __forceinline__ void pass1_dispatch(const Tensor &T, const Hyper &h,
+                                               const LUMA_GLOBAL Grid *old, float inv,
+                                               int64_t beg, int64_t end, bool small, bool scaled,
+                                               float &exm, float &exv, uint32_t *q) {
+  if (scaled) {
+    if (small) pass1_fast_body<GD, true, true>(T, h, old, inv, beg, end, exm, exv, q);
+    else pass1_fast_body<GD, false, true>(T, h, old, inv, beg, end, exm, exv, q);
+  } else {
+    if (small) pass1_fast_body<GD, true, false>(T, h, old, inv, beg, end, exm, exv, q);
+    else pass1_fast_body<GD, false, false>(T, h, old, inv, beg, end, exm, exv, q);
+  }
+}
+
 __global__ __launch_bounds__(kThreads) void pass1_fast_kernel(StepSrc src,
                                                               float *__restrict__ partials) {
+  if (skip_step(src)) return;
   Tensor T;
   LumaGroup grp;
   int64_t ci;
@@ -581,19 +656,17 @@ __global__ __launch_bounds__(kThreads) void pass1_fast_kernel(StepSrc src,
   const int64_t beg = ci * kChunk;
   const int64_t end = beg + kChunk < T.numel ? beg + kChunk : T.numel;
   const bool small = old == nullptr || old->fast[kXTopM] <= kSmall;
+  const bool scaled = src.scaling.grad_scale != nullptr;
+  const float inv = inv_scale(src);
   __shared__ uint32_t qbuf[kThreads / 64][kQueueCap];
   uint32_t *q = qbuf[threadIdx.x >> 6];
   float exm = 0.0f, exv = 0.0f;
-  if (T.grad_dtype == LUMA_GRAD_BF16) {
-    if (small) pass1_fast_body<LUMA_GRAD_BF16, true>(T, h, old, beg, end, exm, exv, q);
-    else pass1_fast_body<LUMA_GRAD_BF16, false>(T, h, old, beg, end, exm, exv, q);
-  } else if (T.grad_dtype == LUMA_GRAD_F16) {
-    if (small) pass1_fast_body<LUMA_GRAD_F16, true>(T, h, old, beg, end, exm, exv, q);
-    else pass1_fast_body<LUMA_GRAD_F16, false>(T, h, old, beg, end, exm, exv, q);
-  } else {
-    if (small) pass1_fast_body<LUMA_GRAD_F32, true>(T, h, old, beg, end, exm, exv, q);
-    else pass1_fast_body<LUMA_GRAD_F32, false>(T, h, old, beg, end, exm, exv, q);
-  }
+  if (T.grad_dtype == LUMA_GRAD_BF16)
+    pass1_dispatch<LUMA_GRAD_BF16>(T, h, old, inv, beg, end, small, scaled, exm, exv, q);
+  else if (T.grad_dtype == LUMA_GRAD_F16)
+    pass1_dispatch<LUMA_GRAD_F16>(T, h, old, inv, beg, end, small, scaled, exm, exv, q);
+  else
+    pass1_dispatch<LUMA_GRAD_F32>(T, h, old, inv, beg, end, small, scaled, exm, exv, q);
   block_max2(exm, exv);
   if (threadIdx.x == 0) {
     partials[2 * (int64_t)blockIdx.x] = exm;
@@ -653,6 +726,7 @@ struct P2Const {
   float zoff;               // 1 - half width of a Philox bucket (1 when injected)
   float k1, k2, k3, k7, k8;
   float kmax_m, kmax_w;     // 32767, 65535
+  float inv;                // inverse gradient scale (SCALED)
   uint32_t sign;            // 0x80000000
 };
 
@@ -696,6 +770,7 @@ __device__ __forceinline__ void launder(P2Const &C) {
   C.nk7 = in_vgpr(C.nk7);
   C.hk8 = in_vgpr(C.hk8);
   C.kmax_w = in_vgpr(C.kmax_w);
+  C.inv = in_vgpr(C.inv);
   C.sign = in_vgpr(C.sign);
 }
 
@@ -703,10 +778,11 @@ __device__ __forceinline__ void launder(P2Const &C) {
 // aligned (vector loads/stores, no masking).  Returns which codes need the
 // exact path (bit j: momentum code of element j, bit 8 + j: preconditioner
 // code); Q and coarse are kept for the queues.
-template <int GD, bool INJ, bool SMALL, bool FULL>
+template <int GD, bool INJ, bool SMALL, bool SCALED, bool FULL>
 __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, int64_t e0, int n,
                                             uint32_t k0, uint32_t k1, Group8 &Q, U4 &coarse) {
   load_group<GD>(T, e0, n, FULL, Q);
+  unscale_group<GD, SCALED>(Q, C.inv);
   float p[kVec], zm0[kVec], zw0[kVec];
   if (FULL) {
     const vf4 p0 = *(const LUMA_GLOBAL vf4 *)(T.param + e0);
@@ -798,9 +874,9 @@ __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, i
   return flags;
 }
 
-template <int GD, bool INJ, bool SMALL>
+template <int GD, bool INJ, bool SMALL, bool SCALED>
 __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOBAL Grid *old,
-                                const LUMA_GLOBAL Grid *nw, int64_t beg, int64_t end,
+                                const LUMA_GLOBAL Grid *nw, float inv, int64_t beg, int64_t end,
                                 uint32_t k0, uint32_t k1, uint4 *queue) {
   const Bounds B = make_bounds((const Grid *)old, (const Grid *)nw, h.beta1, h.beta2);
   P2Const C;
@@ -833,6 +909,7 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   C.k8 = B.k8 + hb;
   C.kmax_m = 32767.0f;
   C.kmax_w = 65535.0f;
+  C.inv = inv;
   C.sign = 0x80000000u;
   C.pk0 = k0;
   C.pk1 = k1;
@@ -892,9 +969,9 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     U4 coarse{};
     uint32_t flags;
     if (vec_ok && n == kVec)
-      flags = p2_iter<GD, INJ, SMALL, true>(T, C, e0, n, k0, k1, Q, coarse);
+      flags = p2_iter<GD, INJ, SMALL, SCALED, true>(T, C, e0, n, k0, k1, Q, coarse);
     else
-      flags = p2_iter<GD, INJ, SMALL, false>(T, C, e0, n, k0, k1, Q, coarse);
+      flags = p2_iter<GD, INJ, SMALL, SCALED, false>(T, C, e0, n, k0, k1, Q, coarse);
     if (!__ballot(flags != 0)) continue;
     const uint32_t off0 = (uint32_t)(e0 - beg);
     // queue positions: a wave prefix sum of (momentum count | preconditioner
@@ -956,23 +1033,34 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   if (lane < qlen_w) run_w(queue_w[lane]);
 }
 
+template <int GD, bool SCALED>
+__device__ __forceinline__ void pass2_dispatch_s(const Tensor &T, const Hyper &h,
+                                                 const LUMA_GLOBAL Grid *old,
+                                                 const LUMA_GLOBAL Grid *nw, float inv,
+                                                 int64_t beg, int64_t end, uint32_t k0,
+                                                 uint32_t k1, bool inj, bool small, uint4 *q) {
+  if (inj) {
+    if (small) pass2_fast_body<GD, true, true, SCALED>(T, h, old, nw, inv, beg, end, k0, k1, q);
+    else pass2_fast_body<GD, true, false, SCALED>(T, h, old, nw, inv, beg, end, k0, k1, q);
+  } else {
+    if (small) pass2_fast_body<GD, false, true, SCALED>(T, h, old, nw, inv, beg, end, k0, k1, q);
+    else pass2_fast_body<GD, false, false, SCALED>(T, h, old, nw, inv, beg, end, k0, k1, q);
+  }
+}
+
 template <int GD>
 __device__ __forceinline__ void pass2_dispatch(const Tensor &T, const Hyper &h,
                                                const LUMA_GLOBAL Grid *old,
-                                               const LUMA_GLOBAL Grid *nw, int64_t beg,
-                                               int64_t end, uint32_t k0, uint32_t k1, bool inj,
-                                               bool small, uint4 *q) {
-  if (inj) {
-    if (small) pass2_fast_body<GD, true, true>(T, h, old, nw, beg, end, k0, k1, q);
-    else pass2_fast_body<GD, true, false>(T, h, old, nw, beg, end, k0, k1, q);
-  } else {
-    if (small) pass2_fast_body<GD, false, true>(T, h, old, nw, beg, end, k0, k1, q);
-    else pass2_fast_body<GD, false, false>(T, h, old, nw, beg, end, k0, k1, q);
-  }
+                                               const LUMA_GLOBAL Grid *nw, float inv, bool scaled,
+                                               int64_t beg, int64_t end, uint32_t k0, uint32_t k1,
+                                               bool inj, bool small, uint4 *q) {
+  if (scaled) pass2_dispatch_s<GD, true>(T, h, old, nw, inv, beg, end, k0, k1, inj, small, q);
+  else pass2_dispatch_s<GD, false>(T, h, old, nw, inv, beg, end, k0, k1, inj, small, q);
 }
 
 __global__ __launch_bounds__(kThreads) void pass2_fast_kernel(StepSrc src, uint64_t base_seed,
                                                               int noise_mode) {
+  if (skip_step(src)) return;
   Tensor T;
   LumaGroup grp;
   int64_t ci;
@@ -988,14 +1076,16 @@ __global__ __launch_bounds__(kThreads) void pass2_fast_kernel(StepSrc src, uint6
   step_key(base_seed, t, T.param_id, k0, k1);
   const bool inj = noise_mode == LUMA_NOISE_INJECTED;
   const bool small = (old == nullptr || old->fast[kXTopM] <= kSmall) && nw->sm <= kSmall;
+  const bool scaled = src.scaling.grad_scale != nullptr;
+  const float inv = inv_scale(src);
   __shared__ uint4 qbuf[kThreads / 64][2 * kQueueCap2];
   uint4 *q = qbuf[threadIdx.x >> 6];
   if (T.grad_dtype == LUMA_GRAD_BF16)
-    pass2_dispatch<LUMA_GRAD_BF16>(T, h, old, nw, beg, end, k0, k1, inj, small, q);
+    pass2_dispatch<LUMA_GRAD_BF16>(T, h, old, nw, inv, scaled, beg, end, k0, k1, inj, small, q);
   else if (T.grad_dtype == LUMA_GRAD_F16)
-    pass2_dispatch<LUMA_GRAD_F16>(T, h, old, nw, beg, end, k0, k1, inj, small, q);
+    pass2_dispatch<LUMA_GRAD_F16>(T, h, old, nw, inv, scaled, beg, end, k0, k1, inj, small, q);
   else
-    pass2_dispatch<LUMA_GRAD_F32>(T, h, old, nw, beg, end, k0, k1, inj, small, q);
+    pass2_dispatch<LUMA_GRAD_F32>(T, h, old, nw, inv, scaled, beg, end, k0, k1, inj, small, q);
 }
 
 // ---------------------------------------------------------------------------
@@ -1220,6 +1310,7 @@ static int step_impl(const LumaStepArgs *a, void *stream, void *const *events) {
   src.tensors = reinterpret_cast<const Tensor *>(a->tensors);
   src.chunks = a->chunks;
   src.groups = a->groups;
+  src.scaling = a->scaling;
   return launch_step(src, a->n_tensors, a->n_chunks, a->partials, a->base_seed, a->noise_mode,
                      a->flags, static_cast<hipStream_t>(stream), events);
 }
@@ -1231,7 +1322,8 @@ int luma_step_profiled(const LumaStepArgs *a, void *stream, void *const events[4
 }
 
 int luma_step_tensor(const LumaTensor *tensor, const LumaGroup *group, float *partials,
-                     uint64_t base_seed, int32_t noise_mode, int32_t flags, void *stream) {
+                     uint64_t base_seed, int32_t noise_mode, int32_t flags,
+                     const LumaScaling *scaling, void *stream) {
   if (!tensor || !group) return fail("luma_step_tensor: null tensor or group");
   if (tensor->numel <= 0) return 0;
   if (!tensor->param || !tensor->grad || !tensor->q_m || !tensor->q_w || !tensor->slot ||
@@ -1245,6 +1337,7 @@ int luma_step_tensor(const LumaTensor *tensor, const LumaGroup *group, float *pa
   memcpy(&src.one, tensor, sizeof(Tensor));
   src.one.first_chunk = 0;
   src.group = *group;
+  if (scaling) src.scaling = *scaling;
   return launch_step(src, 1, (int32_t)nch, partials, base_seed, noise_mode, flags,
                      static_cast<hipStream_t>(stream), nullptr);
 }

@@ -19,6 +19,7 @@ no device tables, no host synchronisation.
 
 from __future__ import annotations
 
+import ctypes
 from typing import Optional, Tuple
 
 import numpy as np
@@ -81,8 +82,14 @@ def _luma_step_op(param: torch.Tensor, grad: torch.Tensor, Q_m: torch.Tensor,
                   Q_w: torch.Tensor, slot: torch.Tensor, beta1: float, beta2: float, eps: float,
                   lr: float, weight_decay: float, param_id: int, base_seed: int,
                   u_m: Optional[torch.Tensor] = None, u_w: Optional[torch.Tensor] = None,
-                  exact: bool = False) -> None:
+                  exact: bool = False, grad_scale: Optional[torch.Tensor] = None,
+                  found_inf: Optional[torch.Tensor] = None) -> None:
     _check(param, grad, Q_m, Q_w, slot, u_m, u_w)
+    for name, t in (("grad_scale", grad_scale), ("found_inf", found_inf)):
+        if t is not None and (t.numel() != 1 or t.dtype != torch.float32
+                              or t.device != param.device):
+            raise ValueError(f"luma_step: {name} must be a one-element float32 tensor on "
+                             f"{param.device}")
     n = param.numel()
     if n == 0:
         return
@@ -103,15 +110,18 @@ def _luma_step_op(param: torch.Tensor, grad: torch.Tensor, Q_m: torch.Tensor,
     partials = torch.empty(max(2 * nch, 2), dtype=torch.float32, device=param.device)
     noise = L.NOISE_PHILOX if u_m is None else L.NOISE_INJECTED
     stream = torch.cuda.current_stream(param.device).cuda_stream
+    scaling = L.Scaling(None if grad_scale is None else grad_scale.data_ptr(),
+                        None if found_inf is None else found_inf.data_ptr())
     rc = lib.luma_step_tensor(tt.ctypes.data, gg.ctypes.data, partials.data_ptr(),
                               base_seed & _MASK64, noise, L.FLAG_EXACT_ONLY if exact else 0,
-                              stream)
+                              ctypes.byref(scaling), stream)
     L.check(rc, "luma_step_tensor")
 
 
 @_luma_step_op.register_fake
 def _luma_step_fake(param, grad, Q_m, Q_w, slot, beta1, beta2, eps, lr, weight_decay, param_id,
-                    base_seed, u_m=None, u_w=None, exact=False) -> None:
+                    base_seed, u_m=None, u_w=None, exact=False, grad_scale=None,
+                    found_inf=None) -> None:
     return None
 
 
@@ -119,7 +129,8 @@ def luma_step(param: torch.Tensor, grad: torch.Tensor, Q_m: torch.Tensor, Q_w: t
               slot: torch.Tensor, beta1: float, beta2: float, eps: float, lr: float,
               weight_decay: float, param_id: int, base_seed: int,
               u_m: Optional[torch.Tensor] = None, u_w: Optional[torch.Tensor] = None,
-              exact: bool = False) -> None:
+              exact: bool = False, grad_scale: Optional[torch.Tensor] = None,
+              found_inf: Optional[torch.Tensor] = None) -> None:
     """One LUMA step of one tensor, in place.
 
     The init step (functional.py:183-228) when ``slot`` holds step count 0,
@@ -127,9 +138,13 @@ def luma_step(param: torch.Tensor, grad: torch.Tensor, Q_m: torch.Tensor, Q_w: t
     come from Philox keyed by ``((t << 32) | 2*param_id) ^ base_seed``, or from
     ``u_m`` / ``u_w`` (float32 in [0, 1), the parameter's shape) when given.
     ``exact`` forces the exact per-element path (same results, slower).
+    ``grad_scale`` / ``found_inf`` (one-element float32 device tensors) are
+    GradScaler's: the gradient is unscaled in the kernel as ``unscale_``
+    would store it, and a nonzero ``found_inf`` skips the step on the device.
     """
     torch.ops.luma_amd.luma_step(param, grad, Q_m, Q_w, slot, beta1, beta2, eps, lr,
-                                 weight_decay, param_id, base_seed, u_m, u_w, exact)
+                                 weight_decay, param_id, base_seed, u_m, u_w, exact, grad_scale,
+                                 found_inf)
 
 
 def init_slot(slot: torch.Tensor, step: int, S_m: float, S_v: float, eps: float) -> None:

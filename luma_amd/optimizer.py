@@ -123,7 +123,7 @@ class _Engine:
         return tt
 
     def launch(self, tt: np.ndarray, groups: np.ndarray, base_seed: int, noise_mode: int,
-               flags: int = 0):
+               flags: int = 0, scaling: Tuple[int, int] = (0, 0)):
         """One step over the tensors of table tt (luma_step), uploading only the
         tables whose contents changed since the previous launch."""
         capturing = torch.cuda.is_current_stream_capturing()
@@ -166,7 +166,8 @@ class _Engine:
             tensors=self._d_tensors.data_ptr(), n_tensors=n, n_chunks=n_chunks,
             chunks=self._d_chunks.data_ptr(), groups=self._d_groups.data_ptr(),
             partials=self._partials.data_ptr(),
-            base_seed=base_seed & _MASK64, noise_mode=noise_mode, flags=flags)
+            base_seed=base_seed & _MASK64, noise_mode=noise_mode, flags=flags,
+            scaling=L.Scaling(scaling[0] or None, scaling[1] or None))
         if self.profile_events is None:
             L.check(self.lib.luma_step(ctypes.byref(args), self._stream()), "luma_step")
         else:
@@ -286,6 +287,13 @@ class LUMA(Optimizer):
 
     _BACKENDS = ("auto", "hip", "triton")
 
+    # torch.amp.GradScaler: instead of unscaling the gradients and checking
+    # them on the host before calling step(), the scaler sets
+    # self.grad_scale / self.found_inf (device tensors) and calls step();
+    # the kernels unscale each gradient as unscale_ would store it and skip
+    # the whole step on the device when found_inf is nonzero.
+    _step_supports_amp_scaling = True
+
     def __init__(self, params, lr: float = 1e-3, betas: Tuple[float, float] = (0.9, 0.999),
                  eps: float = 1e-8, weight_decay: float = 0.01, backend: str = "auto"):
         # optimizer.py:80-89
@@ -311,6 +319,7 @@ class LUMA(Optimizer):
         self._noise: Optional[Dict[int, Tuple[torch.Tensor, torch.Tensor]]] = None
         self._flags = 0
         self._plan: Optional[_Plan] = None
+        self._scaling_keep = []
 
     # ------------------------------------------------------------------
     #  Helpers
@@ -354,6 +363,26 @@ class LUMA(Optimizer):
                 u = torch.empty_like(like, dtype=torch.float32).copy_(u)
             out.append(u)
         return out[0], out[1]
+
+    def _scaling(self, device) -> Tuple[int, int]:
+        """Device pointers of GradScaler's grad_scale / found_inf (0 if unset).
+        The tensors are kept on self until the next step so that they outlive
+        the launch."""
+        keep = []
+        ptrs = []
+        for name in ("grad_scale", "found_inf"):
+            t = getattr(self, name, None)
+            if t is None:
+                ptrs.append(0)
+                continue
+            if not isinstance(t, torch.Tensor) or t.numel() != 1:
+                raise ValueError(f"LUMA: {name} must be a one-element tensor")
+            if t.dtype != torch.float32 or t.device != device:
+                t = t.to(device=device, dtype=torch.float32)
+            keep.append(t)
+            ptrs.append(t.data_ptr())
+        self._scaling_keep = keep
+        return ptrs[0], ptrs[1]
 
     def _group_table(self) -> np.ndarray:
         """Hyper-parameters of every param group as the Python doubles the
@@ -521,7 +550,7 @@ class LUMA(Optimizer):
         plan = self._plan
         if plan is not None and self._noise is None and plan.refresh(self.param_groups):
             self._engine.launch(plan.tt, self._group_table(), self._base_seed, L.NOISE_PHILOX,
-                                self._flags)
+                                self._flags, self._scaling(self._engine.device))
             for state in plan.states:
                 state["step"] += 1
             return loss
@@ -587,7 +616,8 @@ class LUMA(Optimizer):
             rows.append((param, grad, state["Q_m"], state["Q_w"], u_m, u_w, state["_slot"],
                          state["param_id"], code, gi))
         tt = engine.table(rows)
-        engine.launch(tt, self._group_table(), self._base_seed, noise_mode, self._flags)
+        engine.launch(tt, self._group_table(), self._base_seed, noise_mode, self._flags,
+                      self._scaling(engine.device))
         # host count of step() calls; the kernels use the slot's device count
         for state in states:
             state["step"] += 1
