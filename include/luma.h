@@ -57,7 +57,7 @@ extern "C" {
 #define LUMA_ABI_VERSION 3
 
 /* Elements per chunk-table entry (one workgroup's share of a tensor). */
-#define LUMA_CHUNK_ELEMS 32768
+#define LUMA_CHUNK_ELEMS 65536
 
 /*
  * Bytes of one slot: a tensor's persistent device state (step count, S_m,

@@ -16,7 +16,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_NAME = "libluma_hip.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 
-CHUNK_ELEMS = 32768          # LUMA_CHUNK_ELEMS
+CHUNK_ELEMS = 65536          # LUMA_CHUNK_ELEMS
 SLOT_BYTES = 512             # LUMA_SLOT_BYTES
 ABI_VERSION = 3              # LUMA_ABI_VERSION
 

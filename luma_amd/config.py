@@ -6,7 +6,7 @@ SCALE_FLOOR_M: float = 1e-9       # minimum momentum scale S_m
 
 # Launch geometry of the HIP kernels (the reference's get_kernel_config returns
 # Triton launch parameters; these are the gfx950 equivalents).
-CHUNK_ELEMS: int = 32768          # elements per chunk-table entry (one workgroup)
+CHUNK_ELEMS: int = 65536          # elements per chunk-table entry (one workgroup)
 THREADS_PER_BLOCK: int = 256      # four wave64 per workgroup
 ELEMS_PER_THREAD: int = 8         # consecutive elements per thread per iteration
 

@@ -27,6 +27,7 @@ constexpr int kThreads = 256;     // 4 wave64 per workgroup
 constexpr int kVec = 8;           // consecutive elements per thread per iteration
 constexpr int64_t kChunk = LUMA_CHUNK_ELEMS;
 static_assert(kChunk % (kThreads * kVec) == 0, "chunk must be a whole number of iterations");
+static_assert(kChunk <= 65536, "pass 2 queue entries hold a 16-bit offset within the chunk");
 
 // Device view of LumaTensor.  The pointer fields are declared in the global
 // address space so loads and stores through them compile to global_* (not
