@@ -53,6 +53,27 @@ def _ptr(t: Optional[torch.Tensor]) -> int:
     return 0 if t is None else t.data_ptr()
 
 
+_ARENA_ALIGN = 128   # int16 elements: every Q tensor starts on a 256-byte boundary
+
+
+def state_arena(params, device):
+    """Q_m and Q_w for the given (dense) parameters as views of ONE int16
+    allocation: parameter i's Q_m, then its Q_w, each 256-byte aligned and
+    with the parameter's shape and strides.  Two allocations replace two
+    per parameter, and a checkpoint of the state serialises one storage."""
+    sizes = [-(-p.numel() // _ARENA_ALIGN) * _ARENA_ALIGN for p in params]
+    arena = torch.empty(max(2 * sum(sizes), 1), dtype=torch.int16, device=device)
+    storage = arena.untyped_storage()
+    views, off = [], 0
+    for p, n in zip(params, sizes):
+        qm = torch.empty(0, dtype=torch.int16, device=device).set_(storage, off, p.shape, p.stride())
+        qw = torch.empty(0, dtype=torch.int16, device=device).set_(storage, off + n, p.shape,
+                                                                 p.stride())
+        views.append((qm, qw))
+        off += 2 * n
+    return views
+
+
 class _Engine:
     """Device-side tables of one optimizer: tensor, chunk and group tables and
     the chunk-maxima workspace.  Tables are uploaded only when their contents
@@ -593,6 +614,14 @@ class LUMA(Optimizer):
                 raise engine._capture_error("the set of parameters with optimizer state")
             for state, slot in zip(fresh, engine.new_slots(len(fresh))):
                 state["_slot"] = slot
+        no_q = [(self.state[w[1]], w[2]) for w in work if "Q_m" not in self.state[w[1]]]
+        if no_q:
+            if capturing:
+                raise engine._capture_error("the set of parameters with optimizer state")
+            for (state, _), (qm, qw) in zip(no_q, state_arena([p for _, p in no_q],
+                                                              engine.device)):
+                state["Q_m"] = qm
+                state["Q_w"] = qw
         rows, states = [], []
         for gi, p, param, grad, pidx in work:
             self._get_engine(param.device)   # one device for all parameters
@@ -601,9 +630,6 @@ class LUMA(Optimizer):
                 state["step"] = 0
                 state["param_id"] = pidx
             states.append(state)
-            if "Q_m" not in state:
-                state["Q_m"] = torch.empty_like(param, dtype=torch.int16)
-                state["Q_w"] = torch.empty_like(param, dtype=torch.int16)
             code = _GRAD_CODES.get(grad.dtype)
             if code is None:
                 grad = grad.float()

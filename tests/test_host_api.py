@@ -140,3 +140,23 @@ def test_sparse_grad_rejected():
 def test_package_exports():
     assert luma_amd.__all__ == ["LUMA", "get_kernel_config"]
     assert "CHUNK_ELEMS" in luma_amd.get_kernel_config()
+
+
+def test_state_arena_layout():
+    """Q_m / Q_w views of one allocation: parameter shapes and strides
+    (channels_last included), 256-byte aligned offsets, no overlap."""
+    from luma_amd.optimizer import state_arena
+    ps = [torch.zeros(3, 5), torch.zeros(1), torch.zeros(2, 3, 4, 5).to(memory_format=torch.channels_last),
+          torch.zeros(300)]
+    views = state_arena(ps, torch.device("cpu"))
+    base = views[0][0].untyped_storage().data_ptr()
+    for p, (qm, qw) in zip(ps, views):
+        for q in (qm, qw):
+            assert q.dtype == torch.int16 and q.shape == p.shape and q.stride() == p.stride()
+            assert q.untyped_storage().data_ptr() == base
+            assert (q.data_ptr() - base) % 256 == 0
+    for i, (qm, qw) in enumerate(views):
+        qm.fill_(i + 1)
+        qw.fill_(-(i + 1))
+    for i, (qm, qw) in enumerate(views):
+        assert (qm == i + 1).all() and (qw == -(i + 1)).all()
