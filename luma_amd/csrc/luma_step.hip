@@ -4,12 +4,16 @@
 // One step over every parameter is three launches on the caller's stream:
 //   pass 1   (grid = chunks)  decode Q_m/Q_w with the old grid, EMA with the
 //                             gradient, max |m'| and max v' per chunk;
-//   finalize (grid = tensors) reduce the chunk maxima to S_m', S_v' and derive
-//                             the new grid in float64 (functional.py:282-292);
+//   finalize (grid = tensors) reduce the chunk maxima to S_m', S_v', derive
+//                             the new grid in float64 (functional.py:282-292),
+//                             advance the tensor's step count and derive the
+//                             step's scalars (functional.py:209-213, 262-264);
 //   pass 2   (grid = chunks)  recompute m', v' bit-identically, AdamW update of
 //                             the parameter, LogSR re-quantisation on the new
 //                             grid (functional.py:278-279, 293-295).
-// Nothing is materialised between the passes except 8 bytes per chunk.
+// Nothing is materialised between the passes except 8 bytes per chunk.  With
+// GradScaler's scaling (LumaScaling) every kernel unscales the gradients as
+// it loads them, and returns at once when the overflow flag is set.
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
