@@ -248,7 +248,7 @@ class _Plan:
     """
 
     __slots__ = ("all_params", "has_grad", "work_idx", "params", "grads", "gdtypes", "strides",
-                 "device_index", "states", "tt")
+                 "numels", "device_index", "states", "tt")
 
     def __init__(self, param_groups, work, rows, states, tt):
         self.all_params = [p for g in param_groups for p in g["params"]]
@@ -257,7 +257,8 @@ class _Plan:
         self.params = [r[0] for r in rows]
         self.grads = [r[1] for r in rows]
         self.gdtypes = [g.dtype for g in self.grads]
-        self.strides = [g.stride() for g in self.grads]
+        self.strides = [g.stride() for g in self.grads]   # == the parameter's strides
+        self.numels = [p.numel() for p in self.params]
         self.device_index = self.params[0].get_device()
         self.states = states
         self.tt = tt
@@ -281,16 +282,24 @@ class _Plan:
         wg = [grads[i] for i in self.work_idx]
         dev = self.device_index
         for i, (g, old) in enumerate(zip(wg, self.grads)):
-            if g is old:
+            if g is old and g.dtype is self.gdtypes[i]:
                 continue
             if (type(g) is not torch.Tensor or g.dtype is not self.gdtypes[i]
-                    or g.stride() != self.strides[i] or g.get_device() != dev):
+                    or g.stride() != self.strides[i] or g.numel() != self.numels[i]
+                    or g.get_device() != dev):
+                return False
+        n = len(wg)
+        pptr = np.fromiter(map(torch.Tensor.data_ptr, self.params), dtype=np.uint64, count=n)
+        # a parameter whose storage was replaced (p.data = ...) must still be a
+        # dense float32 tensor of the planned size and layout
+        for i in np.nonzero(pptr != self.tt["param"])[0].tolist():
+            p = self.params[i]
+            if (p.dtype is not torch.float32 or p.numel() != self.numels[i]
+                    or p.stride() != self.strides[i] or p.get_device() != dev):
                 return False
         self.grads = wg
-        n = len(wg)
         self.tt["grad"] = np.fromiter(map(torch.Tensor.data_ptr, wg), dtype=np.uint64, count=n)
-        self.tt["param"] = np.fromiter(map(torch.Tensor.data_ptr, self.params), dtype=np.uint64,
-                                       count=n)
+        self.tt["param"] = pptr
         return True
 
 
@@ -630,6 +639,14 @@ class LUMA(Optimizer):
                 state["step"] = 0
                 state["param_id"] = pidx
             states.append(state)
+            for key in ("Q_m", "Q_w"):
+                q = state[key]
+                if (q.dtype != torch.int16 or q.shape != param.shape
+                        or q.stride() != param.stride() or q.device != param.device):
+                    raise ValueError(
+                        f"LUMA: state {key!r} ({tuple(q.shape)}, {q.dtype}) does not match its "
+                        f"parameter ({tuple(param.shape)}); was the parameter replaced after "
+                        "the optimizer state was created?")
             code = _GRAD_CODES.get(grad.dtype)
             if code is None:
                 grad = grad.float()

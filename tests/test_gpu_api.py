@@ -458,3 +458,37 @@ def test_grad_scaler_fp16():
         scaler.step(opt)
         scaler.update()
     assert loss.item() < init * 0.5
+
+
+# ── parameters replaced between steps (the re-used step plan re-checks them) ─
+
+def test_replaced_parameter_storage():
+    torch.manual_seed(0)
+    model = nn.Linear(64, 32).to(DEV)
+    opt = LUMA(model.parameters(), lr=1e-3)
+    x = torch.randn(4, 64, device=DEV)
+    for _ in range(2):
+        opt.zero_grad()
+        model(x).sum().backward()
+        opt.step()
+    torch.cuda.synchronize()
+    # same layout, new storage: the step updates the new storage
+    new_w = model.weight.detach().clone()
+    model.weight.data = new_w
+    before = new_w.clone()
+    opt.zero_grad()
+    model(x).sum().backward()
+    opt.step()
+    torch.cuda.synchronize()
+    assert model.weight.data_ptr() == new_w.data_ptr() and not torch.equal(new_w, before)
+    # reduced precision: rejected, nothing launched
+    model.weight.data = model.weight.detach().half()
+    opt.zero_grad()
+    model.weight.grad = torch.zeros_like(model.weight)
+    with pytest.raises(ValueError, match="float32"):
+        opt.step()
+    # a resized parameter no longer matches its codes: rejected
+    model.weight.data = torch.zeros(32, 65, device=DEV)
+    model.weight.grad = torch.zeros_like(model.weight)
+    with pytest.raises(ValueError, match="does not match"):
+        opt.step()
