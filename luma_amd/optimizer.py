@@ -512,6 +512,10 @@ class LUMA(Optimizer):
                     continue
                 param = self._unwrap_tensor(p)
                 engine = self._get_engine(param.device)
+                if state["Q_m"].shape != param.shape or state["Q_w"].shape != param.shape:
+                    raise ValueError("LUMA.export_adamw_state: the codes do not match their "
+                                     f"parameter ({tuple(state['Q_m'].shape)} vs "
+                                     f"{tuple(param.shape)})")
                 exp_avg = torch.empty_like(param, dtype=torch.float32)
                 exp_avg_sq = torch.empty_like(param, dtype=torch.float32)
                 engine.decode(state["Q_m"], state["Q_w"], state["_slot"], eps,
