@@ -342,8 +342,26 @@ __device__ __forceinline__ float grad_hi(uint32_t w) {
   return __half2float(__ushort_as_half((uint16_t)(w >> 16)));
 }
 
+// Cache policy of the streams.  The gradients, and pass 2's parameters, are
+// touched once per step: they are loaded (and stored) non-temporally, so that
+// they are the first lines L2 evicts.  The codes keep the normal policy:
+// pass 2 overwrites some of its new codes again after the exact path has
+// run for them, a few iterations later, and those late 2-byte stores are
+// cheap while the line is still in L2 but cost a partial-line write-back to
+// HBM once it has been evicted.
+template <typename V>
+__device__ __forceinline__ V load_stream(const LUMA_GLOBAL V *p) {
+  return __builtin_nontemporal_load(p);
+}
+
+template <typename V>
+__device__ __forceinline__ void store_stream(V v, LUMA_GLOBAL V *p) {
+  __builtin_nontemporal_store(v, p);
+}
+
 // Load the codes and gradients of elements e0 .. e0+7 (n of them valid).
-template <int GD>
+// STREAM: the gradient vectors are loaded non-temporally.
+template <int GD, bool STREAM = false>
 __device__ __forceinline__ void load_group(const Tensor &T, int64_t e0, int n, bool vec, Group8 &G) {
   if (vec) {
     const vu4 a = *(const LUMA_GLOBAL vu4 *)(T.q_m + e0);
@@ -357,12 +375,14 @@ __device__ __forceinline__ void load_group(const Tensor &T, int64_t e0, int n, b
     unpack_u16(b.z, G.qw[4], G.qw[5]);
     unpack_u16(b.w, G.qw[6], G.qw[7]);
     if (GD == LUMA_GRAD_F32) {
-      const vf4 g0 = *(const LUMA_GLOBAL vf4 *)((const LUMA_GLOBAL float *)T.grad + e0);
-      const vf4 g1 = *(const LUMA_GLOBAL vf4 *)((const LUMA_GLOBAL float *)T.grad + e0 + 4);
+      const LUMA_GLOBAL vf4 *gp = (const LUMA_GLOBAL vf4 *)((const LUMA_GLOBAL float *)T.grad + e0);
+      const vf4 g0 = STREAM ? load_stream(gp) : gp[0];
+      const vf4 g1 = STREAM ? load_stream(gp + 1) : gp[1];
       G.g[0] = g0.x; G.g[1] = g0.y; G.g[2] = g0.z; G.g[3] = g0.w;
       G.g[4] = g1.x; G.g[5] = g1.y; G.g[6] = g1.z; G.g[7] = g1.w;
     } else {
-      const vu4 gw = *(const LUMA_GLOBAL vu4 *)((const LUMA_GLOBAL uint16_t *)T.grad + e0);
+      const LUMA_GLOBAL vu4 *gp = (const LUMA_GLOBAL vu4 *)((const LUMA_GLOBAL uint16_t *)T.grad + e0);
+      const vu4 gw = STREAM ? load_stream(gp) : gp[0];
       G.g[0] = grad_lo<GD>(gw.x); G.g[1] = grad_hi<GD>(gw.x);
       G.g[2] = grad_lo<GD>(gw.y); G.g[3] = grad_hi<GD>(gw.y);
       G.g[4] = grad_lo<GD>(gw.z); G.g[5] = grad_hi<GD>(gw.z);
@@ -786,12 +806,12 @@ __device__ __forceinline__ void launder(P2Const &C) {
 template <int GD, bool INJ, bool SMALL, bool SCALED, bool FULL>
 __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, int64_t e0, int n,
                                             uint32_t k0, uint32_t k1, Group8 &Q, U4 &coarse) {
-  load_group<GD>(T, e0, n, FULL, Q);
+  load_group<GD, true>(T, e0, n, FULL, Q);
   unscale_group<GD, SCALED>(Q, C.inv);
-  float p[kVec], zm0[kVec], zw0[kVec];
+  float p[kVec];
   if (FULL) {
-    const vf4 p0 = *(const LUMA_GLOBAL vf4 *)(T.param + e0);
-    const vf4 p1 = *(const LUMA_GLOBAL vf4 *)(T.param + e0 + 4);
+    const vf4 p0 = load_stream((const LUMA_GLOBAL vf4 *)(T.param + e0));
+    const vf4 p1 = load_stream((const LUMA_GLOBAL vf4 *)(T.param + e0 + 4));
     p[0] = p0.x; p[1] = p0.y; p[2] = p0.z; p[3] = p0.w;
     p[4] = p1.x; p[5] = p1.y; p[6] = p1.z; p[7] = p1.w;
   } else {
@@ -853,8 +873,8 @@ __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, i
     vf4 p0, p1;
     p0.x = p[0]; p0.y = p[1]; p0.z = p[2]; p0.w = p[3];
     p1.x = p[4]; p1.y = p[5]; p1.z = p[6]; p1.w = p[7];
-    *(LUMA_GLOBAL vf4 *)(T.param + e0) = p0;
-    *(LUMA_GLOBAL vf4 *)(T.param + e0 + 4) = p1;
+    store_stream(p0, (LUMA_GLOBAL vf4 *)(T.param + e0));
+    store_stream(p1, (LUMA_GLOBAL vf4 *)(T.param + e0 + 4));
     vu4 a, b;
     a.x = (uint32_t)(om[0] & 0xFFFF) | ((uint32_t)om[1] << 16);
     a.y = (uint32_t)(om[2] & 0xFFFF) | ((uint32_t)om[3] << 16);
