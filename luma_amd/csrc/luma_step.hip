@@ -359,6 +359,47 @@ __device__ __forceinline__ void store_stream(V v, LUMA_GLOBAL V *p) {
   __builtin_nontemporal_store(v, p);
 }
 
+// The 16-byte words holding the codes and gradients of 8 consecutive
+// elements, as loaded (g1: float32 gradients only).
+struct Raw8 {
+  vu4 qm, qw, g0, g1;
+};
+
+template <int GD>
+__device__ __forceinline__ void load_raw(const Tensor &T, int64_t e0, Raw8 &r) {
+  r.qm = *(const LUMA_GLOBAL vu4 *)(T.q_m + e0);
+  r.qw = *(const LUMA_GLOBAL vu4 *)(T.q_w + e0);
+  if (GD == LUMA_GRAD_F32) {
+    r.g0 = *(const LUMA_GLOBAL vu4 *)((const LUMA_GLOBAL float *)T.grad + e0);
+    r.g1 = *(const LUMA_GLOBAL vu4 *)((const LUMA_GLOBAL float *)T.grad + e0 + 4);
+  } else {
+    r.g0 = *(const LUMA_GLOBAL vu4 *)((const LUMA_GLOBAL uint16_t *)T.grad + e0);
+  }
+}
+
+template <int GD>
+__device__ __forceinline__ void unpack_raw(const Raw8 &r, Group8 &G) {
+  unpack_i16(r.qm.x, G.qm[0], G.qm[1]);
+  unpack_i16(r.qm.y, G.qm[2], G.qm[3]);
+  unpack_i16(r.qm.z, G.qm[4], G.qm[5]);
+  unpack_i16(r.qm.w, G.qm[6], G.qm[7]);
+  unpack_u16(r.qw.x, G.qw[0], G.qw[1]);
+  unpack_u16(r.qw.y, G.qw[2], G.qw[3]);
+  unpack_u16(r.qw.z, G.qw[4], G.qw[5]);
+  unpack_u16(r.qw.w, G.qw[6], G.qw[7]);
+  if (GD == LUMA_GRAD_F32) {
+    G.g[0] = __uint_as_float(r.g0.x); G.g[1] = __uint_as_float(r.g0.y);
+    G.g[2] = __uint_as_float(r.g0.z); G.g[3] = __uint_as_float(r.g0.w);
+    G.g[4] = __uint_as_float(r.g1.x); G.g[5] = __uint_as_float(r.g1.y);
+    G.g[6] = __uint_as_float(r.g1.z); G.g[7] = __uint_as_float(r.g1.w);
+  } else {
+    G.g[0] = grad_lo<GD>(r.g0.x); G.g[1] = grad_hi<GD>(r.g0.x);
+    G.g[2] = grad_lo<GD>(r.g0.y); G.g[3] = grad_hi<GD>(r.g0.y);
+    G.g[4] = grad_lo<GD>(r.g0.z); G.g[5] = grad_hi<GD>(r.g0.z);
+    G.g[6] = grad_lo<GD>(r.g0.w); G.g[7] = grad_hi<GD>(r.g0.w);
+  }
+}
+
 // Load the codes and gradients of elements e0 .. e0+7 (n of them valid).
 // STREAM: the gradient vectors are loaded non-temporally.
 template <int GD, bool STREAM = false>
@@ -470,11 +511,15 @@ __device__ __noinline__ uint64_t exact_pair_w(int qw, float g, const LUMA_GLOBAL
 // are appended without atomics (pass 1: ballot/mbcnt per element slot;
 // pass 2: one wave prefix sum per iteration) and run through the exact path
 // 64 at a time, one per lane, so the exact path runs at full SIMD width.
-// Pass 1 appends up to 8 x 64 entries before it drains its queue.  Pass 2
-// drains below 64 after every iteration and appends at most 192 in one
-// (more is handled in place), so its queues never exceed 255 entries.
+// Pass 1 appends up to 8 x 64 entries before it drains its queue.  Pass 2's
+// queues are rings of 256 entries drained oldest first, 64 at a time, after
+// every iteration; an iteration whose entries would not fit runs them in
+// place.  Oldest first, because the exact codes are stored into lines that
+// the fast path wrote some iterations earlier, and a younger line is more
+// likely to still be in L2.
 constexpr int kQueueCap = kVec * 64 + 64;
 constexpr int kQueueCap2 = 256;
+static_assert((kQueueCap2 & (kQueueCap2 - 1)) == 0, "pass 2 queues are power-of-two rings");
 
 // Keeps a wave-uniform value in a VGPR.  On gfx950 a VALU instruction with
 // an SGPR source operand issues at about half the rate of one whose sources
@@ -546,11 +591,21 @@ __device__ __forceinline__ void unscale_group(Group8 &G, float inv) {
   for (int j = 0; j < kVec; ++j) G.g[j] = unscale<GD>(G.g[j], inv);
 }
 
+// FULL: the group is whole and aligned, and raw already holds its codes
+// and gradients; the iteration reloads raw with the group it will process
+// next (en: elements en .. en+7), so that the load overlaps this group's
+// arithmetic.
 template <int GD, bool SMALL, bool SCALED, bool FULL>
 __device__ __forceinline__ void p1_iter(const Tensor &T, const P1Const &K, int64_t e0, int n,
-                                        uint32_t (&am)[kVec], uint32_t (&av)[kVec]) {
+                                        Raw8 &raw, int64_t en, uint32_t (&am)[kVec],
+                                        uint32_t (&av)[kVec]) {
   Group8 G;
-  load_group<GD>(T, e0, n, FULL, G);
+  if (FULL) {
+    unpack_raw<GD>(raw, G);
+    load_raw<GD>(T, en, raw);
+  } else {
+    load_group<GD>(T, e0, n, false, G);
+  }
   unscale_group<GD, SCALED>(G, K.inv);
 #pragma unroll
   for (int j = 0; j < kVec; ++j) {
@@ -602,18 +657,9 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     exm = nan_max(exm, fabsf(e.x));
     exv = nan_max(exv, e.y);
   };
-  // Every lane runs the same number of iterations (lanes past the end carry
-  // n = 0), so the ballots and the queue length stay uniform across the wave.
-  const int n_it = (int)((end - beg + kThreads * kVec - 1) / (kThreads * kVec));
-  for (int it = 0; it < n_it; ++it) {
-    const int64_t e0 = beg + ((int64_t)it * kThreads + threadIdx.x) * kVec;
-    const int64_t rem = end - e0;
-    const int n = rem <= 0 ? 0 : (rem < kVec ? (int)rem : kVec);
-    uint32_t am[kVec], av[kVec];
-    if (vec_ok && n == kVec)
-      p1_iter<GD, SMALL, SCALED, true>(T, K, e0, n, am, av);
-    else
-      p1_iter<GD, SMALL, SCALED, false>(T, K, e0, n, am, av);
+  // The fast values of one iteration: fold them into the wave maximum and
+  // queue the candidates.
+  auto take = [&](int64_t e0, int n, const uint32_t (&am)[kVec], const uint32_t (&av)[kVec]) {
     const uint32_t im = max(max(max(am[0], am[1]), max(am[2], am[3])),
                             max(max(am[4], am[5]), max(am[6], am[7])));
     const uint32_t iv = max(max(max(av[0], av[1]), max(av[2], av[3])),
@@ -622,9 +668,9 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
       // t = 1: no decode, the fast m', v' are the exact ones
       xbm = max(xbm, im);
       xbv = max(xbv, iv);
-      continue;
+      return;
     }
-    if (!__ballot(im >= Tm || iv >= Tv)) continue;
+    if (!__ballot(im >= Tm || iv >= Tv)) return;
     // some lane reached the threshold: raise the wave maximum, then queue
     // the elements that still reach the new threshold
     Mm = max(Mm, wave_max_u32(im));
@@ -644,6 +690,36 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
       qlen -= 64;
       run(queue[qlen + lane]);
     }
+  };
+  // Every lane runs the same number of iterations (lanes past the end carry
+  // n = 0), so the ballots and the queue length stay uniform across the wave.
+  constexpr int64_t kStride = (int64_t)kThreads * kVec;
+  const int n_it = (int)((end - beg + kStride - 1) / kStride);
+  // Iterations in which every lane's group is whole run in a loop of their
+  // own that loads each group one iteration ahead: raw holds the codes and
+  // gradients of the lane's next group (the current one again after the last
+  // whole group, so that every iteration issues the same loads).
+  const int n_whole = vec_ok ? (int)((end - beg) / kStride) : 0;
+  int it = 0;
+  if (n_whole > 0) {
+    Raw8 raw;
+    load_raw<GD>(T, beg + (int64_t)threadIdx.x * kVec, raw);
+    for (; it < n_whole; ++it) {
+      const int64_t e0 = beg + ((int64_t)it * kThreads + threadIdx.x) * kVec;
+      const int64_t en = end - e0 - kStride >= kVec ? e0 + kStride : e0;
+      uint32_t am[kVec], av[kVec];
+      p1_iter<GD, SMALL, SCALED, true>(T, K, e0, kVec, raw, en, am, av);
+      take(e0, kVec, am, av);
+    }
+  }
+  for (; it < n_it; ++it) {
+    const int64_t e0 = beg + ((int64_t)it * kThreads + threadIdx.x) * kVec;
+    const int64_t rem = end - e0;
+    const int n = rem <= 0 ? 0 : (rem < kVec ? (int)rem : kVec);
+    uint32_t am[kVec], av[kVec];
+    Raw8 unused;
+    p1_iter<GD, SMALL, SCALED, false>(T, K, e0, n, unused, e0, am, av);
+    take(e0, n, am, av);
   }
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   if (lane < qlen) run(queue[lane]);
@@ -667,7 +743,7 @@ __device__ __forceinline__ void pass1_dispatch(const Tensor &T, const Hyper &h,
   }
 }
 
-__global__ __launch_bounds__(kThreads) void pass1_fast_kernel(StepSrc src,
+__global__ __launch_bounds__(kThreads, 4) void pass1_fast_kernel(StepSrc src,
                                                               float *__restrict__ partials) {
   if (skip_step(src)) return;
   Tensor T;
@@ -950,7 +1026,8 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   const bool vec_ok = tensor_vec_ok(T);
   const uint32_t lane = lane_id();
   uint4 *queue_m = queue, *queue_w = queue + kQueueCap2;
-  uint32_t qlen_m = 0, qlen_w = 0;
+  uint32_t qlen_m = 0, qlen_w = 0;   // pending entries
+  uint32_t head_m = 0, head_w = 0;   // ring position of the oldest
   // Queue entry: x = chunk offset | old code << 16, y = the uniform's top 8
   // bits (Philox; its low 16 bits come from the fine block), z = the
   // gradient as float32 bits (no second read of HBM).  The fast codes were
@@ -1017,10 +1094,10 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
                         0u);
     };
     if (qlen_m + tot_m <= (uint32_t)kQueueCap2) {
-      uint32_t pos = qlen_m + (excl & 0xFFFFu);
+      uint32_t pos = head_m + qlen_m + (excl & 0xFFFFu);
       for (uint32_t f = fm; f != 0u; f &= f - 1u) {
         const uint32_t k = (uint32_t)__builtin_ctz(f);
-        queue_m[pos++] = entry(k, sel8(Q.qm, k), 0u);
+        queue_m[pos++ & (kQueueCap2 - 1)] = entry(k, sel8(Q.qm, k), 0u);
       }
       qlen_m += tot_m;
     } else {
@@ -1031,10 +1108,10 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
       }
     }
     if (qlen_w + tot_w <= (uint32_t)kQueueCap2) {
-      uint32_t pos = qlen_w + (excl >> 16);
+      uint32_t pos = head_w + qlen_w + (excl >> 16);
       for (uint32_t f = fw; f != 0u; f &= f - 1u) {
         const uint32_t k = (uint32_t)__builtin_ctz(f);
-        queue_w[pos++] = entry(k, sel8(Q.qw, k), 8u);
+        queue_w[pos++ & (kQueueCap2 - 1)] = entry(k, sel8(Q.qw, k), 8u);
       }
       qlen_w += tot_w;
     } else {
@@ -1045,17 +1122,19 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     }
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     while (qlen_m >= 64) {
+      run_m(queue_m[(head_m + lane) & (kQueueCap2 - 1)]);
+      head_m += 64;
       qlen_m -= 64;
-      run_m(queue_m[qlen_m + lane]);
     }
     while (qlen_w >= 64) {
+      run_w(queue_w[(head_w + lane) & (kQueueCap2 - 1)]);
+      head_w += 64;
       qlen_w -= 64;
-      run_w(queue_w[qlen_w + lane]);
     }
   }
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  if (lane < qlen_m) run_m(queue_m[lane]);
-  if (lane < qlen_w) run_w(queue_w[lane]);
+  if (lane < qlen_m) run_m(queue_m[(head_m + lane) & (kQueueCap2 - 1)]);
+  if (lane < qlen_w) run_w(queue_w[(head_w + lane) & (kQueueCap2 - 1)]);
 }
 
 template <int GD, bool SCALED>
