@@ -138,16 +138,18 @@ struct FastEma {
   float am;   // |m| decoded (for the error bound)
 };
 
-// ndw = -dw; sign = 0x80000000 (both passed in so that callers can keep them
-// in VGPRs).  The preconditioner argument is formed as q * (-dw), which is
-// exactly -(the exact path's float32 q * dw).
+// ndw = -dw, nbias = 2^23 dw; sign = 0x80000000 (passed in so that callers
+// can keep them in VGPRs).  qw holds the bits of the float 2^23 + q (code q
+// in the low 16 bits), so the preconditioner argument
+// fma(2^23 + q, -dw, 2^23 dw) = RN(q * -dw) is exactly -(the exact path's
+// float32 q * dw), formed without a v_cvt.
 //
 // PRECISE_V: form e^-x with the two-word argument reduction (pass 2, whose
 // parameter update and code bounds use v'); pass 1 only needs the cheaper
 // single exp2, whose error its max-tracking bound covers (x * u term).
 template <bool SMALL_M, bool PRECISE_V>
 __device__ __forceinline__ FastEma fast_ema(int qm, int qw, float g, float dm, float ndw,
-                                            float iwmin, float eps, float b1, float omb1,
+                                            float nbias, float iwmin, float eps, float b1, float omb1,
                                             float b2, float omb2, uint32_t sign) {
   FastEma r;
   const float qf = (float)qm;
@@ -155,7 +157,7 @@ __device__ __forceinline__ FastEma fast_ema(int qm, int qw, float g, float dm, f
   const float e = SMALL_M ? fast_expm1_small(x) : fast_expm1_general(x);
   const float m = __uint_as_float(__float_as_uint(e) | (__float_as_uint(qf) & sign));
   r.am = e;
-  const float nx = (float)(qw & 0xFFFF) * ndw;
+  const float nx = fmaf(__int_as_float(qw), ndw, nbias);
   // w_min / w = e^-x: 2^a with a = RN(-x*log2e), times e^d, where
   // d = -x - a*ln2 is formed with a two-word ln2, so the rounding of the
   // exponent argument does not scale with x.

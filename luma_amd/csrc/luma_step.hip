@@ -316,7 +316,7 @@ __global__ __launch_bounds__(kThreads) void pass2_exact_kernel(StepSrc src, uint
 
 struct Group8 {
   int qm[kVec];   // signed momentum codes
-  int qw[kVec];   // unsigned preconditioner codes
+  int qw[kVec];   // unsigned preconditioner codes, as kCodeFloat | code
   float g[kVec];  // gradient promoted to float32
 };
 
@@ -325,9 +325,14 @@ __device__ __forceinline__ void unpack_i16(uint32_t w, int &lo, int &hi) {
   hi = (int)w >> 16;
 }
 
+// Preconditioner codes are kept as the bits of the float 2^23 + q
+// (kCodeFloat | q): their decode then needs no v_cvt, see fast_ema.  The
+// low 16 bits are the code.
+constexpr uint32_t kCodeFloat = 0x4B000000u;
+
 __device__ __forceinline__ void unpack_u16(uint32_t w, int &lo, int &hi) {
-  lo = (int)(w & 0xFFFFu);
-  hi = (int)(w >> 16);
+  lo = (int)((w & 0xFFFFu) | kCodeFloat);
+  hi = (int)((w >> 16) | kCodeFloat);
 }
 
 template <int GD>
@@ -434,7 +439,7 @@ __device__ __forceinline__ void load_group(const Tensor &T, int64_t e0, int n, b
     for (int j = 0; j < kVec; ++j) {
       const bool ok = j < n;
       G.qm[j] = ok ? (int)T.q_m[e0 + j] : 0;
-      G.qw[j] = ok ? (int)(uint16_t)T.q_w[e0 + j] : 0;
+      G.qw[j] = (int)((ok ? (uint32_t)(uint16_t)T.q_w[e0 + j] : 0u) | kCodeFloat);
       G.g[j] = ok ? load_grad(T.grad, e0 + j, GD) : 0.0f;
     }
   }
@@ -578,7 +583,7 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 // above +Inf); invalid elements of a partial group give 0.
 // Constants of the pass-1 loop, kept in VGPRs (see in_vgpr).
 struct P1Const {
-  float dm, ndw, iwmin, eps, b1, omb1, b2, omb2;
+  float dm, ndw, nbias, iwmin, eps, b1, omb1, b2, omb2;
   float inv;   // inverse gradient scale (SCALED)
   uint32_t sign;
 };
@@ -609,7 +614,7 @@ __device__ __forceinline__ void p1_iter(const Tensor &T, const P1Const &K, int64
   unscale_group<GD, SCALED>(G, K.inv);
 #pragma unroll
   for (int j = 0; j < kVec; ++j) {
-    const FastEma f = fast_ema<SMALL, false>(G.qm[j], G.qw[j], G.g[j], K.dm, K.ndw, K.iwmin,
+    const FastEma f = fast_ema<SMALL, false>(G.qm[j], G.qw[j], G.g[j], K.dm, K.ndw, K.nbias, K.iwmin,
                                              K.eps, K.b1, K.omb1, K.b2, K.omb2, K.sign);
     am[j] = __float_as_uint(f.mn) & 0x7FFFFFFFu;
     av[j] = __float_as_uint(f.vn) & 0x7FFFFFFFu;
@@ -632,6 +637,7 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   P1Const K;
   K.dm = in_vgpr(D.dm);
   K.ndw = in_vgpr(-D.dw);
+  K.nbias = in_vgpr(8388608.0f * D.dw);
   K.iwmin = in_vgpr(D.iwmin);
   K.eps = in_vgpr(D.eps);
   K.b1 = in_vgpr(h.beta1);
@@ -804,20 +810,26 @@ __device__ __forceinline__ T sel8(const T (&a)[kVec], uint32_t k) {
 // Certified LogSR decision (see luma_fast.h): with z = y + 1 - c, c the
 // middle of the uniform's interval, the code is floor(z); it is certain
 // when [z - e, z + e] holds no integer, e bounding |z - z_exact| plus the
-// interval's half width.  Given h = 0.5 - e, returns 1 when not certain:
-// the sign bit of max(h - |fract(z) - 0.5|, -1), so that NaN counts as
-// uncertain (fmax drops it) -- computed without compares, whose lane-mask
-// results cost more than plain VALU on gfx950.
-__device__ __forceinline__ uint32_t unsure(float z, float h) {
-  const float d = fmaxf(h - fabsf(__builtin_amdgcn_fractf(z) - 0.5f), -1.0f);
+// interval's half width.  Given fz = fract(z) and h = 0.5 - e, returns 1
+// when not certain: the sign bit of max(h - |fz - 0.5|, -1), so that NaN
+// counts as uncertain (fmax drops it) -- computed without compares, whose
+// lane-mask results cost more than plain VALU on gfx950.
+__device__ __forceinline__ uint32_t unsure(float fz, float h) {
+  const float d = fmaxf(h - fabsf(fz - 0.5f), -1.0f);
   return __float_as_uint(d) >> 31;
 }
+
+// Adding 1.5 * 2^23 to an integer-valued float k with |k| < 2^22 gives a
+// float whose low 16 bits are k's two's complement 16-bit code: one
+// dual-issued add instead of a single-issued v_cvt_i32_f32.
+constexpr float kCodeBias = 12582912.0f;
 
 // Per-tensor constants of pass 2.
 struct P2Const {
   DecodeK D;
   uint32_t pk0, pk1, pm0, pm1;  // Philox key and multipliers
   float ndw;                    // -dw of the old grid (decode)
+  float nbias;                  // 2^23 dw: fma(2^23 + q, -dw, nbias) = q * -dw exactly
   float nk1, nk2, hk3, nk7, hk8;   // -k1, -k2, 0.5 - k3, -k7, 0.5 - k8
   float b1, omb1, b2, omb2, decay, neg_eta, eps;
   float isbc2, eps_u;       // 1 / (sqrt(bc2) (-eta)), eps / (-eta)
@@ -865,6 +877,7 @@ __device__ __forceinline__ void launder(P2Const &C) {
   C.k8 = in_vgpr(C.k8);
   C.kmax_m = in_vgpr(C.kmax_m);
   C.ndw = in_vgpr(C.ndw);
+  C.nbias = in_vgpr(C.nbias);
   C.nk1 = in_vgpr(C.nk1);
   C.nk2 = in_vgpr(C.nk2);
   C.hk3 = in_vgpr(C.hk3);
@@ -911,11 +924,11 @@ __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, i
       zmu_w[j] = fmaf((float)u4_byte(coarse, 2 * j + 1), -1.0f / 256.0f, C.zoff);
     }
   }
-  int om[kVec], ow[kVec];
+  uint32_t om[kVec], ow[kVec];   // codes in the low 16 bits (kCodeBias)
   uint32_t flags = 0;
 #pragma unroll
   for (int j = 0; j < kVec; ++j) {
-    const FastEma f = fast_ema<SMALL, true>(Q.qm[j], Q.qw[j], Q.g[j], C.D.dm, C.ndw, C.D.iwmin,
+    const FastEma f = fast_ema<SMALL, true>(Q.qm[j], Q.qw[j], Q.g[j], C.D.dm, C.ndw, C.nbias, C.D.iwmin,
                                             C.D.eps, C.b1, C.omb1, C.b2, C.omb2, C.sign);
     const float s = __builtin_amdgcn_sqrtf(f.vn);
     // AdamW update (functional.py:278-279), within 1e-6 of the exact path:
@@ -928,9 +941,14 @@ __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, i
     const float L = SMALL ? fast_log1p_small(am) : fast_log1p_general(am);
     const float zm = fmaf(L, C.idm, zmu_m[j]);
     const float hm = fmaf(f.am, C.nk1, fmaf(zm, C.nk2, C.hk3));    // 0.5 - e
-    om[j] = (int)__uint_as_float(
-        __float_as_uint(__builtin_amdgcn_fmed3f(floorf(zm), 0.0f, C.kmax_m)) |
+    // floor(z) as z - fract(z) (exact for |z| < 2^23; v_fract is needed for
+    // the certification anyway, and the subtraction dual-issues where
+    // v_floor does not)
+    const float fzm = __builtin_amdgcn_fractf(zm);
+    const float cm = __uint_as_float(
+        __float_as_uint(__builtin_amdgcn_fmed3f(zm - fzm, 0.0f, C.kmax_m)) |
         (__float_as_uint(f.mn) & C.sign));
+    om[j] = __float_as_uint(cm + kCodeBias);   // low 16 bits: the signed code
     // preconditioner code: x = w_min t, clamped to the exact path's w range;
     // y = -log2(x) ln2/dw = (e + log2 mant) C, with e C exact (16-bit C_hi)
     // so that only O(|C|) terms round.  delta_w = 0 gives C = 0: code 0.
@@ -938,11 +956,14 @@ __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, i
     const float ef = (float)__builtin_amdgcn_frexp_expf(x);
     const float l2 = __builtin_amdgcn_logf(__builtin_amdgcn_frexp_mantf(x));
     const float A = ef * C.ch;
-    const float zw = fmaf(l2, C.cf, fmaf(ef, C.cl, __builtin_amdgcn_fractf(A) + zmu_w[j]));
+    const float fA = __builtin_amdgcn_fractf(A);
+    const float zw = fmaf(l2, C.cf, fmaf(ef, C.cl, fA + zmu_w[j]));
     const float hw = fmaf(A, C.nk7, C.hk8);                        // 0.5 - e
-    ow[j] = (int)__builtin_amdgcn_fmed3f(floorf(A) + floorf(zw), 0.0f, C.kmax_w);
+    const float fzw = __builtin_amdgcn_fractf(zw);
+    ow[j] = __float_as_uint(
+        __builtin_amdgcn_fmed3f((A - fA) + (zw - fzw), 0.0f, C.kmax_w) + kCodeBias);
     // uncertain when 0.5 - e - |fract(z) - 0.5| < 0 or NaN: its sign bit
-    const uint32_t um = unsure(zm, hm), uw = unsure(zw, hw);
+    const uint32_t um = unsure(fzm, hm), uw = unsure(fzw, hw);
     if (FULL || j < n) flags |= (um << j) | (uw << (8 + j));
   }
   if (FULL) {
@@ -951,15 +972,16 @@ __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, i
     p1.x = p[4]; p1.y = p[5]; p1.z = p[6]; p1.w = p[7];
     store_stream(p0, (LUMA_GLOBAL vf4 *)(T.param + e0));
     store_stream(p1, (LUMA_GLOBAL vf4 *)(T.param + e0 + 4));
+    // two codes per word: the low halves of om[2i] and om[2i + 1] (v_perm)
     vu4 a, b;
-    a.x = (uint32_t)(om[0] & 0xFFFF) | ((uint32_t)om[1] << 16);
-    a.y = (uint32_t)(om[2] & 0xFFFF) | ((uint32_t)om[3] << 16);
-    a.z = (uint32_t)(om[4] & 0xFFFF) | ((uint32_t)om[5] << 16);
-    a.w = (uint32_t)(om[6] & 0xFFFF) | ((uint32_t)om[7] << 16);
-    b.x = (uint32_t)ow[0] | ((uint32_t)ow[1] << 16);
-    b.y = (uint32_t)ow[2] | ((uint32_t)ow[3] << 16);
-    b.z = (uint32_t)ow[4] | ((uint32_t)ow[5] << 16);
-    b.w = (uint32_t)ow[6] | ((uint32_t)ow[7] << 16);
+    a.x = __builtin_amdgcn_perm(om[1], om[0], 0x05040100u);
+    a.y = __builtin_amdgcn_perm(om[3], om[2], 0x05040100u);
+    a.z = __builtin_amdgcn_perm(om[5], om[4], 0x05040100u);
+    a.w = __builtin_amdgcn_perm(om[7], om[6], 0x05040100u);
+    b.x = __builtin_amdgcn_perm(ow[1], ow[0], 0x05040100u);
+    b.y = __builtin_amdgcn_perm(ow[3], ow[2], 0x05040100u);
+    b.z = __builtin_amdgcn_perm(ow[5], ow[4], 0x05040100u);
+    b.w = __builtin_amdgcn_perm(ow[7], ow[6], 0x05040100u);
     *(LUMA_GLOBAL vu4 *)(T.q_m + e0) = a;
     *(LUMA_GLOBAL vu4 *)(T.q_w + e0) = b;
   } else {
@@ -967,7 +989,7 @@ __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, i
     for (int j = 0; j < kVec; ++j) {
       if (j < n) {
         T.param[e0 + j] = p[j];
-        T.q_m[e0 + j] = (int16_t)om[j];
+        T.q_m[e0 + j] = (int16_t)(uint16_t)om[j];
         T.q_w[e0 + j] = (int16_t)(uint16_t)ow[j];
       }
     }
@@ -1017,6 +1039,7 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   C.pm0 = kPhiloxM0;
   C.pm1 = kPhiloxM1;
   C.ndw = -C.D.dw;
+  C.nbias = 8388608.0f * C.D.dw;
   C.nk1 = -C.k1;
   C.nk2 = -C.k2;
   C.hk3 = 0.5f - C.k3;
