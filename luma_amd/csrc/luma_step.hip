@@ -523,8 +523,19 @@ __device__ __noinline__ uint64_t exact_pair_w(int qw, float g, const LUMA_GLOBAL
 // the fast path wrote some iterations earlier, and a younger line is more
 // likely to still be in L2.
 constexpr int kQueueCap = kVec * 64 + 64;
-constexpr int kQueueCap2 = 256;
-static_assert((kQueueCap2 & (kQueueCap2 - 1)) == 0, "pass 2 queues are power-of-two rings");
+constexpr int kQueueCapW = 256;   // pass 2 preconditioner ring (entries)
+constexpr int kQueueCapM = 128;   // pass 2 momentum ring (uncertain 8x less often)
+static_assert((kQueueCapW & (kQueueCapW - 1)) == 0 && (kQueueCapM & (kQueueCapM - 1)) == 0,
+              "pass 2 queues are power-of-two rings");
+// Pass 2 stages the new preconditioner codes of its last kStage iterations
+// in LDS (one 16-byte group per lane per iteration) and writes an
+// iteration's codes to HBM only once its queued exact codes are in: the
+// exact codes then land in LDS instead of in lines already written back.
+// With about 15 uncertain preconditioner codes per wave iteration, the ring
+// fills a 64-entry batch every 4-5 iterations, so 7 slots rarely force a
+// partial batch.  LDS per workgroup: 4 x (128 + 256 + 7 x 64) x 16 B = 52 KB,
+// so three workgroups (the VGPR limit) still fit a CU's 160 KB.
+constexpr int kStage = 7;
 
 // Keeps a wave-uniform value in a VGPR.  On gfx950 a VALU instruction with
 // an SGPR source operand issues at about half the rate of one whose sources
@@ -892,9 +903,12 @@ __device__ __forceinline__ void launder(P2Const &C) {
 // aligned (vector loads/stores, no masking).  Returns which codes need the
 // exact path (bit j: momentum code of element j, bit 8 + j: preconditioner
 // code); Q and coarse are kept for the queues.
-template <int GD, bool INJ, bool SMALL, bool SCALED, bool FULL>
+// STAGE (FULL only): the preconditioner codes go to *stage (LDS) instead
+// of HBM.
+template <int GD, bool INJ, bool SMALL, bool SCALED, bool FULL, bool STAGE>
 __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, int64_t e0, int n,
-                                            uint32_t k0, uint32_t k1, Group8 &Q, U4 &coarse) {
+                                            uint32_t k0, uint32_t k1, Group8 &Q, U4 &coarse,
+                                            uint4 *stage) {
   load_group<GD, true>(T, e0, n, FULL, Q);
   unscale_group<GD, SCALED>(Q, C.inv);
   float p[kVec];
@@ -983,7 +997,10 @@ __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, i
     b.z = __builtin_amdgcn_perm(ow[5], ow[4], 0x05040100u);
     b.w = __builtin_amdgcn_perm(ow[7], ow[6], 0x05040100u);
     *(LUMA_GLOBAL vu4 *)(T.q_m + e0) = a;
-    *(LUMA_GLOBAL vu4 *)(T.q_w + e0) = b;
+    if (STAGE)
+      *stage = make_uint4(b.x, b.y, b.z, b.w);
+    else
+      *(LUMA_GLOBAL vu4 *)(T.q_w + e0) = b;
   } else {
 #pragma unroll
     for (int j = 0; j < kVec; ++j) {
@@ -1048,14 +1065,16 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   launder(C);
   const bool vec_ok = tensor_vec_ok(T);
   const uint32_t lane = lane_id();
-  uint4 *queue_m = queue, *queue_w = queue + kQueueCap2;
+  // the wave's LDS block: momentum ring, preconditioner ring, staging slots
+  uint4 *queue_m = queue, *queue_w = queue + kQueueCapM;
+  uint4 *stage = queue_w + kQueueCapW;
   uint32_t qlen_m = 0, qlen_w = 0;   // pending entries
   uint32_t head_m = 0, head_w = 0;   // ring position of the oldest
   // Queue entry: x = chunk offset | old code << 16, y = the uniform's top 8
   // bits (Philox; its low 16 bits come from the fine block), z = the
   // gradient as float32 bits (no second read of HBM).  The fast codes were
-  // already stored; the exact ones overwrite them (same wavefront, so the
-  // stores stay in program order).
+  // already stored (or staged); the exact ones overwrite them (same
+  // wavefront, so the stores stay in program order).
   // The code is c.hi when u < c.p.  With Philox the top 8 bits of u are
   // known: u lies in [top/256, (top + 1)/256 - 2^-24], which decides unless
   // c.p falls inside (then the fine block gives the low 16 bits).
@@ -1069,6 +1088,12 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     }
     return b;
   };
+  // Staging: whole-group iterations [staged_lo, staged_hi) keep their
+  // preconditioner codes in stage[(it % kStage) * 64 + lane] until written
+  // back.  Chunk offset o belongs to iteration o >> 11 (kThreads * kVec =
+  // 2048 elements per iteration) and to lane (o >> 3) & 63 of this wave.
+  static_assert(kThreads * kVec == 2048, "iteration of a chunk offset");
+  int staged_lo = 0, staged_hi = 0;
   auto run_m = [&](uint4 ent) {
     const int64_t i = beg + (ent.x & 0xFFFFu);
     const CodePair c =
@@ -1077,27 +1102,24 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     T.q_m[i] = (int16_t)(b ? c.hi : c.lo);
   };
   auto run_w = [&](uint4 ent) {
-    const int64_t i = beg + (ent.x & 0xFFFFu);
+    const uint32_t o = ent.x & 0xFFFFu;
+    const int64_t i = beg + o;
     const CodePair c =
         unpack_pair(exact_pair_w((int)(ent.x >> 16), __uint_as_float(ent.z), old, nw, h));
     const bool b = INJ ? T.u_w[i] < c.p : below(c.p, i, ent.y, 1);
-    T.q_w[i] = (int16_t)(b ? c.hi : c.lo);
+    const uint16_t code = (uint16_t)(b ? c.hi : c.lo);
+    const int it_e = (int)(o >> 11);
+    if (it_e >= staged_lo && it_e < staged_hi) {
+      uint16_t *slot = (uint16_t *)&stage[(it_e % kStage) * 64 + ((o >> 3) & 63u)];
+      slot[o & 7u] = code;
+    } else {
+      T.q_w[i] = (int16_t)code;
+    }
   };
-  // Every lane runs the same number of iterations (lanes past the end carry
-  // n = 0), so the ballots and the queue lengths stay uniform across the wave.
-  const int n_it = (int)((end - beg + kThreads * kVec - 1) / (kThreads * kVec));
-  for (int it = 0; it < n_it; ++it) {
-    const int64_t e0 = beg + ((int64_t)it * kThreads + threadIdx.x) * kVec;
-    const int64_t rem = end - e0;
-    const int n = rem <= 0 ? 0 : (rem < kVec ? (int)rem : kVec);
-    Group8 Q;
-    U4 coarse{};
-    uint32_t flags;
-    if (vec_ok && n == kVec)
-      flags = p2_iter<GD, INJ, SMALL, SCALED, true>(T, C, e0, n, k0, k1, Q, coarse);
-    else
-      flags = p2_iter<GD, INJ, SMALL, SCALED, false>(T, C, e0, n, k0, k1, Q, coarse);
-    if (!__ballot(flags != 0)) continue;
+  // Queue the codes of one iteration that the fast path could not certify,
+  // and run full batches of 64, oldest first.
+  auto take = [&](int64_t e0, uint32_t flags, const Group8 &Q, const U4 &coarse) {
+    if (!__ballot(flags != 0)) return;
     const uint32_t off0 = (uint32_t)(e0 - beg);
     // queue positions: a wave prefix sum of (momentum count | preconditioner
     // count << 16) gives each lane its first slot in both queues
@@ -1116,11 +1138,11 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
       return make_uint4((off0 + k) | ((uint32_t)code << 16), byte, __float_as_uint(sel8(Q.g, k)),
                         0u);
     };
-    if (qlen_m + tot_m <= (uint32_t)kQueueCap2) {
+    if (qlen_m + tot_m <= (uint32_t)kQueueCapM) {
       uint32_t pos = head_m + qlen_m + (excl & 0xFFFFu);
       for (uint32_t f = fm; f != 0u; f &= f - 1u) {
         const uint32_t k = (uint32_t)__builtin_ctz(f);
-        queue_m[pos++ & (kQueueCap2 - 1)] = entry(k, sel8(Q.qm, k), 0u);
+        queue_m[pos++ & (kQueueCapM - 1)] = entry(k, sel8(Q.qm, k), 0u);
       }
       qlen_m += tot_m;
     } else {
@@ -1130,11 +1152,11 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
         run_m(entry(k, sel8(Q.qm, k), 0u));
       }
     }
-    if (qlen_w + tot_w <= (uint32_t)kQueueCap2) {
+    if (qlen_w + tot_w <= (uint32_t)kQueueCapW) {
       uint32_t pos = head_w + qlen_w + (excl >> 16);
       for (uint32_t f = fw; f != 0u; f &= f - 1u) {
         const uint32_t k = (uint32_t)__builtin_ctz(f);
-        queue_w[pos++ & (kQueueCap2 - 1)] = entry(k, sel8(Q.qw, k), 8u);
+        queue_w[pos++ & (kQueueCapW - 1)] = entry(k, sel8(Q.qw, k), 8u);
       }
       qlen_w += tot_w;
     } else {
@@ -1145,19 +1167,81 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     }
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     while (qlen_m >= 64) {
-      run_m(queue_m[(head_m + lane) & (kQueueCap2 - 1)]);
+      run_m(queue_m[(head_m + lane) & (kQueueCapM - 1)]);
       head_m += 64;
       qlen_m -= 64;
     }
     while (qlen_w >= 64) {
-      run_w(queue_w[(head_w + lane) & (kQueueCap2 - 1)]);
+      run_w(queue_w[(head_w + lane) & (kQueueCapW - 1)]);
       head_w += 64;
       qlen_w -= 64;
     }
+  };
+  // Run the oldest min(qlen_w, 64) preconditioner entries (a partial batch).
+  auto batch_w = [&]() {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    const uint32_t nb = qlen_w < 64u ? qlen_w : 64u;
+    if (lane < nb) run_w(queue_w[(head_w + lane) & (kQueueCapW - 1)]);
+    head_w += nb;
+    qlen_w -= nb;
+  };
+  // Oldest pending preconditioner entry's iteration (the ring is FIFO).
+  auto oldest_w = [&]() -> int {
+    const uint32_t x = queue_w[head_w & (kQueueCapW - 1)].x;
+    return (int)(((uint32_t)__builtin_amdgcn_readfirstlane((int)x) & 0xFFFFu) >> 11);
+  };
+  // Write iteration j's staged preconditioner codes to HBM.
+  auto write_back = [&](int j) {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    const uint4 v = stage[(j % kStage) * 64 + lane];
+    const int64_t e = beg + ((int64_t)j * kThreads + threadIdx.x) * kVec;
+    vu4 w;
+    w.x = v.x; w.y = v.y; w.z = v.z; w.w = v.w;
+    *(LUMA_GLOBAL vu4 *)(T.q_w + e) = w;
+  };
+  // Every lane runs the same number of iterations (lanes past the end carry
+  // n = 0), so the ballots and the queue lengths stay uniform across the wave.
+  constexpr int64_t kStride = (int64_t)kThreads * kVec;
+  const int n_it = (int)((end - beg + kStride - 1) / kStride);
+  // Iterations in which every lane's group is whole stage their
+  // preconditioner codes; before a slot is reused, the iteration it holds has
+  // its queued entries run and is written back.
+  const int n_whole = vec_ok ? (int)((end - beg) / kStride) : 0;
+  int it = 0;
+  for (; it < n_whole; ++it) {
+    const int64_t e0 = beg + ((int64_t)it * kThreads + threadIdx.x) * kVec;
+    Group8 Q;
+    U4 coarse{};
+    const uint32_t flags = p2_iter<GD, INJ, SMALL, SCALED, true, true>(
+        T, C, e0, kVec, k0, k1, Q, coarse, &stage[(it % kStage) * 64 + lane]);
+    staged_hi = it + 1;
+    take(e0, flags, Q, coarse);
+    const int wb = it + 1 - kStage;   // the slot iteration it + 1 will use
+    if (wb >= 0) {
+      while (qlen_w > 0 && oldest_w() <= wb) batch_w();
+      write_back(wb);
+      staged_lo = wb + 1;
+    }
+  }
+  // drain the staged iterations
+  while (qlen_w > 0) batch_w();
+  for (int j = staged_lo; j < staged_hi; ++j) write_back(j);
+  staged_lo = staged_hi = 0;
+  for (; it < n_it; ++it) {
+    const int64_t e0 = beg + ((int64_t)it * kThreads + threadIdx.x) * kVec;
+    const int64_t rem = end - e0;
+    const int n = rem <= 0 ? 0 : (rem < kVec ? (int)rem : kVec);
+    Group8 Q;
+    U4 coarse{};
+    const uint32_t flags =
+        (vec_ok && n == kVec)
+            ? p2_iter<GD, INJ, SMALL, SCALED, true, false>(T, C, e0, n, k0, k1, Q, coarse, nullptr)
+            : p2_iter<GD, INJ, SMALL, SCALED, false, false>(T, C, e0, n, k0, k1, Q, coarse, nullptr);
+    take(e0, flags, Q, coarse);
   }
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  if (lane < qlen_m) run_m(queue_m[(head_m + lane) & (kQueueCap2 - 1)]);
-  if (lane < qlen_w) run_w(queue_w[(head_w + lane) & (kQueueCap2 - 1)]);
+  if (lane < qlen_m) run_m(queue_m[(head_m + lane) & (kQueueCapM - 1)]);
+  if (lane < qlen_w) run_w(queue_w[(head_w + lane) & (kQueueCapW - 1)]);
 }
 
 template <int GD, bool SCALED>
@@ -1205,7 +1289,7 @@ __global__ __launch_bounds__(kThreads) void pass2_fast_kernel(StepSrc src, uint6
   const bool small = (old == nullptr || old->fast[kXTopM] <= kSmall) && nw->sm <= kSmall;
   const bool scaled = src.scaling.grad_scale != nullptr;
   const float inv = inv_scale(src);
-  __shared__ uint4 qbuf[kThreads / 64][2 * kQueueCap2];
+  __shared__ uint4 qbuf[kThreads / 64][kQueueCapM + kQueueCapW + kStage * 64];
   uint4 *q = qbuf[threadIdx.x >> 6];
   if (T.grad_dtype == LUMA_GRAD_BF16)
     pass2_dispatch<LUMA_GRAD_BF16>(T, h, old, nw, inv, scaled, beg, end, k0, k1, inj, small, q);
