@@ -18,8 +18,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 SOURCES = [os.path.join(HERE, "csrc", "luma_step.hip")]
-HEADERS = [os.path.join(HERE, "csrc", h) for h in ("luma_exact.h", "luma_philox.h")] + [
-    os.path.join(ROOT, "include", "luma.h")]
+
 OUT = os.path.join(HERE, "libluma_hip.so")
 ARCH = os.environ.get("LUMA_OFFLOAD_ARCH", "gfx950")
 

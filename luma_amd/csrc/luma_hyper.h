@@ -22,11 +22,11 @@
 
 #include "../../include/luma.h"
 
-#ifndef LUMA_HD
+#ifndef LUMA_HYPER_FN
 #if defined(__HIPCC__)
-#define LUMA_HD __host__ __device__
+#define LUMA_HYPER_FN __host__ __device__
 #else
-#define LUMA_HD
+#define LUMA_HYPER_FN
 #endif
 #endif
 
@@ -44,7 +44,7 @@ struct DD {
 };
 
 // Product of two double-doubles, normalised (|lo| <= ulp(hi)/2).
-LUMA_HD inline DD dd_mul(DD a, DD b) {
+LUMA_HYPER_FN inline DD dd_mul(DD a, DD b) {
   const double p = a.hi * b.hi;
   double e = fma(a.hi, b.hi, -p);
   e += a.hi * b.lo + a.lo * b.hi;
@@ -56,7 +56,7 @@ LUMA_HD inline DD dd_mul(DD a, DD b) {
 
 // Correctly rounded b^t for 0 <= b <= 1 and t >= 1.  Returns 0 once the
 // power is below 2^-60, where 1 - b^t rounds to 1 in double either way.
-LUMA_HD inline double pow_rn(double b, int64_t t) {
+LUMA_HYPER_FN inline double pow_rn(double b, int64_t t) {
   DD r = {1.0, 0.0}, x = {b, 0.0};
   for (;;) {
     if (t & 1) r = dd_mul(r, x);
@@ -70,7 +70,7 @@ LUMA_HD inline double pow_rn(double b, int64_t t) {
 }
 
 // Step-independent fields (pass 1 reads only these).
-LUMA_HD inline Hyper group_hyper(const LumaGroup &g) {
+LUMA_HYPER_FN inline Hyper group_hyper(const LumaGroup &g) {
   Hyper h;
   h.beta1 = (float)g.beta1;
   h.omb1 = (float)(1.0 - g.beta1);
@@ -85,7 +85,7 @@ LUMA_HD inline Hyper group_hyper(const LumaGroup &g) {
 }
 
 // All fields for step t >= 1.
-LUMA_HD inline Hyper step_hyper(const LumaGroup &g, int64_t t) {
+LUMA_HYPER_FN inline Hyper step_hyper(const LumaGroup &g, int64_t t) {
   Hyper h = group_hyper(g);
   const double bc1 = 1.0 - pow_rn(g.beta1, t);
   const double bc2 = 1.0 - pow_rn(g.beta2, t);

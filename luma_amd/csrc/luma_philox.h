@@ -20,9 +20,9 @@
 #include <stdint.h>
 
 #if defined(__HIPCC__)
-#define LUMA_HD __host__ __device__ __forceinline__
+#define LUMA_PHILOX_FN __host__ __device__ __forceinline__
 #else
-#define LUMA_HD static inline
+#define LUMA_PHILOX_FN static inline
 #endif
 
 namespace luma {
@@ -36,7 +36,7 @@ struct U4 {
   uint32_t x, y, z, w;
 };
 
-LUMA_HD void philox_round(uint32_t &c0, uint32_t &c1, uint32_t &c2, uint32_t &c3, uint32_t k0,
+LUMA_PHILOX_FN void philox_round(uint32_t &c0, uint32_t &c1, uint32_t &c2, uint32_t &c3, uint32_t k0,
                           uint32_t k1) {
   const uint64_t p0 = (uint64_t)kPhiloxM0 * c0;
   const uint64_t p1 = (uint64_t)kPhiloxM1 * c2;
@@ -51,7 +51,7 @@ LUMA_HD void philox_round(uint32_t &c0, uint32_t &c1, uint32_t &c2, uint32_t &c3
 }
 
 // Ten rounds; round r uses key (k0 + r*W0, k1 + r*W1).
-LUMA_HD U4 philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint32_t k0,
+LUMA_PHILOX_FN U4 philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint32_t k0,
                          uint32_t k1) {
 #if defined(__HIP_DEVICE_COMPILE__)
 #pragma unroll
@@ -93,28 +93,28 @@ __device__ __forceinline__ U4 philox4x32_10_v(uint32_t c0, uint32_t c1, uint32_t
 #endif
 
 // Counter-block indices for element e (see the header comment).
-LUMA_HD U4 philox_coarse_block(uint64_t e, uint32_t k0, uint32_t k1) {
+LUMA_PHILOX_FN U4 philox_coarse_block(uint64_t e, uint32_t k0, uint32_t k1) {
   const uint64_t b = e >> 3;
   return philox4x32_10((uint32_t)b, (uint32_t)(b >> 32), 0u, 0u, k0, k1);
 }
 
-LUMA_HD U4 philox_fine_block(uint64_t e, uint32_t k0, uint32_t k1) {
+LUMA_PHILOX_FN U4 philox_fine_block(uint64_t e, uint32_t k0, uint32_t k1) {
   const uint64_t b = e >> 2;
   return philox4x32_10((uint32_t)b, (uint32_t)(b >> 32), 1u, 0u, k0, k1);
 }
 
-LUMA_HD uint32_t u4_word(const U4 &v, int i) {
+LUMA_PHILOX_FN uint32_t u4_word(const U4 &v, int i) {
   return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
 }
 
 // Byte i (0..15) of a block, little-endian across x, y, z, w.
-LUMA_HD uint32_t u4_byte(const U4 &v, int i) { return (u4_word(v, i >> 2) >> (8 * (i & 3))) & 0xFFu; }
+LUMA_PHILOX_FN uint32_t u4_byte(const U4 &v, int i) { return (u4_word(v, i >> 2) >> (8 * (i & 3))) & 0xFFu; }
 
 // 16-bit half i (0..7) of a block.
-LUMA_HD uint32_t u4_half(const U4 &v, int i) { return (u4_word(v, i >> 1) >> (16 * (i & 1))) & 0xFFFFu; }
+LUMA_PHILOX_FN uint32_t u4_half(const U4 &v, int i) { return (u4_word(v, i >> 1) >> (16 * (i & 1))) & 0xFFFFu; }
 
 // The two 24-bit integers (u * 2^24) of element e, from its two blocks.
-LUMA_HD void philox_uniform_bits(const U4 &coarse, const U4 &fine, uint64_t e, uint32_t &bits_m,
+LUMA_PHILOX_FN void philox_uniform_bits(const U4 &coarse, const U4 &fine, uint64_t e, uint32_t &bits_m,
                                  uint32_t &bits_w) {
   const int j = (int)(e & 7), i = (int)(e & 3);
   bits_m = (u4_byte(coarse, 2 * j) << 16) | u4_half(fine, 2 * i);
