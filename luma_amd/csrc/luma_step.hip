@@ -595,6 +595,7 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 // Constants of the pass-1 loop, kept in VGPRs (see in_vgpr).
 struct P1Const {
   float dm, ndw, nbias, iwmin, eps, b1, omb1, b2, omb2;
+  float up_m, up_v, abs_v;   // pruning margins: 1 + 8u, 1 + 16u, eps^2 * 1e-10
   float inv;   // inverse gradient scale (SCALED)
   uint32_t sign;
 };
@@ -611,10 +612,16 @@ __device__ __forceinline__ void unscale_group(Group8 &G, float inv) {
 // and gradients; the iteration reloads raw with the group it will process
 // next (en: elements en .. en+7), so that the load overlaps this group's
 // arithmetic.
-template <int GD, bool SMALL, bool SCALED, bool FULL>
+// PRUNE (FULL only): first bound every fast |m'| and v' of the lane's group
+// by the fast formulas at its largest |q_m|, smallest q_w and largest |g|
+// (each formula is non-decreasing in those, up to the few-ulp wobble of the
+// hardware exp2 that the margins cover).  When that bound is below the
+// thresholds Tm / Tv in every lane, no element of the iteration can be a
+// candidate and its per-element decode is skipped (am = av = 0).
+template <int GD, bool SMALL, bool SCALED, bool FULL, bool PRUNE>
 __device__ __forceinline__ void p1_iter(const Tensor &T, const P1Const &K, int64_t e0, int n,
-                                        Raw8 &raw, int64_t en, uint32_t (&am)[kVec],
-                                        uint32_t (&av)[kVec]) {
+                                        Raw8 &raw, int64_t en, uint32_t Tm, uint32_t Tv,
+                                        uint32_t (&am)[kVec], uint32_t (&av)[kVec]) {
   Group8 G;
   if (FULL) {
     unpack_raw<GD>(raw, G);
@@ -623,6 +630,26 @@ __device__ __forceinline__ void p1_iter(const Tensor &T, const P1Const &K, int64
     load_group<GD>(T, e0, n, false, G);
   }
   unscale_group<GD, SCALED>(G, K.inv);
+  if (PRUNE) {
+    int qa = 0, qw_lo = G.qw[0];
+    uint32_t gb = 0;
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) {
+      qa = max(qa, abs(G.qm[j]));
+      qw_lo = min(qw_lo, G.qw[j]);   // kCodeFloat | code: ordered as the codes
+      gb = max(gb, __float_as_uint(G.g[j]) & 0x7FFFFFFFu);   // NaN above +Inf
+    }
+    const FastEma fb = fast_ema<SMALL, false>(qa, qw_lo, __uint_as_float(gb), K.dm, K.ndw,
+                                              K.nbias, K.iwmin, K.eps, K.b1, K.omb1, K.b2,
+                                              K.omb2, K.sign);
+    const uint32_t um = __float_as_uint(fb.mn * K.up_m) & 0x7FFFFFFFu;
+    const uint32_t uv = __float_as_uint(fmaf(fb.vn, K.up_v, K.abs_v)) & 0x7FFFFFFFu;
+    if (!__ballot(um >= Tm || uv >= Tv)) {
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) am[j] = av[j] = 0u;
+      return;
+    }
+  }
 #pragma unroll
   for (int j = 0; j < kVec; ++j) {
     const FastEma f = fast_ema<SMALL, false>(G.qm[j], G.qw[j], G.g[j], K.dm, K.ndw, K.nbias, K.iwmin,
@@ -657,6 +684,13 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   K.omb2 = in_vgpr(h.omb2);
   K.inv = in_vgpr(inv);
   K.sign = in_vgpr(0x80000000u);
+  // 8u covers the rounding of the bound's own products and the non-monotone
+  // wobble of the hardware exp2 / of the expm1 branch switch (a few ulp);
+  // abs_v covers decodes whose 1/w - eps rounds slightly below zero
+  // (|rr| <= 4u eps, so rr^2 <= 1e-13 eps^2)
+  K.up_m = in_vgpr(1.0f + 8.0f * kU);
+  K.up_v = in_vgpr(1.0f + 16.0f * kU);
+  K.abs_v = in_vgpr(D.eps * D.eps * 1e-10f);
   const bool vec_ok = tensor_vec_ok(T);
   const float lo_m = 1.0f - B.dlt_m, hi_m = 1.0f / (1.0f + B.dlt_m);
   const float lo_v = 1.0f - B.dlt_v, hi_v = 1.0f / (1.0f + B.dlt_v);
@@ -725,7 +759,10 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
       const int64_t e0 = beg + ((int64_t)it * kThreads + threadIdx.x) * kVec;
       const int64_t en = end - e0 - kStride >= kVec ? e0 + kStride : e0;
       uint32_t am[kVec], av[kVec];
-      p1_iter<GD, SMALL, SCALED, true>(T, K, e0, kVec, raw, en, am, av);
+      if (exact_fast)
+        p1_iter<GD, SMALL, SCALED, true, false>(T, K, e0, kVec, raw, en, Tm, Tv, am, av);
+      else
+        p1_iter<GD, SMALL, SCALED, true, true>(T, K, e0, kVec, raw, en, Tm, Tv, am, av);
       take(e0, kVec, am, av);
     }
   }
@@ -735,7 +772,7 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     const int n = rem <= 0 ? 0 : (rem < kVec ? (int)rem : kVec);
     uint32_t am[kVec], av[kVec];
     Raw8 unused;
-    p1_iter<GD, SMALL, SCALED, false>(T, K, e0, n, unused, e0, am, av);
+    p1_iter<GD, SMALL, SCALED, false, false>(T, K, e0, n, unused, e0, Tm, Tv, am, av);
     take(e0, n, am, av);
   }
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
