@@ -70,6 +70,40 @@ def test_exact_heterogeneous_scales():
     _check_exact(res)
 
 
+def test_pass1_pruning_adversarial():
+    """Pass 1 skips the per-element decode of an iteration when a bound on its
+    groups' |m'| and v' is below the running thresholds.  Layouts whose
+    maxima sit in the last iterations of a chunk (elements 63488.. of each
+    65536-element chunk), a hair above everything before them, must still
+    give the exact S_m and S_v."""
+    n = 2 * 65536 + 4096
+    late = [65536 - 3, 2 * 65536 - 1, n - 2]
+
+    def grads(t, i, shape):
+        if i == 0:
+            # constant |g| with alternating signs; late elements a few ulp larger
+            x = torch.full(shape, 1e-3)
+            x[1::2] = -1e-3
+            for k, e in enumerate(late):
+                x[e] = 1e-3 * (1.0 + (k + 1) * 2.0 ** -20)
+        elif i == 1:
+            # magnitudes falling along the tensor, the largest at the very end
+            x = torch.linspace(1e-2, 1e-4, shape[0])
+            x[late[1]] = 1.0001e-2
+            x[-1] = -1.0002e-2
+        else:
+            # one large gradient at t = 1 only, late in a chunk: its m and v
+            # decay but stay the maxima while everything else is small
+            g = torch.Generator().manual_seed(11 * t)
+            x = torch.randn(shape, generator=g) * 1e-5
+            if t == 0:
+                x[late[0]] = 0.5
+                x[late[2]] = -0.25
+        return x
+    res = run_pair([(n,), (n,), (n,)], grads, n_steps=4, math_mode="cr")
+    _check_exact(res)
+
+
 def test_multi_group_exact():
     res = run_pair([(64, 32), (32,), (16, 8), (8,)], normal_grads(1e-2), n_steps=3,
                    math_mode="cr", groups_split=2)
