@@ -33,6 +33,9 @@ import torch
 from torch.optim import Optimizer
 
 from . import _lib as L
+
+_GRAD = operator.attrgetter("grad")
+_DTYPE = operator.attrgetter("dtype")
 from .config import SCALE_FLOOR_M  # noqa: F401  (re-exported constant)
 
 _GRAD_CODES = {torch.float32: L.GRAD_F32, torch.bfloat16: L.GRAD_BF16, torch.float16: L.GRAD_F16}
@@ -273,21 +276,26 @@ class _Plan:
             r[1] is w[1].grad and type(r[1]) is torch.Tensor for w, r in zip(work, rows))
 
     def refresh(self, param_groups) -> bool:
+        # The common case (the same gradient tensors as last step) is checked
+        # with C-level map/all passes; the per-tensor loop runs only when some
+        # gradient object or dtype changed.
         flat = [p for g in param_groups for p in g["params"]]
         if len(flat) != len(self.all_params) or not all(map(operator.is_, flat, self.all_params)):
             return False
-        grads = [p.grad for p in flat]
+        grads = list(map(_GRAD, flat))
         if [g is not None for g in grads] != self.has_grad:
             return False
-        wg = [grads[i] for i in self.work_idx]
+        wg = list(map(grads.__getitem__, self.work_idx))
         dev = self.device_index
-        for i, (g, old) in enumerate(zip(wg, self.grads)):
-            if g is old and g.dtype is self.gdtypes[i]:
-                continue
-            if (type(g) is not torch.Tensor or g.dtype is not self.gdtypes[i]
-                    or g.stride() != self.strides[i] or g.numel() != self.numels[i]
-                    or g.get_device() != dev):
-                return False
+        if not (all(map(operator.is_, wg, self.grads))
+                and all(map(operator.is_, map(_DTYPE, wg), self.gdtypes))):
+            for i, (g, old) in enumerate(zip(wg, self.grads)):
+                if g is old and g.dtype is self.gdtypes[i]:
+                    continue
+                if (type(g) is not torch.Tensor or g.dtype is not self.gdtypes[i]
+                        or g.stride() != self.strides[i] or g.numel() != self.numels[i]
+                        or g.get_device() != dev):
+                    return False
         n = len(wg)
         pptr = np.fromiter(map(torch.Tensor.data_ptr, self.params), dtype=np.uint64, count=n)
         # a parameter whose storage was replaced (p.data = ...) must still be a
