@@ -324,7 +324,7 @@ def main():
         copy_calibration(args.copy_calibration)
         return
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
+        print(f"bench.py: measures one GPU only (--gpus {args.gpus} requested); "
               "the LUMA step is rank-local and shards with no exchange", file=sys.stderr)
         sys.exit(2)
 

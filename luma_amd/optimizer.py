@@ -352,7 +352,7 @@ class LUMA(Optimizer):
             torch.randint(-(2**63), 2**63 - 1, (1,), dtype=torch.int64).item())
         if backend not in self._BACKENDS:
             raise ValueError(f"Invalid backend: {backend}. Expected one of "
-                             "{'auto', 'hip', 'triton'} (this build has the HIP backend only).")
+                             "{'auto', 'hip', 'triton'} (all three select the HIP library).")
         self._engine: Optional[_Engine] = None
         self._noise: Optional[Dict[int, Tuple[torch.Tensor, torch.Tensor]]] = None
         self._flags = 0

@@ -3,12 +3,12 @@
 This module restates, on CPU with torch float32 arithmetic, the reference's
 PyTorch backend (``src/luma_optimizer/functional.py``) and the bookkeeping of
 ``LUMA.step`` / ``state_dict`` / ``export_adamw_state`` /
-``import_adamw_state`` (``src/luma_optimizer/optimizer.py``).  It is the
-checker for the HIP implementation in ``luma_amd``: only ``tests/``,
+``import_adamw_state`` (``src/luma_optimizer/optimizer.py``).  The tests
+compare the HIP implementation in ``luma_amd`` against it: only ``tests/``,
 ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline leg may import it,
 and never as the code path being measured or shipped.
 
-Two knobs make it useful as a checker:
+Two knobs make it useful for those comparisons:
 
 * ``math`` -- the elementwise transcendental functions.  ``"torch"`` uses the
   same ATen CPU kernels the reference calls (MKL VML for exp/log/sqrt, SLEEF
