@@ -14,6 +14,13 @@
 // Nothing is materialised between the passes except 8 bytes per chunk.  With
 // GradScaler's scaling (LumaScaling) every kernel unscales the gradients as
 // it loads them, and returns at once when the overflow flag is set.
+//
+// Both passes take each rounding decision from fast float32 arithmetic when an
+// error bound proves it equal to the exact path's (luma_fast.h), and queue
+// the other elements for the exact path, 64 at a time.  Pass 2 keeps each
+// wave's new preconditioner codes in LDS for a few iterations so that the
+// exact codes land there before the codes go to HBM, and it streams the
+// gradients and parameters non-temporally so that L2 holds the code lines.
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
