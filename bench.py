@@ -284,6 +284,50 @@ def stats_report(config, trace_csv, bench_json, out):
     print("\n".join(lines))
 
 
+ISSUE_COUNTERS = ("SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_WAIT_ANY SQ_WAIT_INST_ANY SQ_ACTIVE_INST_ANY "
+                  "SQ_ACTIVE_INST_VALU SQ_ACTIVE_INST_VALU2 SQ_INSTS_VALU")
+
+
+def issue_report(config, kernel, pmc_csv, out):
+    """Write the instruction-issue summary of a kernel from one rocprofv3 run
+    of bench.py with ISSUE_COUNTERS (steady-state launches: all but the
+    first).  The SQ counters are summed over the shader engines; cycle
+    counts other than SQ_BUSY_CYCLES are in quad-cycles."""
+    cfg = CONFIGS[config]
+    n_params = sum(math.prod(s) for s in cfg["shapes"]())
+    c = {}
+    for name in ISSUE_COUNTERS.split():
+        v = _pmc_per_dispatch(pmc_csv, kernel, name)
+        v = v[1:] or v
+        c[name] = sum(v) / len(v)
+    n_se = 32                      # MI355X: 8 XCDs x 4 shader engines, 8 CUs each
+    se_cycles = c["SQ_BUSY_CYCLES"] / n_se
+    wave_cycles = 4.0 * c["SQ_WAVE_CYCLES"]
+    lines = [
+        f"# Instruction issue of {kernel} on {config} ({n_params} params)",
+        "",
+        "Commands (MI355X, one GPU):",
+        f"    rocprofv3 --pmc {ISSUE_COUNTERS} --output-format csv -d <dir> -- "
+        f"python bench.py --config {config} --steps 2 --warmup 1 --no-cpu",
+        f"    python bench.py --issue-report {config} {kernel} <counter_collection.csv> <out.md>",
+        "",
+        f"kernel time from SQ_BUSY_CYCLES at 2.4 GHz: {se_cycles / 2.4e6:.2f} ms",
+        f"VALU instructions per element: {c['SQ_INSTS_VALU'] * 64 / n_params:.1f}",
+        f"VALU issue rate: {c['SQ_INSTS_VALU'] / (se_cycles * 256):.2f} wave instructions per clock per CU",
+        f"quad-cycles with two VALU instructions issued, per VALU instruction: "
+        f"{c['SQ_ACTIVE_INST_VALU2'] / c['SQ_INSTS_VALU']:.3f} "
+        f"(so {200 * c['SQ_ACTIVE_INST_VALU2'] / c['SQ_INSTS_VALU']:.0f}% of the instructions issued in pairs)",
+        f"resident waves per SIMD: {wave_cycles / (se_cycles * n_se * 32):.2f}",
+        f"wave cycles waiting for an issue slot with an instruction ready (SQ_WAIT_INST_ANY): "
+        f"{100 * 4 * c['SQ_WAIT_INST_ANY'] / wave_cycles:.0f}%",
+        f"wave cycles waiting on a dependency or counter (SQ_WAIT_ANY): {100 * 4 * c['SQ_WAIT_ANY'] / wave_cycles:.0f}%",
+        f"wave cycles issuing (SQ_ACTIVE_INST_ANY): {100 * 4 * c['SQ_ACTIVE_INST_ANY'] / wave_cycles:.0f}%",
+    ]
+    with open(out, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def read_traffic(config, kernel):
     path = os.path.join(TRAFFIC_DIR, f"{kernel.replace('::', '_')}_{config}_traffic.md")
     try:
@@ -311,6 +355,8 @@ def main():
                     metavar=("CONFIG", "KERNEL", "FETCH_CSV", "WRITE_CSV", "COPY_FETCH_CSV",
                              "COPY_WRITE_CSV", "OUT"),
                     help="summarise rocprofv3 FETCH_SIZE/WRITE_SIZE runs into OUT")
+    ap.add_argument("--issue-report", nargs=4, metavar=("CONFIG", "KERNEL", "PMC_CSV", "OUT"),
+                    help="summarise a rocprofv3 --pmc run with the SQ issue counters")
     ap.add_argument("--stats-report", nargs=4, metavar=("CONFIG", "TRACE_CSV", "BENCH_JSON", "OUT"),
                     help="summarise a rocprofv3 --kernel-trace --stats run of bench.py into OUT")
     args = ap.parse_args()
@@ -319,6 +365,9 @@ def main():
         return
     if args.stats_report:
         stats_report(*args.stats_report)
+        return
+    if args.issue_report:
+        issue_report(*args.issue_report)
         return
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
