@@ -54,10 +54,16 @@
 extern "C" {
 #endif
 
-#define LUMA_ABI_VERSION 3
+#define LUMA_ABI_VERSION 4
 
-/* Elements per chunk-table entry (one workgroup's share of a tensor). */
+/*
+ * Elements per chunk-table entry (one workgroup's share of a tensor): the
+ * default and the largest.  luma_step accepts any power of two from
+ * LUMA_CHUNK_ELEMS_MIN to LUMA_CHUNK_ELEMS per launch (LumaStepArgs.chunk_elems);
+ * smaller chunks give small tensor sets more workgroups.
+ */
 #define LUMA_CHUNK_ELEMS 65536
+#define LUMA_CHUNK_ELEMS_MIN 2048
 
 /*
  * Bytes of one slot: a tensor's persistent device state (step count, S_m,
@@ -95,7 +101,7 @@ typedef struct LumaTensor {
   int32_t reserved;     /* 0                                                 */
 } LumaTensor;
 
-/* Chunk c of a tensor covers elements [c*LUMA_CHUNK_ELEMS, min(numel, (c+1)*LUMA_CHUNK_ELEMS)). */
+/* Chunk c of a tensor covers elements [c*C, min(numel, (c+1)*C)), C the launch's chunk length. */
 typedef struct LumaChunk {
   int32_t tensor; /* index into the LumaTensor table */
   int32_t index;  /* chunk number within that tensor */
@@ -141,6 +147,9 @@ typedef struct LumaStepArgs {
   uint64_t base_seed;        /* LUMA._base_seed as its two's-complement bits */
   int32_t noise_mode;        /* LUMA_NOISE_* */
   int32_t flags;             /* LUMA_FLAG_* */
+  int32_t chunk_elems;       /* chunk length C of the chunk table: a power of two in
+                                [LUMA_CHUNK_ELEMS_MIN, LUMA_CHUNK_ELEMS]; 0 = LUMA_CHUNK_ELEMS */
+  int32_t reserved;          /* 0 */
   LumaScaling scaling;       /* both NULL: unscaled gradients, always step */
 } LumaStepArgs;
 

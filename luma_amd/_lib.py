@@ -16,9 +16,10 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_NAME = "libluma_hip.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 
-CHUNK_ELEMS = 65536          # LUMA_CHUNK_ELEMS
+CHUNK_ELEMS = 65536          # LUMA_CHUNK_ELEMS (default and largest chunk length)
+CHUNK_ELEMS_MIN = 2048       # LUMA_CHUNK_ELEMS_MIN
 SLOT_BYTES = 512             # LUMA_SLOT_BYTES
-ABI_VERSION = 3              # LUMA_ABI_VERSION
+ABI_VERSION = 4              # LUMA_ABI_VERSION
 
 GRAD_F32, GRAD_BF16, GRAD_F16 = 0, 1, 2
 NOISE_PHILOX, NOISE_INJECTED = 0, 1
@@ -58,6 +59,8 @@ class StepArgs(ctypes.Structure):
         ("base_seed", ctypes.c_uint64),
         ("noise_mode", ctypes.c_int32),
         ("flags", ctypes.c_int32),
+        ("chunk_elems", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
         ("scaling", Scaling),
     ]
 

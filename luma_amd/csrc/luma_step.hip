@@ -39,6 +39,8 @@ constexpr int kVec = 8;           // consecutive elements per thread per iterati
 constexpr int64_t kChunk = LUMA_CHUNK_ELEMS;
 static_assert(kChunk % (kThreads * kVec) == 0, "chunk must be a whole number of iterations");
 static_assert(kChunk <= 65536, "pass 2 queue entries hold a 16-bit offset within the chunk");
+static_assert(LUMA_CHUNK_ELEMS_MIN % (kThreads * kVec) == 0,
+              "every chunk length must be a whole number of iterations");
 
 // Device view of LumaTensor.  The pointer fields are declared in the global
 // address space so loads and stores through them compile to global_* (not
@@ -78,7 +80,16 @@ struct StepSrc {
   Tensor one;
   LumaGroup group;
   LumaScaling scaling;
+  int32_t chunk_shift;   // log2 of the launch's chunk length
 };
+
+// Elements [beg, end) of chunk ci of tensor T.
+__device__ __forceinline__ void chunk_range(const StepSrc &src, const Tensor &T, int64_t ci,
+                                            int64_t &beg, int64_t &end) {
+  const int64_t len = (int64_t)1 << src.chunk_shift;
+  beg = ci << src.chunk_shift;
+  end = beg + len < T.numel ? beg + len : T.numel;
+}
 
 // GradScaler's found_inf: a nonzero value makes the whole step a no-op.
 __device__ __forceinline__ bool skip_step(const StepSrc &src) {
@@ -211,8 +222,8 @@ __global__ __launch_bounds__(kThreads) void pass1_exact_kernel(StepSrc src,
   // this step is t = step + 1; its decode reads the grid of step t - 1
   const int64_t prev = T.slot->step;
   const Grid *old = prev >= 1 ? (const Grid *)&T.slot->grid[prev & 1] : nullptr;
-  const int64_t beg = ci * kChunk;
-  const int64_t end = beg + kChunk < T.numel ? beg + kChunk : T.numel;
+  int64_t beg, end;
+  chunk_range(src, T, ci, beg, end);
 
   float am = 0.0f, av = 0.0f;
   for (int64_t e0 = beg + (int64_t)threadIdx.x * kVec; e0 < end; e0 += (int64_t)kThreads * kVec) {
@@ -241,7 +252,7 @@ __global__ __launch_bounds__(64) void finalize_kernel(StepSrc src,
   Tensor T;
   LumaGroup grp;
   tensor_job(src, T, grp);
-  const int nch = (int)((T.numel + kChunk - 1) / kChunk);
+  const int nch = (int)(((T.numel - 1) >> src.chunk_shift) + 1);
   float am = 0.0f, av = 0.0f;
   for (int i = threadIdx.x; i < nch; i += 64) {
     const int64_t c = (int64_t)T.first_chunk + i;
@@ -282,8 +293,8 @@ __global__ __launch_bounds__(kThreads) void pass2_exact_kernel(StepSrc src, uint
   const Hyper h = S.hyp;
   const Grid *old = t >= 2 ? &S.grid[(t - 1) & 1] : nullptr;
   const Grid G = S.grid[t & 1];
-  const int64_t beg = ci * kChunk;
-  const int64_t end = beg + kChunk < T.numel ? beg + kChunk : T.numel;
+  int64_t beg, end;
+  chunk_range(src, T, ci, beg, end);
   uint32_t k0, k1;
   step_key(base_seed, t, T.param_id, k0, k1);
 
@@ -815,8 +826,8 @@ __global__ __launch_bounds__(kThreads, 4) void pass1_fast_kernel(StepSrc src,
   // this step is t = step + 1; its decode reads the grid of step t - 1
   const int64_t prev = T.slot->step;
   const LUMA_GLOBAL Grid *old = prev >= 1 ? &T.slot->grid[prev & 1] : nullptr;
-  const int64_t beg = ci * kChunk;
-  const int64_t end = beg + kChunk < T.numel ? beg + kChunk : T.numel;
+  int64_t beg, end;
+  chunk_range(src, T, ci, beg, end);
   const bool small = old == nullptr || old->fast[kXTopM] <= kSmall;
   const bool scaled = src.scaling.grad_scale != nullptr;
   const float inv = inv_scale(src);
@@ -1325,8 +1336,8 @@ __global__ __launch_bounds__(kThreads) void pass2_fast_kernel(StepSrc src, uint6
   const Hyper h = S->hyp;
   const LUMA_GLOBAL Grid *old = t >= 2 ? &S->grid[(t - 1) & 1] : nullptr;
   const LUMA_GLOBAL Grid *nw = &S->grid[t & 1];
-  const int64_t beg = ci * kChunk;
-  const int64_t end = beg + kChunk < T.numel ? beg + kChunk : T.numel;
+  int64_t beg, end;
+  chunk_range(src, T, ci, beg, end);
   uint32_t k0, k1;
   step_key(base_seed, t, T.param_id, k0, k1);
   const bool inj = noise_mode == LUMA_NOISE_INJECTED;
@@ -1561,11 +1572,15 @@ static int step_impl(const LumaStepArgs *a, void *stream, void *const *events) {
   if (a->n_tensors <= 0 || a->n_chunks <= 0) return 0;
   if (!a->tensors || !a->chunks || !a->groups || !a->partials)
     return fail("luma_step: null table pointer");
+  const int32_t c = a->chunk_elems ? a->chunk_elems : (int32_t)LUMA_CHUNK_ELEMS;
+  if (c < LUMA_CHUNK_ELEMS_MIN || c > LUMA_CHUNK_ELEMS || (c & (c - 1)) != 0)
+    return fail("luma_step: chunk_elems must be a power of two in [2048, 65536]");
   StepSrc src{};
   src.tensors = reinterpret_cast<const Tensor *>(a->tensors);
   src.chunks = a->chunks;
   src.groups = a->groups;
   src.scaling = a->scaling;
+  src.chunk_shift = __builtin_ctz((unsigned)c);
   return launch_step(src, a->n_tensors, a->n_chunks, a->partials, a->base_seed, a->noise_mode,
                      a->flags, static_cast<hipStream_t>(stream), events);
 }
@@ -1592,6 +1607,7 @@ int luma_step_tensor(const LumaTensor *tensor, const LumaGroup *group, float *pa
   memcpy(&src.one, tensor, sizeof(Tensor));
   src.one.first_chunk = 0;
   src.group = *group;
+  src.chunk_shift = __builtin_ctz((unsigned)LUMA_CHUNK_ELEMS);
   if (scaling) src.scaling = *scaling;
   return launch_step(src, 1, (int32_t)nch, partials, base_seed, noise_mode, flags,
                      static_cast<hipStream_t>(stream), nullptr);

@@ -37,6 +37,7 @@ from . import _lib as L
 _GRAD = operator.attrgetter("grad")
 _DTYPE = operator.attrgetter("dtype")
 from .config import SCALE_FLOOR_M  # noqa: F401  (re-exported constant)
+from .config import STEP_CHUNK_MIN, STEP_TARGET_CHUNKS
 
 _GRAD_CODES = {torch.float32: L.GRAD_F32, torch.bfloat16: L.GRAD_BF16, torch.float16: L.GRAD_F16}
 _MASK64 = (1 << 64) - 1
@@ -88,7 +89,9 @@ class _Engine:
         self.lib = L.load()
         self.device = device
         self._tensor_key = None      # bytes of the uploaded tensor table
-        self._numel_key = None       # bytes of its numel column (chunk table)
+        self._numel_key = None       # bytes of its numel column and chunk length (chunk table)
+        self._chunk = L.CHUNK_ELEMS  # chunk length of the uploaded chunk table
+        self.chunk_elems = 0         # fixed chunk length (a power of two), 0: chunk_for's choice
         self._d_tensors = None
         self._d_chunks = None
         self._n_chunks = 0
@@ -120,14 +123,27 @@ class _Engine:
             "hyper-parameters before capturing.")
 
     # -- entry points -------------------------------------------------------
-    @staticmethod
-    def table(rows) -> np.ndarray:
+    def chunk_for(self, numels: np.ndarray) -> int:
+        """Chunk length of a step over tensors of these sizes: the largest power
+        of two from CHUNK_ELEMS down to STEP_CHUNK_MIN that still gives
+        STEP_TARGET_CHUNKS workgroups (small sets get more, shorter chunks).
+        The result does not depend on it: every element is computed alone and
+        the per-tensor maxima are exact."""
+        if self.chunk_elems:
+            return self.chunk_elems
+        c = L.CHUNK_ELEMS
+        while c > STEP_CHUNK_MIN and int(((numels + c - 1) // c).sum()) < STEP_TARGET_CHUNKS:
+            c //= 2
+        return c
+
+    def table(self, rows) -> np.ndarray:
         """Tensor table of rows: (param, grad, q_m, q_w, u_m, u_w, slot, param_id,
         grad_code, group) per tensor, chunks numbered consecutively."""
         n = len(rows)
         tt = np.zeros(n, dtype=L.TENSOR_DTYPE)
         numels = np.fromiter((r[0].numel() for r in rows), dtype=np.int64, count=n)
-        nch = (numels + L.CHUNK_ELEMS - 1) // L.CHUNK_ELEMS
+        c = self.chunk_for(numels)
+        nch = (numels + c - 1) // c
         first = np.zeros(n, dtype=np.int64)
         np.cumsum(nch[:-1], out=first[1:])
         if int(nch.sum()) >= 2**31:
@@ -157,9 +173,10 @@ class _Engine:
             if capturing:
                 raise self._capture_error("the parameter or gradient set")
             numels = tt["numel"]
-            nkey = numels.tobytes()
+            c = self.chunk_for(numels)
+            nkey = numels.tobytes() + c.to_bytes(4, "little")
             if nkey != self._numel_key:
-                nch = (numels + L.CHUNK_ELEMS - 1) // L.CHUNK_ELEMS
+                nch = (numels + c - 1) // c
                 n_chunks = int(nch.sum())
                 ch = np.empty(n_chunks, dtype=L.CHUNK_DTYPE)
                 ch["tensor"] = np.repeat(np.arange(n, dtype=np.int32), nch)
@@ -167,6 +184,7 @@ class _Engine:
                                - np.repeat(tt["first_chunk"].astype(np.int64), nch))
                 self._d_chunks = self._upload(ch)
                 self._n_chunks = n_chunks
+                self._chunk = c
                 self._numel_key = nkey
             self._d_tensors = self._upload(tt)
             self._tensor_key = key
@@ -191,6 +209,7 @@ class _Engine:
             chunks=self._d_chunks.data_ptr(), groups=self._d_groups.data_ptr(),
             partials=self._partials.data_ptr(),
             base_seed=base_seed & _MASK64, noise_mode=noise_mode, flags=flags,
+            chunk_elems=self._chunk, reserved=0,
             scaling=L.Scaling(scaling[0] or None, scaling[1] or None))
         if self.profile_events is None:
             L.check(self.lib.luma_step(ctypes.byref(args), self._stream()), "luma_step")

@@ -53,11 +53,12 @@ def _u16(q):
 
 def run_pair(shapes, grad_fn: Callable, n_steps: int, math_mode: str = "cr",
              hyper=None, resync: bool = False, base_seed: int = 0x5DEECE66D,
-             init_std: float = 0.02, groups_split=None) -> PairResult:
+             init_std: float = 0.02, groups_split=None, chunk_elems: int = 0) -> PairResult:
     """Step the HIP optimizer and the oracle ``n_steps`` times; compare each step.
 
     ``resync`` loads the oracle's state into the HIP optimizer before every
     step, so each comparison is one step from an identical state.
+    ``chunk_elems`` fixes the step's chunk length (0: the optimizer's choice).
     """
     hyper = dict(hyper or dict(lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01))
     gen = torch.Generator().manual_seed(12345)
@@ -74,6 +75,8 @@ def run_pair(shapes, grad_fn: Callable, n_steps: int, math_mode: str = "cr",
     oracle = O.OracleLUMA(groups_cpu, base_seed, math_mode)
     opt = LUMA(groups_dev, **hyper)
     opt._base_seed = base_seed
+    if chunk_elems:
+        opt._get_engine(dev[0].device).chunk_elems = chunk_elems
     res = PairResult()
     for t in range(1, n_steps + 1):
         if resync and t > 1:

@@ -70,12 +70,14 @@ def test_exact_heterogeneous_scales():
     _check_exact(res)
 
 
-def test_pass1_pruning_adversarial():
+@pytest.mark.parametrize("chunk", [65536, 16384])
+def test_pass1_pruning_adversarial(chunk):
     """Pass 1 skips the per-element decode of an iteration when a bound on its
     groups' |m'| and v' is below the running thresholds.  Layouts whose
-    maxima sit in the last iterations of a chunk (elements 63488.. of each
-    65536-element chunk), a hair above everything before them, must still
-    give the exact S_m and S_v."""
+    maxima sit in the last iteration of a chunk (of 65536 or of 16384
+    elements), a hair above everything before them, must still give the
+    exact S_m and S_v."""
+    print(f"case pruning chunk={chunk}", flush=True)
     n = 2 * 65536 + 4096
     late = [65536 - 3, 2 * 65536 - 1, n - 2]
 
@@ -100,7 +102,7 @@ def test_pass1_pruning_adversarial():
                 x[late[0]] = 0.5
                 x[late[2]] = -0.25
         return x
-    res = run_pair([(n,), (n,), (n,)], grads, n_steps=4, math_mode="cr")
+    res = run_pair([(n,), (n,), (n,)], grads, n_steps=4, math_mode="cr", chunk_elems=chunk)
     _check_exact(res)
 
 
