@@ -168,15 +168,20 @@ class _Engine:
         tables whose contents changed since the previous launch."""
         capturing = torch.cuda.is_current_stream_capturing()
         n = len(tt)
+        # first_chunk follows the chunk length of this launch (a cached table
+        # may have been built for another)
+        numels = tt["numel"]
+        c = self.chunk_for(numels)
+        nch = (numels + c - 1) // c
+        first = np.zeros(n, dtype=np.int64)
+        np.cumsum(nch[:-1], out=first[1:])
+        tt["first_chunk"] = first
         key = tt.tobytes()
         if key != self._tensor_key:
             if capturing:
                 raise self._capture_error("the parameter or gradient set")
-            numels = tt["numel"]
-            c = self.chunk_for(numels)
             nkey = numels.tobytes() + c.to_bytes(4, "little")
             if nkey != self._numel_key:
-                nch = (numels + c - 1) // c
                 n_chunks = int(nch.sum())
                 ch = np.empty(n_chunks, dtype=L.CHUNK_DTYPE)
                 ch["tensor"] = np.repeat(np.arange(n, dtype=np.int32), nch)
