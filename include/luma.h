@@ -64,6 +64,7 @@ extern "C" {
  */
 #define LUMA_CHUNK_ELEMS 65536
 #define LUMA_CHUNK_ELEMS_MIN 2048
+#define LUMA_STEP_TENSOR_CHUNK_MIN 16384   /* shortest chunk luma_step_tensor uses */
 
 /*
  * Bytes of one slot: a tensor's persistent device state (step count, S_m,
@@ -195,8 +196,10 @@ int luma_step_profiled(const LumaStepArgs *args, void *stream, void *const event
 /*
  * luma_step for one tensor with no device tables: *tensor, *group and
  * *scaling (may be NULL) are host structs read during the call
- * (tensor->first_chunk is ignored);
- * `partials` needs luma_workspace_bytes(ceil(numel / LUMA_CHUNK_ELEMS)).
+ * (tensor->first_chunk is ignored).  The chunk length is LUMA_CHUNK_ELEMS,
+ * halved down to LUMA_STEP_TENSOR_CHUNK_MIN while the tensor has fewer than
+ * 4096 chunks; `partials` needs
+ * luma_workspace_bytes(ceil(numel / LUMA_STEP_TENSOR_CHUNK_MIN)).
  */
 int luma_step_tensor(const LumaTensor *tensor, const LumaGroup *group, float *partials,
                      uint64_t base_seed, int32_t noise_mode, int32_t flags,

@@ -1601,13 +1601,19 @@ int luma_step_tensor(const LumaTensor *tensor, const LumaGroup *group, float *pa
     return fail("luma_step_tensor: null pointer");
   if (noise_mode == LUMA_NOISE_INJECTED && (!tensor->u_m || !tensor->u_w))
     return fail("luma_step_tensor: injected noise needs u_m and u_w");
-  const int64_t nch = (tensor->numel + kChunk - 1) / kChunk;
+  // 4096 chunks fill the chip (16 workgroups per CU); a smaller tensor takes
+  // shorter chunks, down to LUMA_STEP_TENSOR_CHUNK_MIN
+  int shift = __builtin_ctz((unsigned)LUMA_CHUNK_ELEMS);
+  while (shift > __builtin_ctz((unsigned)LUMA_STEP_TENSOR_CHUNK_MIN) &&
+         ((tensor->numel - 1) >> shift) + 1 < 4096)
+    --shift;
+  const int64_t nch = ((tensor->numel - 1) >> shift) + 1;
   if (nch > 0x7fffffff) return fail("luma_step_tensor: tensor too large");
   StepSrc src{};
   memcpy(&src.one, tensor, sizeof(Tensor));
   src.one.first_chunk = 0;
   src.group = *group;
-  src.chunk_shift = __builtin_ctz((unsigned)LUMA_CHUNK_ELEMS);
+  src.chunk_shift = shift;
   if (scaling) src.scaling = *scaling;
   return launch_step(src, 1, (int32_t)nch, partials, base_seed, noise_mode, flags,
                      static_cast<hipStream_t>(stream), nullptr);
