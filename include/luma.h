@@ -62,7 +62,7 @@ extern "C" {
  * LUMA_CHUNK_ELEMS_MIN to LUMA_CHUNK_ELEMS per launch (LumaStepArgs.chunk_elems);
  * smaller chunks give small tensor sets more workgroups.
  */
-#define LUMA_CHUNK_ELEMS 65536
+#define LUMA_CHUNK_ELEMS 131072
 #define LUMA_CHUNK_ELEMS_MIN 2048
 #define LUMA_STEP_TENSOR_CHUNK_MIN 16384   /* shortest chunk luma_step_tensor uses */
 

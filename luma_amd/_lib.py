@@ -16,7 +16,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_NAME = "libluma_hip.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 
-CHUNK_ELEMS = 65536          # LUMA_CHUNK_ELEMS (default and largest chunk length)
+CHUNK_ELEMS = 131072         # LUMA_CHUNK_ELEMS (default and largest chunk length)
 CHUNK_ELEMS_MIN = 2048       # LUMA_CHUNK_ELEMS_MIN
 STEP_TENSOR_CHUNK_MIN = 16384  # LUMA_STEP_TENSOR_CHUNK_MIN
 SLOT_BYTES = 512             # LUMA_SLOT_BYTES

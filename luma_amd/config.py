@@ -6,7 +6,7 @@ SCALE_FLOOR_M: float = 1e-9       # minimum momentum scale S_m
 
 # Launch geometry of the HIP kernels (the reference's get_kernel_config returns
 # Triton launch parameters; these are the gfx950 equivalents).
-CHUNK_ELEMS: int = 65536          # elements per chunk-table entry (one workgroup), at most
+CHUNK_ELEMS: int = 131072         # elements per chunk-table entry (one workgroup), at most
 STEP_CHUNK_MIN: int = 16384       # shortest chunk the optimizer picks for a small tensor set
 STEP_TARGET_CHUNKS: int = 4096    # workgroups a step aims for (16 per CU) before shortening chunks
 THREADS_PER_BLOCK: int = 256      # four wave64 per workgroup

@@ -38,7 +38,7 @@ constexpr int kThreads = 256;     // 4 wave64 per workgroup
 constexpr int kVec = 8;           // consecutive elements per thread per iteration
 constexpr int64_t kChunk = LUMA_CHUNK_ELEMS;
 static_assert(kChunk % (kThreads * kVec) == 0, "chunk must be a whole number of iterations");
-static_assert(kChunk <= 65536, "pass 2 queue entries hold a 16-bit offset within the chunk");
+static_assert(kChunk <= (1 << 20), "pass 2 iteration indices of a chunk offset stay small");
 static_assert(LUMA_CHUNK_ELEMS_MIN % (kThreads * kVec) == 0,
               "every chunk length must be a whole number of iterations");
 
@@ -1125,9 +1125,9 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   uint4 *stage = queue_w + kQueueCapW;
   uint32_t qlen_m = 0, qlen_w = 0;   // pending entries
   uint32_t head_m = 0, head_w = 0;   // ring position of the oldest
-  // Queue entry: x = chunk offset | old code << 16, y = the uniform's top 8
-  // bits (Philox; its low 16 bits come from the fine block), z = the
-  // gradient as float32 bits (no second read of HBM).  The fast codes were
+  // Queue entry: x = chunk offset, y = the uniform's top 8 bits (Philox; its
+  // low 16 bits come from the fine block), z = the gradient as float32 bits
+  // (no second read of HBM), w = the old code's 16 bits.  The fast codes were
   // already stored (or staged); the exact ones overwrite them (same
   // wavefront, so the stores stay in program order).
   // The code is c.hi when u < c.p.  With Philox the top 8 bits of u are
@@ -1150,17 +1150,17 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   static_assert(kThreads * kVec == 2048, "iteration of a chunk offset");
   int staged_lo = 0, staged_hi = 0;
   auto run_m = [&](uint4 ent) {
-    const int64_t i = beg + (ent.x & 0xFFFFu);
+    const int64_t i = beg + ent.x;
     const CodePair c =
-        unpack_pair(exact_pair_m((int)(int16_t)(ent.x >> 16), __uint_as_float(ent.z), old, nw, h));
+        unpack_pair(exact_pair_m((int)(int16_t)ent.w, __uint_as_float(ent.z), old, nw, h));
     const bool b = INJ ? T.u_m[i] < c.p : below(c.p, i, ent.y, 0);
     T.q_m[i] = (int16_t)(b ? c.hi : c.lo);
   };
   auto run_w = [&](uint4 ent) {
-    const uint32_t o = ent.x & 0xFFFFu;
+    const uint32_t o = ent.x;
     const int64_t i = beg + o;
     const CodePair c =
-        unpack_pair(exact_pair_w((int)(ent.x >> 16), __uint_as_float(ent.z), old, nw, h));
+        unpack_pair(exact_pair_w((int)ent.w, __uint_as_float(ent.z), old, nw, h));
     const bool b = INJ ? T.u_w[i] < c.p : below(c.p, i, ent.y, 1);
     const uint16_t code = (uint16_t)(b ? c.hi : c.lo);
     const int it_e = (int)(o >> 11);
@@ -1190,8 +1190,7 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
       const uint32_t w01 = (k & 2u) ? coarse.y : coarse.x, w23 = (k & 2u) ? coarse.w : coarse.z;
       const uint32_t wd = (k & 4u) ? w23 : w01;
       const uint32_t byte = INJ ? 0u : (wd >> (16u * (k & 1u) + byte_shift)) & 0xFFu;
-      return make_uint4((off0 + k) | ((uint32_t)code << 16), byte, __float_as_uint(sel8(Q.g, k)),
-                        0u);
+      return make_uint4(off0 + k, byte, __float_as_uint(sel8(Q.g, k)), (uint32_t)code & 0xFFFFu);
     };
     if (qlen_m + tot_m <= (uint32_t)kQueueCapM) {
       uint32_t pos = head_m + qlen_m + (excl & 0xFFFFu);
@@ -1243,7 +1242,7 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   // Oldest pending preconditioner entry's iteration (the ring is FIFO).
   auto oldest_w = [&]() -> int {
     const uint32_t x = queue_w[head_w & (kQueueCapW - 1)].x;
-    return (int)(((uint32_t)__builtin_amdgcn_readfirstlane((int)x) & 0xFFFFu) >> 11);
+    return (int)((uint32_t)__builtin_amdgcn_readfirstlane((int)x) >> 11);
   };
   // Write iteration j's staged preconditioner codes to HBM.
   auto write_back = [&](int j) {
@@ -1574,7 +1573,7 @@ static int step_impl(const LumaStepArgs *a, void *stream, void *const *events) {
     return fail("luma_step: null table pointer");
   const int32_t c = a->chunk_elems ? a->chunk_elems : (int32_t)LUMA_CHUNK_ELEMS;
   if (c < LUMA_CHUNK_ELEMS_MIN || c > LUMA_CHUNK_ELEMS || (c & (c - 1)) != 0)
-    return fail("luma_step: chunk_elems must be a power of two in [2048, 65536]");
+    return fail("luma_step: chunk_elems must be a power of two in [LUMA_CHUNK_ELEMS_MIN, LUMA_CHUNK_ELEMS]");
   StepSrc src{};
   src.tensors = reinterpret_cast<const Tensor *>(a->tensors);
   src.chunks = a->chunks;

@@ -2,7 +2,7 @@
 
 Every element is computed on its own (its Philox uniforms are keyed by the
 element's index in the tensor, not by its chunk) and the per-tensor maxima
-are exact, so the same step at chunk lengths 2048, 16384 and 65536 must give
+are exact, so the same step at chunk lengths 2048, 16384, 65536 and 131072 must give
 bit-identical parameters, codes and scales.
 """
 
@@ -13,7 +13,7 @@ from luma_amd import LUMA
 
 pytestmark = pytest.mark.gpu
 
-SHAPES = [(1,), (2047,), (3 * 2048 + 5,), (65536 + 7,), (300, 700), (4096, 64)]
+SHAPES = [(1,), (2047,), (3 * 2048 + 5,), (65536 + 7,), (300, 700), (4096, 64), (2 * 131072 + 77,)]
 
 
 def _run(chunk, grad_dtype, steps=3):
@@ -40,8 +40,8 @@ def _run(chunk, grad_dtype, steps=3):
 
 @pytest.mark.parametrize("grad_dtype", [torch.float32, torch.bfloat16])
 def test_chunk_length_invariance(grad_dtype):
-    ref_p, ref_s = _run(65536, grad_dtype)
-    for chunk in (2048, 16384):
+    ref_p, ref_s = _run(131072, grad_dtype)
+    for chunk in (2048, 16384, 65536):
         print(f"case chunk={chunk} grad={grad_dtype}", flush=True)
         ps, st = _run(chunk, grad_dtype)
         for i, (a, b) in enumerate(zip(ps, ref_p)):
@@ -54,8 +54,8 @@ def test_chunk_length_invariance(grad_dtype):
 def test_chunk_length_change_between_steps():
     """Steps that re-use the cached tensor table (same parameters and gradient
     tensors) at a different chunk length each step."""
-    ref_p, ref_s = _run(65536, torch.bfloat16)
-    ps, st = _run([65536, 2048, 16384], torch.bfloat16)
+    ref_p, ref_s = _run(131072, torch.bfloat16)
+    ps, st = _run([131072, 2048, 16384], torch.bfloat16)
     for i, (a, b) in enumerate(zip(ps, ref_p)):
         assert torch.equal(a.view(torch.int32), b.view(torch.int32)), i
         assert torch.equal(st[i]["Q_m"].cpu(), ref_s[i]["Q_m"].cpu()), i
@@ -63,7 +63,7 @@ def test_chunk_length_change_between_steps():
 
 
 def test_automatic_chunk_choice():
-    """A small tensor set steps with shorter chunks; a large one keeps 65536."""
+    """A small tensor set steps with shorter chunks."""
     p = torch.zeros(4096, 4096, device="cuda", requires_grad=True)
     opt = LUMA([p], lr=1e-3)
     p.grad = torch.full_like(p, 1e-3)

@@ -70,13 +70,12 @@ def test_exact_heterogeneous_scales():
     _check_exact(res)
 
 
-@pytest.mark.parametrize("chunk", [65536, 16384])
+@pytest.mark.parametrize("chunk", [131072, 65536, 16384])
 def test_pass1_pruning_adversarial(chunk):
     """Pass 1 skips the per-element decode of an iteration when a bound on its
     groups' |m'| and v' is below the running thresholds.  Layouts whose
-    maxima sit in the last iteration of a chunk (of 65536 or of 16384
-    elements), a hair above everything before them, must still give the
-    exact S_m and S_v."""
+    maxima sit late in a chunk (of 131072, 65536 or 16384 elements), a hair
+    above everything before them, must still give the exact S_m and S_v."""
     print(f"case pruning chunk={chunk}", flush=True)
     n = 2 * 65536 + 4096
     late = [65536 - 3, 2 * 65536 - 1, n - 2]

@@ -138,7 +138,7 @@ def test_sparse_grad_rejected():
 
 
 def test_step_chunk_policy():
-    """The step's chunk length: 65536 while that gives 4096 workgroups, else
+    """The step's chunk length: 131072 while that gives 4096 workgroups, else
     halved down to 16384; a fixed length overrides it."""
     import types
     import numpy as np
@@ -146,18 +146,19 @@ def test_step_chunk_policy():
     pick = _Engine.chunk_for
     auto = types.SimpleNamespace(chunk_elems=0)
     assert pick(auto, np.array([4096 * 4096], dtype=np.int64)) == 16384
-    assert pick(auto, np.array([65536] * 4096, dtype=np.int64)) == 65536
+    assert pick(auto, np.array([65536] * 4096, dtype=np.int64)) == 131072
+    assert pick(auto, np.array([131072] * 2048, dtype=np.int64)) == 65536
     assert pick(auto, np.array([65536] * 4095, dtype=np.int64)) == 32768
     assert pick(auto, np.array([65536] * 2048, dtype=np.int64)) == 32768
     assert pick(auto, np.array([65536] * 2047, dtype=np.int64)) == 16384
-    assert pick(auto, np.array([1] * 20000, dtype=np.int64)) == 65536
+    assert pick(auto, np.array([1] * 20000, dtype=np.int64)) == 131072
     assert pick(types.SimpleNamespace(chunk_elems=2048), np.array([10], dtype=np.int64)) == 2048
 
 
 def test_step_rejects_bad_chunk_length():
     """luma_step validates chunk_elems before any launch."""
     lib = L.load()
-    for bad in (1000, 1024, 131072, 3 * 4096):
+    for bad in (1000, 1024, 262144, 3 * 4096):
         args = L.StepArgs(tensors=16, n_tensors=1, n_chunks=1, chunks=16, groups=16, partials=16,
                           base_seed=0, noise_mode=L.NOISE_PHILOX, flags=0, chunk_elems=bad,
                           reserved=0, scaling=L.Scaling(None, None))
