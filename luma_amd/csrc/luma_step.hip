@@ -38,7 +38,7 @@ constexpr int kThreads = 256;     // 4 wave64 per workgroup
 constexpr int kVec = 8;           // consecutive elements per thread per iteration
 constexpr int64_t kChunk = LUMA_CHUNK_ELEMS;
 static_assert(kChunk % (kThreads * kVec) == 0, "chunk must be a whole number of iterations");
-static_assert(kChunk <= (1 << 20), "pass 2 iteration indices of a chunk offset stay small");
+static_assert(kChunk <= (1 << 20), "chunk offsets fit the 32-bit word of a pass-2 queue entry");
 static_assert(LUMA_CHUNK_ELEMS_MIN % (kThreads * kVec) == 0,
               "every chunk length must be a whole number of iterations");
 
