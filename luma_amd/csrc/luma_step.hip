@@ -20,7 +20,8 @@
 // the other elements for the exact path, 64 at a time.  Pass 2 keeps each
 // wave's new preconditioner codes in LDS for a few iterations so that the
 // exact codes land there before the codes go to HBM, and it streams the
-// gradients and parameters non-temporally so that L2 holds the code lines.
+// gradients, parameters and preconditioner codes non-temporally so that L2
+// holds the momentum code lines.
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
@@ -367,11 +368,12 @@ __device__ __forceinline__ float grad_hi(uint32_t w) {
 
 // Cache policy of the streams.  The gradients, and pass 2's parameters, are
 // touched once per step: they are loaded (and stored) non-temporally, so that
-// they are the first lines L2 evicts.  The codes keep the normal policy:
-// pass 2 overwrites some of its new codes again after the exact path has
-// run for them, a few iterations later, and those late 2-byte stores are
-// cheap while the line is still in L2 but cost a partial-line write-back to
-// HBM once it has been evicted.
+// they are the first lines L2 evicts.  So are pass 2's preconditioner codes,
+// which reach HBM only as whole staged vectors.  The momentum codes keep the
+// normal policy: pass 2 overwrites some of its new momentum codes again after
+// the exact path has run for them, some iterations later, and those late
+// 2-byte stores are cheap while the line is still in L2 but cost a
+// partial-line write-back to HBM once it has been evicted.
 template <typename V>
 __device__ __forceinline__ V load_stream(const LUMA_GLOBAL V *p) {
   return __builtin_nontemporal_load(p);
@@ -424,12 +426,12 @@ __device__ __forceinline__ void unpack_raw(const Raw8 &r, Group8 &G) {
 }
 
 // Load the codes and gradients of elements e0 .. e0+7 (n of them valid).
-// STREAM: the gradient vectors are loaded non-temporally.
+// STREAM: the gradient and preconditioner-code vectors are loaded non-temporally.
 template <int GD, bool STREAM = false>
 __device__ __forceinline__ void load_group(const Tensor &T, int64_t e0, int n, bool vec, Group8 &G) {
   if (vec) {
     const vu4 a = *(const LUMA_GLOBAL vu4 *)(T.q_m + e0);
-    const vu4 b = *(const LUMA_GLOBAL vu4 *)(T.q_w + e0);
+    const vu4 b = STREAM ? load_stream((const LUMA_GLOBAL vu4 *)(T.q_w + e0)) : *(const LUMA_GLOBAL vu4 *)(T.q_w + e0);
     unpack_i16(a.x, G.qm[0], G.qm[1]);
     unpack_i16(a.y, G.qm[2], G.qm[3]);
     unpack_i16(a.z, G.qm[4], G.qm[5]);
@@ -1251,7 +1253,7 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     const int64_t e = beg + ((int64_t)j * kThreads + threadIdx.x) * kVec;
     vu4 w;
     w.x = v.x; w.y = v.y; w.z = v.z; w.w = v.w;
-    *(LUMA_GLOBAL vu4 *)(T.q_w + e) = w;
+    store_stream(w, (LUMA_GLOBAL vu4 *)(T.q_w + e));
   };
   // Every lane runs the same number of iterations (lanes past the end carry
   // n = 0), so the ballots and the queue lengths stay uniform across the wave.
