@@ -402,22 +402,22 @@ def main():
         torch.cuda.synchronize()
     print("bench: warmup done", file=sys.stderr, flush=True)
 
-    evs = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
-    for e in evs:
-        e.record()
-    torch.cuda.synchronize()
-    opt._engine.profile_events = evs
-    k_times = [[], [], []]
+    # one set of four events per timed step (before pass 1, after pass 1,
+    # after finalize, after pass 2), so that the steps run back to back as
+    # in a training loop, with no synchronisation between them
+    ev_sets = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    for es in ev_sets:
+        for e in es:
+            e.record()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for es in ev_sets:
+        opt._engine.profile_events = es
         opt.step()
-        torch.cuda.synchronize()
-        for k in range(3):
-            k_times[k].append(evs[k].elapsed_time(evs[k + 1]))
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     opt._engine.profile_events = None
+    k_times = [[es[k].elapsed_time(es[k + 1]) for es in ev_sets] for k in range(3)]
     ms = wall * 1e3 / args.steps
 
     avg = [sum(v) / len(v) for v in k_times]
