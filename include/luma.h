@@ -54,7 +54,7 @@
 extern "C" {
 #endif
 
-#define LUMA_ABI_VERSION 4
+#define LUMA_ABI_VERSION 5
 
 /*
  * Elements per chunk-table entry (one workgroup's share of a tensor): the
@@ -78,7 +78,12 @@ extern "C" {
 #define LUMA_GRAD_BF16 1
 #define LUMA_GRAD_F16 2
 
-/* Where the stochastic-rounding uniforms come from. */
+/*
+ * Where the stochastic-rounding uniforms come from.  Under
+ * LUMA_NOISE_INJECTED a tensor whose u_m or u_w is NULL draws from Philox as
+ * under LUMA_NOISE_PHILOX, so a caller may inject uniforms for some tensors
+ * of a step only.
+ */
 #define LUMA_NOISE_PHILOX 0   /* counter-based Philox4x32-10, keyed per (seed, step, param) */
 #define LUMA_NOISE_INJECTED 1 /* caller-supplied u_m / u_w float32 arrays in [0, 1) */
 
@@ -96,6 +101,10 @@ typedef struct LumaTensor {
   void *slot;           /* device, LUMA_SLOT_BYTES: this tensor's state     */
   int64_t numel;        /* elements                                          */
   int64_t param_id;     /* position of the parameter in param_groups order  */
+  int64_t elem_offset;  /* index of element 0 in the whole parameter when this
+                           tensor is one shard of it, else 0: the Philox
+                           counters follow the whole parameter's element
+                           index, so shards draw independent uniforms       */
   int32_t grad_dtype;   /* LUMA_GRAD_*                                       */
   int32_t group;        /* index into the LumaGroup table                    */
   int32_t first_chunk;  /* index of this tensor's first LumaChunk            */

@@ -9,9 +9,18 @@
 //   key      = seed = ((t << 32) | 2*param_id) ^ base_seed  (the reference's
 //              per-step seed, functional.py:99-106), split lo/hi.
 //   element e gets two 24-bit uniforms u_m(e), u_w(e) in [0, 1):
-//     high 8 bits  -- bytes 2j, 2j+1 (j = e & 7) of block ctr = (e >> 3, 0, 0)
-//     low 16 bits  -- halves 2i, 2i+1 (i = e & 3) of block ctr = (e >> 2, 1, 0)
-//   (counter words: c0 = lo32(index), c1 = hi32(index), c2 = stream, c3 = 0).
+//     high 8 bits  -- bytes 2j, 2j+1 (j = e & 7) of the coarse block
+//                     ctr = (B + (e >> 3), 0, r)
+//     low 16 bits  -- halves 2i, 2i+1 (i = e & 3) of the fine block
+//                     ctr = (2B + (e >> 2), 1, r)
+//   (counter words: c0 = lo32(index), c1 = hi32(index), c2 = stream, c3 = r).
+// B = o >> 3 and r = o & 7 come from the tensor's element offset o: the
+// index of its element 0 in the whole parameter when the tensor is one shard
+// of it (0 otherwise).  A shard whose offset is a multiple of 8 therefore
+// draws exactly the uniforms of the same elements of the unsharded
+// parameter; shards with another offset draw from the disjoint counter
+// space r != 0, and two shards of one parameter never share a block (their
+// element ranges are disjoint, so their block ranges are too).
 // The split lets the fast path decide most roundings from one block per 8
 // elements and fetch the low bits only for the rare elements whose decision
 // depends on them.
@@ -92,15 +101,29 @@ __device__ __forceinline__ U4 philox4x32_10_v(uint32_t c0, uint32_t c1, uint32_t
 }
 #endif
 
-// Counter-block indices for element e (see the header comment).
-LUMA_PHILOX_FN U4 philox_coarse_block(uint64_t e, uint32_t k0, uint32_t k1) {
-  const uint64_t b = e >> 3;
-  return philox4x32_10((uint32_t)b, (uint32_t)(b >> 32), 0u, 0u, k0, k1);
+// Where a tensor's blocks start: B = offset >> 3 and r = offset & 7 of its
+// element offset (see the header comment).
+struct PhiloxBase {
+  uint64_t blk;
+  uint32_t rot;
+};
+
+LUMA_PHILOX_FN PhiloxBase philox_base(int64_t elem_offset) {
+  PhiloxBase b;
+  b.blk = (uint64_t)elem_offset >> 3;
+  b.rot = (uint32_t)elem_offset & 7u;
+  return b;
 }
 
-LUMA_PHILOX_FN U4 philox_fine_block(uint64_t e, uint32_t k0, uint32_t k1) {
-  const uint64_t b = e >> 2;
-  return philox4x32_10((uint32_t)b, (uint32_t)(b >> 32), 1u, 0u, k0, k1);
+// The coarse and fine blocks of element e of a tensor.
+LUMA_PHILOX_FN U4 philox_coarse_block(uint64_t e, PhiloxBase o, uint32_t k0, uint32_t k1) {
+  const uint64_t b = o.blk + (e >> 3);
+  return philox4x32_10((uint32_t)b, (uint32_t)(b >> 32), 0u, o.rot, k0, k1);
+}
+
+LUMA_PHILOX_FN U4 philox_fine_block(uint64_t e, PhiloxBase o, uint32_t k0, uint32_t k1) {
+  const uint64_t b = 2 * o.blk + (e >> 2);
+  return philox4x32_10((uint32_t)b, (uint32_t)(b >> 32), 1u, o.rot, k0, k1);
 }
 
 LUMA_PHILOX_FN uint32_t u4_word(const U4 &v, int i) {

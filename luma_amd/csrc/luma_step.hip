@@ -64,6 +64,7 @@ struct Tensor {
   LUMA_GLOBAL Slot *slot;
   int64_t numel;
   int64_t param_id;
+  int64_t elem_offset;
   int32_t grad_dtype;
   int32_t group;
   int32_t first_chunk;
@@ -160,6 +161,12 @@ __device__ __forceinline__ float load_grad(const LUMA_GLOBAL void *g, int64_t i,
   const uint16_t b = ((const LUMA_GLOBAL uint16_t *)g)[i];
   if (dt == LUMA_GRAD_BF16) return __uint_as_float((uint32_t)b << 16);
   return __half2float(__ushort_as_half(b));
+}
+
+// Whether tensor T takes injected uniforms: the launch asks for them and T
+// has both arrays (a tensor without them draws from Philox).
+__device__ __forceinline__ bool injected(const Tensor &T, int noise_mode) {
+  return noise_mode == LUMA_NOISE_INJECTED && T.u_m != nullptr && T.u_w != nullptr;
 }
 
 // Key of the (param, step) uniform stream: the reference's step seed
@@ -298,13 +305,15 @@ __global__ __launch_bounds__(kThreads) void pass2_exact_kernel(StepSrc src, uint
   chunk_range(src, T, ci, beg, end);
   uint32_t k0, k1;
   step_key(base_seed, t, T.param_id, k0, k1);
+  const PhiloxBase pb = philox_base(T.elem_offset);
+  const bool inj = injected(T, noise_mode);
 
   for (int64_t e0 = beg + (int64_t)threadIdx.x * kVec; e0 < end; e0 += (int64_t)kThreads * kVec) {
     U4 coarse{}, fine0{}, fine1{};
-    if (noise_mode == LUMA_NOISE_PHILOX) {
-      coarse = philox_coarse_block((uint64_t)e0, k0, k1);
-      fine0 = philox_fine_block((uint64_t)e0, k0, k1);
-      fine1 = philox_fine_block((uint64_t)e0 + 4, k0, k1);
+    if (!inj) {
+      coarse = philox_coarse_block((uint64_t)e0, pb, k0, k1);
+      fine0 = philox_fine_block((uint64_t)e0, pb, k0, k1);
+      fine1 = philox_fine_block((uint64_t)e0 + 4, pb, k0, k1);
     }
     for (int j = 0; j < kVec; ++j) {
       const int64_t i = e0 + j;
@@ -313,7 +322,7 @@ __global__ __launch_bounds__(kThreads) void pass2_exact_kernel(StepSrc src, uint
       element_ema(T, h, old, i, scaled, inv, mn, vn);
       T.param[i] = exact_param_update(T.param[i], mn, vn, h);
       float um, uw;
-      if (noise_mode == LUMA_NOISE_PHILOX) {
+      if (!inj) {
         uint32_t bm, bw;
         philox_uniform_bits(coarse, j < 4 ? fine0 : fine1, (uint64_t)i, bm, bw);
         um = (float)bm * 0x1p-24f;
@@ -897,6 +906,8 @@ constexpr float kCodeBias = 12582912.0f;
 struct P2Const {
   DecodeK D;
   uint32_t pk0, pk1, pm0, pm1;  // Philox key and multipliers
+  uint64_t pblk;                // Philox block base of the tensor (element offset >> 3)
+  uint32_t prot;                // and its counter word 3 (element offset & 7)
   float ndw;                    // -dw of the old grid (decode)
   float nbias;                  // 2^23 dw: fma(2^23 + q, -dw, nbias) = q * -dw exactly
   float nk1, nk2, hk3, nk7, hk8;   // -k1, -k2, 0.5 - k3, -k7, 0.5 - k8
@@ -988,8 +999,9 @@ __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, i
       zmu_w[j] = C.zoff - ((FULL || j < n) ? T.u_w[e0 + j] : 0.5f);
     }
   } else {
-    const uint64_t b = (uint64_t)e0 >> 3;   // coarse block of elements e0 .. e0+7
-    coarse = philox4x32_10_v((uint32_t)b, (uint32_t)(b >> 32), 0u, 0u, C.pk0, C.pk1, C.pm0, C.pm1);
+    const uint64_t b = C.pblk + ((uint64_t)e0 >> 3);   // coarse block of elements e0 .. e0+7
+    coarse = philox4x32_10_v((uint32_t)b, (uint32_t)(b >> 32), 0u, C.prot, C.pk0, C.pk1, C.pm0,
+                             C.pm1);
 #pragma unroll
     for (int j = 0; j < kVec; ++j) {
       zmu_m[j] = fmaf((float)u4_byte(coarse, 2 * j), -1.0f / 256.0f, C.zoff);
@@ -1113,6 +1125,9 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   C.pk1 = k1;
   C.pm0 = kPhiloxM0;
   C.pm1 = kPhiloxM1;
+  const PhiloxBase pb = philox_base(T.elem_offset);
+  C.pblk = pb.blk;
+  C.prot = pb.rot;
   C.ndw = -C.D.dw;
   C.nbias = 8388608.0f * C.D.dw;
   C.nk1 = -C.k1;
@@ -1141,7 +1156,7 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     const float hi = (float)((top << 16) | 0xFFFFu) * 0x1p-24f;
     bool b = p > hi;                  // u <= hi < p
     if (p > lo && !b) {               // else u >= lo >= p (a NaN p also: false)
-      const U4 fine = philox_fine_block((uint64_t)i, k0, k1);
+      const U4 fine = philox_fine_block((uint64_t)i, pb, k0, k1);
       b = (float)((top << 16) | u4_half(fine, 2 * (int)(i & 3) + which)) * 0x1p-24f < p;
     }
     return b;
@@ -1342,7 +1357,7 @@ __global__ __launch_bounds__(kThreads) void pass2_fast_kernel(StepSrc src, uint6
   chunk_range(src, T, ci, beg, end);
   uint32_t k0, k1;
   step_key(base_seed, t, T.param_id, k0, k1);
-  const bool inj = noise_mode == LUMA_NOISE_INJECTED;
+  const bool inj = injected(T, noise_mode);
   const bool small = (old == nullptr || old->fast[kXTopM] <= kSmall) && nw->sm <= kSmall;
   const bool scaled = src.scaling.grad_scale != nullptr;
   const float inv = inv_scale(src);
@@ -1454,9 +1469,9 @@ __global__ __launch_bounds__(kThreads) void quant_kernel(const float *__restrict
   for (int64_t e0 = beg + (int64_t)threadIdx.x * kVec; e0 < end; e0 += (int64_t)kThreads * kVec) {
     U4 coarse{}, fine0{}, fine1{};
     if (noise_mode == LUMA_NOISE_PHILOX) {
-      coarse = philox_coarse_block((uint64_t)e0, k0, k1);
-      fine0 = philox_fine_block((uint64_t)e0, k0, k1);
-      fine1 = philox_fine_block((uint64_t)e0 + 4, k0, k1);
+      coarse = philox_coarse_block((uint64_t)e0, PhiloxBase{0, 0}, k0, k1);
+      fine0 = philox_fine_block((uint64_t)e0, PhiloxBase{0, 0}, k0, k1);
+      fine1 = philox_fine_block((uint64_t)e0 + 4, PhiloxBase{0, 0}, k0, k1);
     }
     for (int j = 0; j < kVec; ++j) {
       const int64_t i = e0 + j;

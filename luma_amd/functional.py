@@ -83,8 +83,10 @@ def _luma_step_op(param: torch.Tensor, grad: torch.Tensor, Q_m: torch.Tensor,
                   lr: float, weight_decay: float, param_id: int, base_seed: int,
                   u_m: Optional[torch.Tensor] = None, u_w: Optional[torch.Tensor] = None,
                   exact: bool = False, grad_scale: Optional[torch.Tensor] = None,
-                  found_inf: Optional[torch.Tensor] = None) -> None:
+                  found_inf: Optional[torch.Tensor] = None, elem_offset: int = 0) -> None:
     _check(param, grad, Q_m, Q_w, slot, u_m, u_w)
+    if elem_offset < 0:
+        raise ValueError("luma_step: elem_offset must be >= 0")
     for name, t in (("grad_scale", grad_scale), ("found_inf", found_inf)):
         if t is not None and (t.numel() != 1 or t.dtype != torch.float32
                               or t.device != param.device):
@@ -104,6 +106,7 @@ def _luma_step_op(param: torch.Tensor, grad: torch.Tensor, Q_m: torch.Tensor,
     tt["slot"] = slot.data_ptr()
     tt["numel"] = n
     tt["param_id"] = param_id
+    tt["elem_offset"] = elem_offset
     tt["grad_dtype"] = _GRAD_CODES[grad.dtype]
     gg = np.array([(lr, beta1, beta2, eps, weight_decay, 0.0)], dtype=L.GROUP_DTYPE)
     nch = (n + L.STEP_TENSOR_CHUNK_MIN - 1) // L.STEP_TENSOR_CHUNK_MIN   # at most this many chunks
@@ -121,7 +124,7 @@ def _luma_step_op(param: torch.Tensor, grad: torch.Tensor, Q_m: torch.Tensor,
 @_luma_step_op.register_fake
 def _luma_step_fake(param, grad, Q_m, Q_w, slot, beta1, beta2, eps, lr, weight_decay, param_id,
                     base_seed, u_m=None, u_w=None, exact=False, grad_scale=None,
-                    found_inf=None) -> None:
+                    found_inf=None, elem_offset=0) -> None:
     return None
 
 
@@ -130,7 +133,7 @@ def luma_step(param: torch.Tensor, grad: torch.Tensor, Q_m: torch.Tensor, Q_w: t
               weight_decay: float, param_id: int, base_seed: int,
               u_m: Optional[torch.Tensor] = None, u_w: Optional[torch.Tensor] = None,
               exact: bool = False, grad_scale: Optional[torch.Tensor] = None,
-              found_inf: Optional[torch.Tensor] = None) -> None:
+              found_inf: Optional[torch.Tensor] = None, elem_offset: int = 0) -> None:
     """One LUMA step of one tensor, in place.
 
     The init step (functional.py:183-228) when ``slot`` holds step count 0,
@@ -141,10 +144,15 @@ def luma_step(param: torch.Tensor, grad: torch.Tensor, Q_m: torch.Tensor, Q_w: t
     ``grad_scale`` / ``found_inf`` (one-element float32 device tensors) are
     GradScaler's: the gradient is unscaled in the kernel as ``unscale_``
     would store it, and a nonzero ``found_inf`` skips the step on the device.
+    ``elem_offset``: when ``param`` is one shard of a larger parameter, the
+    index of its first element in the whole (flattened) parameter; the Philox
+    counters follow that index, so shards draw independent uniforms (and a
+    shard whose offset is a multiple of 8 draws exactly the uniforms of the
+    same elements of the unsharded parameter).
     """
     torch.ops.luma_amd.luma_step(param, grad, Q_m, Q_w, slot, beta1, beta2, eps, lr,
                                  weight_decay, param_id, base_seed, u_m, u_w, exact, grad_scale,
-                                 found_inf)
+                                 found_inf, elem_offset)
 
 
 def init_slot(slot: torch.Tensor, step: int, S_m: float, S_v: float, eps: float) -> None:

@@ -57,6 +57,39 @@ def _ptr(t: Optional[torch.Tensor]) -> int:
     return 0 if t is None else t.data_ptr()
 
 
+def shard_offset(t) -> int:
+    """Index, in the whole parameter's flattened (row-major) elements, of the
+    first element of a DTensor's local shard, when that shard is one
+    contiguous range of the whole parameter (a ``Shard(0)`` placement, as
+    FSDP2 uses, or any placement that leaves the shard whole); 0 for plain
+    tensors.  The step keys its Philox counters on ``offset + local index``,
+    so the shards of one parameter draw independent uniforms.  A shard that
+    is not one contiguous range (e.g. ``Shard(1)`` of a matrix) keys on its
+    local index, as the reference's Triton path does for every shard
+    (triton_kernel.py:296-301)."""
+    if not hasattr(t, "_local_tensor") or not hasattr(t, "device_mesh"):
+        return 0
+    try:
+        from torch.distributed.tensor._utils import compute_local_shape_and_global_offset
+    except ImportError:   # pragma: no cover - older torch
+        return 0
+    gshape = tuple(t.shape)
+    lshape, goff = compute_local_shape_and_global_offset(gshape, t.device_mesh, t.placements)
+    lshape, goff = tuple(lshape), tuple(goff)
+    diff = [d for d in range(len(gshape)) if lshape[d] != gshape[d]]
+    if diff:
+        d0 = diff[0]
+        # contiguous: every dim before d0 has extent 1, every dim after d0 is whole
+        if any(gshape[d] != 1 for d in range(d0)) or any(lshape[d] != gshape[d]
+                                                           for d in range(d0 + 1, len(gshape))):
+            return 0
+    off, stride = 0, 1
+    for d in range(len(gshape) - 1, -1, -1):
+        off += goff[d] * stride
+        stride *= gshape[d]
+    return int(off)
+
+
 _ARENA_ALIGN = 128   # int16 elements: every Q tensor starts on a 256-byte boundary
 
 
@@ -138,7 +171,7 @@ class _Engine:
 
     def table(self, rows) -> np.ndarray:
         """Tensor table of rows: (param, grad, q_m, q_w, u_m, u_w, slot, param_id,
-        grad_code, group) per tensor, chunks numbered consecutively."""
+        grad_code, group, elem_offset) per tensor, chunks numbered consecutively."""
         n = len(rows)
         tt = np.zeros(n, dtype=L.TENSOR_DTYPE)
         numels = np.fromiter((r[0].numel() for r in rows), dtype=np.int64, count=n)
@@ -157,6 +190,7 @@ class _Engine:
         tt["slot"] = [r[6].data_ptr() for r in rows]
         tt["numel"] = numels
         tt["param_id"] = [r[7] for r in rows]
+        tt["elem_offset"] = [r[10] for r in rows]
         tt["grad_dtype"] = [r[8] for r in rows]
         tt["group"] = [r[9] for r in rows]
         tt["first_chunk"] = first
@@ -341,13 +375,16 @@ class LUMA(Optimizer):
     Stores two int16 tensors per parameter (signed log-grid momentum ``Q_m``,
     unsigned log-grid preconditioner ``Q_w``): 4 bytes/param of state.
 
-    ``backend`` accepts ``"auto"``, ``"hip"`` and ``"triton"`` (an alias kept
-    for drop-in use); all select the HIP library.  Parameters must be float32
-    and live on a ROCm GPU; gradients may be float32, bfloat16 or float16
-    (others are promoted to float32 first).
+    ``backend`` accepts the reference's names ``"auto"``, ``"triton"`` and
+    ``"pytorch"`` (optimizer.py:98-113), and ``"hip"``; every name selects the
+    HIP library, whose stochastic rounding draws from Philox (as the
+    reference's GPU backend does) rather than from the CPU generator of its
+    PyTorch backend.  Parameters must be float32 and live on a ROCm GPU;
+    gradients may be float32, bfloat16 or float16 (others are promoted to
+    float32 first).
     """
 
-    _BACKENDS = ("auto", "hip", "triton")
+    _BACKENDS = ("auto", "triton", "pytorch", "hip")
 
     # torch.amp.GradScaler: instead of unscaling the gradients and checking
     # them on the host before calling step(), the scaler sets
@@ -376,9 +413,11 @@ class LUMA(Optimizer):
             torch.randint(-(2**63), 2**63 - 1, (1,), dtype=torch.int64).item())
         if backend not in self._BACKENDS:
             raise ValueError(f"Invalid backend: {backend}. Expected one of "
-                             "{'auto', 'hip', 'triton'} (all three select the HIP library).")
+                             "{'auto', 'triton', 'pytorch', 'hip'} (every name selects the HIP "
+                             "library).")
         self._engine: Optional[_Engine] = None
         self._noise: Optional[Dict[int, Tuple[torch.Tensor, torch.Tensor]]] = None
+        self._noise_strict = True
         self._flags = 0
         self._plan: Optional[_Plan] = None
         self._scaling_keep = []
@@ -403,17 +442,22 @@ class LUMA(Optimizer):
                                f"({self._engine.device} vs {device})")
         return self._engine
 
-    def inject_noise(self, noise: Dict[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]):
+    def inject_noise(self, noise: Dict[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]],
+                     strict: bool = True):
         """Use the given uniforms (u_m, u_w), float32 in [0, 1) with each parameter's
         shape and device, for the next ``step()`` or ``import_adamw_state()``
-        instead of Philox draws.  Every parameter updated by that call needs an
-        entry."""
+        instead of Philox draws.  With ``strict`` every parameter updated by
+        that call needs an entry; otherwise parameters without one draw from
+        Philox as usual."""
         self._noise = {id(p): (u_m, u_w) for p, (u_m, u_w) in noise.items()}
+        self._noise_strict = strict
 
     def _take_noise(self, p, like):
         if self._noise is None:
             return None, None
         if id(p) not in self._noise:
+            if not self._noise_strict:
+                return None, None
             raise ValueError("LUMA.inject_noise: missing uniforms for a parameter")
         u_m, u_w = self._noise[id(p)]
         out = []
@@ -572,7 +616,6 @@ class LUMA(Optimizer):
             for p in group["params"]:
                 group_of[len(all_params)] = group
                 all_params.append(p)
-        noise_mode = L.NOISE_INJECTED if self._noise is not None else L.NOISE_PHILOX
         for idx_key, s in adamw_sd["state"].items():
             idx = int(idx_key) if isinstance(idx_key, str) else idx_key
             if idx >= len(all_params):
@@ -591,6 +634,7 @@ class LUMA(Optimizer):
             state = self.state[p]
             slot = state["_slot"] if "_slot" in state else engine.new_slots(1)[0]
             u_m, u_w = self._take_noise(p, param)
+            noise_mode = L.NOISE_PHILOX if u_m is None else L.NOISE_INJECTED
             seed = make_step_seed(self._base_seed, 0, idx)   # optimizer.py:315-317
             engine.quantize(m, v, q_m, q_w, slot, step, group["eps"], seed, noise_mode, u_m, u_w)
             state["step"] = step
@@ -693,7 +737,7 @@ class LUMA(Optimizer):
                 grad = torch.empty_like(param, dtype=grad.dtype).copy_(grad)
             u_m, u_w = self._take_noise(p, param)
             rows.append((param, grad, state["Q_m"], state["Q_w"], u_m, u_w, state["_slot"],
-                         state["param_id"], code, gi))
+                         state["param_id"], code, gi, shard_offset(p)))
         tt = engine.table(rows)
         engine.launch(tt, self._group_table(), self._base_seed, noise_mode, self._flags,
                       self._scaling(engine.device))

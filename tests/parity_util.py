@@ -32,6 +32,8 @@ class StepStats:
 @dataclass
 class PairResult:
     steps: List[StepStats] = field(default_factory=list)
+    # per step: {"S_m": [per tensor], "S_v": [per tensor]} of the HIP optimizer
+    scales: List[dict] = field(default_factory=list)
 
     def total_mismatch(self):
         return sum(s.qm_mismatch + s.qw_mismatch for s in self.steps)
@@ -122,4 +124,5 @@ def run_pair(shapes, grad_fn: Callable, n_steps: int, math_mode: str = "cr",
             scale = float(p.abs().max())
             st.p_rel = max(st.p_rel, float((pd - p).abs().max()) / max(scale, 1e-30))
         res.steps.append(st)
+        res.scales.append({k: [sd["state"][i][k] for i in range(len(cpu))] for k in ("S_m", "S_v")})
     return res

@@ -97,12 +97,17 @@ def test_pass1_pruning_adversarial(chunk):
             # decay but stay the maxima while everything else is small
             g = torch.Generator().manual_seed(11 * t)
             x = torch.randn(shape, generator=g) * 1e-5
-            if t == 0:
+            if t == 1:   # run_pair numbers its steps from 1
                 x[late[0]] = 0.5
                 x[late[2]] = -0.25
         return x
     res = run_pair([(n,), (n,), (n,)], grads, n_steps=4, math_mode="cr", chunk_elems=chunk)
     _check_exact(res)
+    # the large t = 1 gradient set tensor 2's scales: S_m = f32(1 - beta1) * 0.5
+    # at t = 1 (functional.py:201-219), and it stays the maximum as it decays
+    s_m = [st["S_m"][2] for st in res.scales]
+    assert s_m[0] == float(torch.tensor(0.1, dtype=torch.float32) * 0.5), s_m
+    assert all(a > b > 1e-3 for a, b in zip(s_m, s_m[1:])), s_m
 
 
 def test_multi_group_exact():

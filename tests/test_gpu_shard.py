@@ -1,0 +1,207 @@
+"""Sharded parameters on one GPU: the global element offset of a shard keys
+its Philox counters, a DTensor parameter steps through its local shard, and
+uniforms may be injected for some tensors of a step only.
+
+Reference: optimizer.py:399-407 and 434-435 (a DTensor's local shard is
+stepped), tests/test_fsdp.py:139-184 (per-shard scales); the reference's
+Triton path keys its noise on the local offset (triton_kernel.py:296-301),
+which makes the shards of one parameter draw the same noise.
+"""
+
+import socket
+
+import pytest
+import torch
+
+import luma_amd.optimizer as optmod
+from luma_amd import LUMA
+from luma_amd.functional import luma_step as f_step
+from luma_amd.functional import new_slot
+from oracle import luma_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+HYPER = dict(lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01)
+BASE = 0x243F6A8885A308D3 - (1 << 64)
+
+
+def _grads(t, n, half, j):
+    """N(0, 1e-3) with one large gradient at position j of each half (equal
+    in both, so the halves' scales equal the whole tensor's)."""
+    g = torch.Generator().manual_seed(500 + t)
+    x = torch.randn(n, generator=g) * 1e-3
+    x[j] = x[half + j] = 0.05 * (1.0 + 0.1 * t)
+    return x.cuda()
+
+
+def _new(p):
+    opt = LUMA([p], **HYPER)
+    opt._base_seed = BASE
+    return opt
+
+
+def _set_state(opt, p, q_m, q_w, step, s_m, s_v):
+    sd = opt.state_dict()
+    sd["state"] = {0: {"step": step, "param_id": 0, "Q_m": q_m.clone(), "Q_w": q_w.clone(),
+                       "S_m": s_m, "S_v": s_v}}
+    opt.load_state_dict(sd)
+
+
+@pytest.mark.parametrize("half", [40000, 40003])
+def test_halves_with_offsets_equal_whole(monkeypatch, half):
+    """A parameter stepped as two shards, each keyed on its global offset,
+    equals the parameter stepped whole, bit for bit, when the shard offset is
+    a multiple of 8 (then every element draws the uniforms of the same
+    element of the whole).  Each step starts both from the whole's state,
+    with the two maximum elements given equal codes, so every scale agrees.
+    An offset that is not a multiple of 8 draws from a disjoint counter space:
+    there the second shard's codes differ from the whole's."""
+    n, j = 2 * half, 123
+    offsets = {}
+    monkeypatch.setattr(optmod, "shard_offset", lambda p: offsets.get(id(p), 0))
+    gen = torch.Generator().manual_seed(7)
+    p0 = (torch.randn(n, generator=gen) * 0.02).cuda()
+    whole = p0.clone().requires_grad_(True)
+    a = p0[:half].clone().requires_grad_(True)
+    b = p0[half:].clone().requires_grad_(True)
+    offsets[id(b)] = half
+    ow, oa, ob = _new(whole), _new(a), _new(b)
+    aligned = half % 8 == 0
+    for t in range(1, 4):
+        if t > 1:
+            sd = ow.state_dict()["state"][0]
+            q_m, q_w = sd["Q_m"].clone(), sd["Q_w"].clone()
+            q_m[half + j], q_w[half + j] = q_m[j], q_w[j]
+            _set_state(ow, whole, q_m, q_w, t - 1, sd["S_m"], sd["S_v"])
+            _set_state(oa, a, q_m[:half], q_w[:half], t - 1, sd["S_m"], sd["S_v"])
+            _set_state(ob, b, q_m[half:], q_w[half:], t - 1, sd["S_m"], sd["S_v"])
+            with torch.no_grad():
+                a.copy_(whole[:half])
+                b.copy_(whole[half:])
+        g = _grads(t, n, half, j)
+        whole.grad, a.grad, b.grad = g, g[:half].clone(), g[half:].clone()
+        for o in (ow, oa, ob):
+            o.step()
+        torch.cuda.synchronize()
+        sw, sa, sb = (o.state_dict()["state"][0] for o in (ow, oa, ob))
+        assert sw["S_m"] == sa["S_m"] == sb["S_m"] and sw["S_v"] == sa["S_v"] == sb["S_v"], t
+        assert torch.equal(sw["Q_m"][:half], sa["Q_m"]) and torch.equal(sw["Q_w"][:half], sa["Q_w"])
+        assert torch.equal(whole.detach()[:half], a.detach())
+        assert torch.equal(whole.detach()[half:], b.detach())   # the update draws nothing
+        same_m = torch.equal(sw["Q_m"][half:], sb["Q_m"])
+        same_w = torch.equal(sw["Q_w"][half:], sb["Q_w"])
+        if aligned:
+            assert same_m and same_w, t
+        else:
+            assert not same_m and not same_w, t
+
+
+def test_functional_offset_equals_whole():
+    """The one-tensor entry point (luma_step_tensor) keys on elem_offset too:
+    the second half of a tensor stepped with offset n/2 equals the whole
+    tensor's second half after an init step whose maxima are equal in both
+    halves, and differs from it with offset 0."""
+    half, j = 65536, 11
+    n = 2 * half
+    gen = torch.Generator().manual_seed(3)
+    p0 = (torch.randn(n, generator=gen) * 0.02).cuda()
+    g = _grads(1, n, half, j)
+    args = dict(beta1=0.9, beta2=0.999, eps=1e-8, lr=1e-3, weight_decay=0.01, param_id=4,
+                base_seed=BASE)
+    out = {}
+    for name, (lo, hi, off) in {"whole": (0, n, 0), "b": (half, n, half),
+                                "b0": (half, n, 0)}.items():
+        p = p0[lo:hi].clone()
+        qm = torch.empty(hi - lo, dtype=torch.int16, device="cuda")
+        qw = torch.empty_like(qm)
+        f_step(p, g[lo:hi].contiguous(), qm, qw, new_slot("cuda"), elem_offset=off, **args)
+        out[name] = (p, qm, qw)
+    torch.cuda.synchronize()
+    assert torch.equal(out["whole"][1][half:], out["b"][1])
+    assert torch.equal(out["whole"][2][half:], out["b"][2])
+    assert not torch.equal(out["whole"][1][half:], out["b0"][1])
+
+
+def test_partial_injection():
+    """Uniforms injected for one tensor of a step (strict=False): that tensor
+    matches the oracle's codes, the others draw from Philox exactly as in a
+    step without injection."""
+    shapes = [(4099,), (300, 70), (1,)]
+    gen = torch.Generator().manual_seed(11)
+    cpu = [torch.randn(s, generator=gen) * 0.02 for s in shapes]
+    dev = [p.clone().cuda().requires_grad_(True) for p in cpu]
+    ref = [p.clone().cuda().requires_grad_(True) for p in cpu]
+    oracle = O.OracleLUMA([dict(params=cpu, **HYPER)], BASE, "cr")
+    opt = LUMA(dev, **HYPER)
+    plain = LUMA(ref, **HYPER)
+    opt._base_seed = plain._base_seed = BASE
+    for t in range(1, 4):
+        if t > 1:
+            # each step starts from the oracle's state for tensor 1 and from
+            # the Philox run's state otherwise
+            sd = opt.state_dict()
+            o = oracle.state[id(cpu[1])]
+            sd["state"][1].update(Q_m=o["Q_m"].clone(), Q_w=o["Q_w"].clone(), S_m=o["S_m"],
+                                  S_v=o["S_v"])
+            opt.load_state_dict(sd)
+            with torch.no_grad():
+                dev[1].copy_(cpu[1])
+        grads = [torch.randn(s, generator=gen) * 1e-3 for s in shapes]
+        for p, g in zip(cpu, grads):
+            p.grad = g
+        oracle.step()
+        for d, r, g in zip(dev, ref, grads):
+            d.grad, r.grad = g.cuda(), g.cuda()
+        u_m, u_w = oracle.last_draws[1]
+        opt.inject_noise({dev[1]: (u_m.cuda(), u_w.cuda())}, strict=False)
+        opt.step()
+        plain.step()
+        torch.cuda.synchronize()
+        sd, sp = opt.state_dict()["state"], plain.state_dict()["state"]
+        o = oracle.state[id(cpu[1])]
+        assert torch.equal(sd[1]["Q_m"].cpu(), o["Q_m"]) and torch.equal(sd[1]["Q_w"].cpu(), o["Q_w"])
+        assert sd[1]["S_m"] == o["S_m"] and sd[1]["S_v"] == o["S_v"]
+        err = float((dev[1].detach().cpu() - cpu[1]).abs().max()) / float(cpu[1].abs().max())
+        assert err <= 1e-6, err
+        for i in (0, 2):
+            assert torch.equal(sd[i]["Q_m"], sp[i]["Q_m"]) and torch.equal(sd[i]["Q_w"], sp[i]["Q_w"])
+            assert torch.equal(dev[i].detach(), ref[i].detach())
+
+
+def _free_port() -> int:
+    with socket.socket() as s:
+        s.bind(("127.0.0.1", 0))
+        return s.getsockname()[1]
+
+
+def test_dtensor_local_shard_world_size_one():
+    """A DTensor parameter (Shard(0) on a one-GPU mesh) steps through its
+    local shard (optimizer.py:399-407): bit-identical to the plain tensor."""
+    import torch.distributed as dist
+    from torch.distributed.device_mesh import init_device_mesh
+    from torch.distributed.tensor import Shard, distribute_tensor
+
+    dist.init_process_group("nccl", init_method=f"tcp://127.0.0.1:{_free_port()}", rank=0,
+                            world_size=1)
+    try:
+        mesh = init_device_mesh("cuda", (1,))
+        gen = torch.Generator().manual_seed(5)
+        w0 = torch.randn(96, 40, generator=gen) * 0.02
+        dp = torch.nn.Parameter(distribute_tensor(w0.cuda(), mesh, [Shard(0)]))
+        pp = torch.nn.Parameter(w0.cuda())
+        assert optmod.shard_offset(dp) == 0
+        od, op_ = LUMA([dp], **HYPER), LUMA([pp], **HYPER)
+        od._base_seed = op_._base_seed = BASE
+        for t in range(3):
+            g = torch.randn(96, 40, generator=gen) * 1e-3
+            dp.grad = distribute_tensor(g.cuda(), mesh, [Shard(0)])
+            pp.grad = g.cuda()
+            od.step()
+            op_.step()
+        torch.cuda.synchronize()
+        assert torch.equal(dp.to_local(), pp.detach())
+        sd, sp = od.state_dict()["state"][0], op_.state_dict()["state"][0]
+        assert torch.equal(sd["Q_m"], sp["Q_m"]) and torch.equal(sd["Q_w"], sp["Q_w"])
+        assert sd["S_m"] == sp["S_m"] and sd["S_v"] == sp["S_v"] and sd["step"] == 3
+    finally:
+        dist.destroy_process_group()
