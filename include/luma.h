@@ -25,6 +25,9 @@
  *                         skip-on-overflow around it (the reference runs
  *                         them outside the optimizer).
  *   luma_step_profiled -- luma_step with event records between its launches.
+ *   luma_step_noalloc  -- luma_step with its workspace inside the library
+ *                         (no counterpart in the reference; for callers that
+ *                         cannot allocate).
  *   luma_step_tensor   -- one tensor, no device tables: the per-tensor
  *                         functional ops luma_triton_step /
  *                         luma_triton_init_step (triton_kernel.py:409-492).
@@ -201,6 +204,25 @@ int luma_step(const LumaStepArgs *args, void *stream);
  * entries are skipped).  Used to time each kernel on its own stream.
  */
 int luma_step_profiled(const LumaStepArgs *args, void *stream, void *const events[4]);
+
+/*
+ * Largest n_chunks luma_step_noalloc takes: its workspace is a fixed device
+ * array of 2 floats per chunk (2 MiB per GPU).
+ */
+#define LUMA_NOALLOC_MAX_CHUNKS 262144
+
+/*
+ * luma_step that allocates nothing and takes no workspace: args->partials is
+ * ignored, and pass 1's per-chunk maxima go to a fixed array inside the
+ * library (one per GPU, kept until the process ends), so no memory is
+ * allocated on any call, the first included.  No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Limits:
+ * n_chunks <= LUMA_NOALLOC_MAX_CHUNKS (else an error, nothing launched); the
+ * stream's device must be the current device; calls that overlap on one GPU
+ * (other streams, other threads) share that GPU's array and race.
+ */
+int luma_step_noalloc(const LumaStepArgs *args, void *stream);
 
 /*
  * luma_step for one tensor with no device tables: *tensor, *group and

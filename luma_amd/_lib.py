@@ -20,6 +20,7 @@ CHUNK_ELEMS = 131072         # LUMA_CHUNK_ELEMS (default and largest chunk lengt
 CHUNK_ELEMS_MIN = 2048       # LUMA_CHUNK_ELEMS_MIN
 STEP_TENSOR_CHUNK_MIN = 16384  # LUMA_STEP_TENSOR_CHUNK_MIN
 SLOT_BYTES = 512             # LUMA_SLOT_BYTES
+NOALLOC_MAX_CHUNKS = 262144  # LUMA_NOALLOC_MAX_CHUNKS
 ABI_VERSION = 5              # LUMA_ABI_VERSION
 
 GRAD_F32, GRAD_BF16, GRAD_F16 = 0, 1, 2
@@ -79,6 +80,7 @@ _SIGNATURES = {
     "luma_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int32]),
     "luma_layout": (None, [ctypes.POINTER(ctypes.c_int32)]),
     "luma_step": (ctypes.c_int, [ctypes.POINTER(StepArgs), _VP]),
+    "luma_step_noalloc": (ctypes.c_int, [ctypes.POINTER(StepArgs), _VP]),
     "luma_step_profiled": (ctypes.c_int, [ctypes.POINTER(StepArgs), _VP,
                                           ctypes.POINTER(ctypes.c_void_p)]),
     "luma_step_tensor": (ctypes.c_int, [_VP, _VP, _VP, ctypes.c_uint64, ctypes.c_int32,

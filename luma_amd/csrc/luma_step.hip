@@ -25,6 +25,7 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
+#include <mutex>
 #include <stdio.h>
 #include <string.h>
 
@@ -1516,6 +1517,16 @@ __global__ void hyper_rows_kernel(LumaGroup g, int64_t t0, int n, float *__restr
 
 using namespace luma;
 
+// Workspace of luma_step_noalloc: pass 1's two maxima per chunk, for at most
+// LUMA_NOALLOC_MAX_CHUNKS chunks (2 MiB).  Each GPU the library runs on holds
+// its own copy until the process ends.  In host code `scratch` only names the
+// symbol; its device address (one per device) comes from hipGetSymbolAddress.
+static __device__ __align__(256) float scratch[2 * (size_t)LUMA_NOALLOC_MAX_CHUNKS];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static float *g_scratch_ptr[kMaxDevices] = {};
+
 static thread_local char g_err[512] = "";
 
 static int fail(const char *msg, hipError_t e = hipSuccess) {
@@ -1606,6 +1617,43 @@ int luma_step(const LumaStepArgs *a, void *stream) { return step_impl(a, stream,
 
 int luma_step_profiled(const LumaStepArgs *a, void *stream, void *const events[4]) {
   return step_impl(a, stream, events);
+}
+
+// Device address of this device's `scratch`, looked up on the first call
+// made with the device current and kept for later calls.
+static int scratch_for(hipStream_t stream, float **out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail("luma_step_noalloc: hipGetDevice", e);
+  if (stream) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(stream, &sdev);
+    if (e != hipSuccess) return fail("luma_step_noalloc: hipStreamGetDevice", e);
+    if ((int)sdev != dev) return fail("luma_step_noalloc: the stream's device must be the current device");
+  }
+  if (dev < 0 || dev >= kMaxDevices) return fail("luma_step_noalloc: device index out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) return fail("luma_step_noalloc: hipGetSymbolAddress(scratch)", e);
+    g_scratch_ptr[dev] = static_cast<float *>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+int luma_step_noalloc(const LumaStepArgs *a, void *stream) {
+  if (!a) return fail("luma_step_noalloc: null args");
+  if (a->n_tensors <= 0 || a->n_chunks <= 0) return 0;
+  if (a->n_chunks > LUMA_NOALLOC_MAX_CHUNKS)
+    return fail("luma_step_noalloc: more chunks than LUMA_NOALLOC_MAX_CHUNKS (use luma_step with a "
+                "caller-allocated workspace, or a longer chunk_elems)");
+  float *ws = nullptr;
+  if (int r = scratch_for(static_cast<hipStream_t>(stream), &ws)) return r;
+  LumaStepArgs b = *a;
+  b.partials = ws;   // every chunk writes its two maxima before finalize reads them
+  return step_impl(&b, stream, nullptr);
 }
 
 int luma_step_tensor(const LumaTensor *tensor, const LumaGroup *group, float *partials,
