@@ -22,7 +22,7 @@ from oracle import luma_oracle as O
 pytestmark = pytest.mark.gpu
 
 HYPER = dict(lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01)
-BASE = 0x243F6A8885A308D3 - (1 << 64)
+BASE = -0x243F6A8885A308D3   # a negative _base_seed, as torch.randint may draw
 
 
 def _grads(t, n, half, j):
