@@ -106,16 +106,42 @@ def decode_uint16(q: Tensor) -> Tensor:
     return (q.to(torch.int32) & 0xFFFF).float()
 
 
+def log_sr_threshold(y: Tensor, delta: float, z_denom: float, math_mode="torch"):
+    """functional.py:61-64 -- ``floor(y)`` and the round-up probability
+    ``p* = expm1(frac(y) * delta) / z_denom`` of LogSR (delta > 0)."""
+    M = _m(math_mode)
+    fl = y.floor()
+    frac = y - fl
+    return fl, M.expm1(frac * delta) / z_denom
+
+
 def log_sr(y: Tensor, delta: float, z_denom: float, rand: Tensor, k_max: int,
            math_mode="torch") -> Tensor:
     """functional.py:38-67 -- log-to-linear corrected stochastic rounding."""
-    M = _m(math_mode)
     if delta <= 0.0:
         return torch.zeros_like(y)
-    fl = y.floor()
-    frac = y - fl
-    p_star = M.expm1(frac * delta) / z_denom
+    fl, p_star = log_sr_threshold(y, delta, z_denom, math_mode)
     return (fl + (rand < p_star).to(y.dtype)).clamp(0, k_max)
+
+
+def momentum_bin(m: Tensor, S_m: float, delta_m: float, math_mode="torch"):
+    """functional.py:142-143 -- the clamped momentum and its continuous bin
+    index ``y = log1p(|clamp(m, +-S_m)|) / delta_m``."""
+    M = _m(math_mode)
+    m_clip = m.clamp(-S_m, S_m)
+    return m_clip, M.log1p(m_clip.abs()) / delta_m
+
+
+def preconditioner_bin(v: Tensor, eps: float, w_min: float, delta_w: float,
+                       math_mode="torch") -> Tensor:
+    """functional.py:163-169 -- the continuous bin index of ``w = 1/(sqrt(v)+eps)``
+    on the preconditioner grid (0 when delta_w <= 0)."""
+    M = _m(math_mode)
+    w = 1.0 / (M.sqrt(v.clamp_min(0)) + eps)
+    w_clip = w.clamp(w_min, 1.0 / eps)
+    if delta_w > 0.0:
+        return M.log(w_clip / w_min) / delta_w
+    return torch.zeros_like(w_clip)
 
 
 def precompute(S_m: float, S_v: float, eps: float):
@@ -162,8 +188,7 @@ def quantize_momentum(m: Tensor, S_m: float, delta_m: float, z_m: float,
                       rand: Tensor, math_mode="torch") -> Tensor:
     """functional.py:133-150 (the uniforms are passed in instead of drawn)."""
     M = _m(math_mode)
-    m_clip = m.clamp(-S_m, S_m)
-    y = M.log1p(m_clip.abs()) / delta_m
+    m_clip, y = momentum_bin(m, S_m, delta_m, M)
     q_mag = log_sr(y, delta_m, z_m, rand, K_M, M)
     return (m_clip.sign() * q_mag).to(torch.int16)
 
@@ -172,12 +197,7 @@ def quantize_preconditioner(v: Tensor, eps: float, w_min: float, delta_w: float,
                             z_w: float, rand: Tensor, math_mode="torch") -> Tensor:
     """functional.py:153-176 (the uniforms are passed in instead of drawn)."""
     M = _m(math_mode)
-    w = 1.0 / (M.sqrt(v.clamp_min(0)) + eps)
-    w_clip = w.clamp(w_min, 1.0 / eps)
-    if delta_w > 0.0:
-        y = M.log(w_clip / w_min) / delta_w
-    else:
-        y = torch.zeros_like(w_clip)
+    y = preconditioner_bin(v, eps, w_min, delta_w, M)
     q = log_sr(y, delta_w, z_w, rand, K_W, M)
     return encode_uint16(q.to(torch.int32))
 
@@ -234,14 +254,18 @@ def injected_draw(u_m: Tensor, u_w: Tensor) -> Draw:
 #  Step functions (functional.py:183-298)
 # ---------------------------------------------------------------------------
 
+def init_moments(grad: Tensor, beta1: float, beta2: float):
+    """functional.py:200-204 -- the first step's moments ``m = (1-b1) g``,
+    ``v = (1-b2) g^2`` (float32, the scalar cast once)."""
+    g = grad.float()
+    return (1.0 - beta1) * g, (1.0 - beta2) * g.square()
+
+
 def init_step(param: Tensor, grad: Tensor, beta1: float, beta2: float, eps: float,
               lr: float, weight_decay: float, draw: Draw, math_mode="torch"):
     """functional.py:183-228.  Mutates ``param``; returns (Q_m, Q_w, S_m, S_v)."""
     M = _m(math_mode)
-    g = grad.float()
-    m = (1.0 - beta1) * g
-    v = (1.0 - beta2) * g.square()
-    del g
+    m, v = init_moments(grad, beta1, beta2)
     bc1 = 1.0 - beta1
     bc2 = 1.0 - beta2
     eta_t = lr / bc1

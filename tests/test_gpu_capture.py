@@ -5,7 +5,8 @@ tests/test_compile.py, and its device step counter, optimizer.py:382-387).
   double arithmetic (luma_hyper_rows);
 * LUMA.step() captured into a CUDA (HIP) graph after eager warm-up steps and
   replayed: after every replay the parameters, codes, scales and step counts
-  equal those of an identical optimizer stepped eagerly (bitwise);
+  equal those of an identical optimizer stepped eagerly (bitwise), and, with
+  the oracle's uniforms refilled into the captured buffers, the oracle's;
 * a capture whose tables would change is refused before anything launches;
 * the per-tensor op (luma_amd.functional.luma_step) equals the multi-tensor
   step bit for bit, including its init step;
@@ -146,6 +147,73 @@ def test_graph_replay_matches_eager(gdt):
     torch.cuda.synchronize()
     _assert_same(_state(opt_a, pa), _state(opt_b, pb), "eager after replay")
     assert opt_a.state[pa[0]]["step"] == 9
+
+
+def test_graph_replay_matches_oracle():
+    """A captured LUMA.step() against the correctly rounded CPU oracle: the
+    injected-uniform buffers are persistent (the graph reads them), refilled
+    with the oracle's draws of each step before the replay, and every replay's
+    codes and scales must equal the oracle's, parameters within 1e-6 of their
+    scale (the reference's compiled-step test, tests/test_compile.py:181-242,
+    with its device step counter, optimizer.py:382-387)."""
+    from oracle import luma_oracle as O
+
+    hyper = dict(lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01)
+    pa = _params(5)
+    cpu = [p.detach().cpu().clone() for p in pa]
+    for c in cpu:
+        c.grad_dtype = None
+    grads = _grad_sets(8, torch.bfloat16, 6)
+    base = 0x3C6EF372FE94F82B
+    oracle = O.OracleLUMA([dict(params=cpu, **hyper)], base, "cr")
+    opt = LUMA(pa, **hyper)
+    opt._base_seed = base
+    for p, g in zip(pa, grads[0]):
+        p.grad = torch.empty_like(g)
+    u_bufs = {p: (torch.empty_like(p), torch.empty_like(p)) for p in pa}
+
+    def load(k):
+        """Step k's gradients into both, the oracle's step, and its draws into
+        the uniform buffers the captured step reads."""
+        for p, c, g in zip(pa, cpu, grads[k]):
+            p.grad.copy_(g)
+            c.grad = g.cpu()
+        oracle.step()
+        for i, p in enumerate(pa):
+            u_m, u_w = oracle.last_draws[i]
+            u_bufs[p][0].copy_(u_m)
+            u_bufs[p][1].copy_(u_w)
+
+    def check(where):
+        sd = opt.state_dict()["state"]
+        for i, (p, c) in enumerate(zip(pa, cpu)):
+            o = oracle.state[id(c)]
+            assert torch.equal(sd[i]["Q_m"].cpu(), o["Q_m"]), f"{where}: Q_m {i}"
+            assert torch.equal(sd[i]["Q_w"].cpu(), o["Q_w"]), f"{where}: Q_w {i}"
+            assert (sd[i]["S_m"], sd[i]["S_v"]) == (o["S_m"], o["S_v"]), f"{where}: S {i}"
+            assert sd[i]["step"] == o["step"], f"{where}: step {i}"
+            err = float((p.detach().cpu() - c).abs().max())
+            assert err <= 1e-6 * float(c.abs().max()) + 1e-8, f"{where}: param {i} {err}"
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for k in range(2):          # warm-up: init step + one update, eagerly
+            load(k)
+            opt.inject_noise(u_bufs)
+            opt.step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    check("warm-up")
+    graph = torch.cuda.CUDAGraph()
+    opt.inject_noise(u_bufs)
+    with torch.cuda.graph(graph):
+        opt.step()
+    for k in range(2, 8):
+        load(k)
+        graph.replay()
+        torch.cuda.synchronize()
+        check(f"replay {k - 1}")
 
 
 def test_capture_refuses_changed_tables(monkeypatch):

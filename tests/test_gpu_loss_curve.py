@@ -19,13 +19,20 @@ agreement threshold, 0.5% relative (tests/test_correctness.py:333-339):
 * native noise -- HIP draws from Philox, the oracle from torch.Generator, so
   the curves are two independent samples of the same stochastic rounding.
 
+* injected noise, exact path -- the library's exact per-element path
+  (LUMA_FLAG_EXACT_ONLY), whose parameter update is the reference's float32
+  operation sequence with correctly rounded sqrt: the two runs must stay
+  identical to within 1e-6 at every evaluation point.
+
 While the loss falls fastest (steps 700-1000 here) training amplifies any
-difference: with injected noise the curves agree to 5e-6 up to step 600,
-and at step 1000 two update roundings that each meet the 1e-6 per-step
-bound gave 0.13% and 0.84%; native noise gave 0.77%.  So each evaluation
-point must be within 1.5%, and the mean over the curve -- which a bias in
-the noise, the rounding or the update would move -- within 0.2% (injected)
-and 0.5% (native; the reference's backend-agreement threshold,
+difference: with injected noise the fast path's curve agrees to 5e-6 up to
+step 600, and at step 1000 the update's rounding (within 1e-6 per step, but
+not the reference's bits) has grown to 0.84% (measured on MI355X; native
+noise: 0.77%).  The exact-path run shows that nothing else differs.  So each
+evaluation point of the fast path must be within 1.0% (the measured 0.84%
+plus a 20% margin), and the mean over the curve -- which a bias in the
+noise, the rounding or the update would move -- within 0.2% (injected) and
+0.5% (native; the reference's backend-agreement threshold,
 tests/test_correctness.py:333-339).
 """
 
@@ -39,6 +46,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from luma_amd import LUMA
+from luma_amd import _lib as L
 from oracle import luma_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -48,8 +56,8 @@ EVAL_EVERY = 100
 BLOCK, BATCH = 64, 32
 N_LAYER, N_HEAD, N_EMBD = 4, 4, 128
 LR, BETAS, WD, CLIP = 3e-4, (0.9, 0.95), 0.1, 1.0
-POINT_TOL = 1.5e-2
-MEAN_TOL = {True: 2e-3, False: 5e-3}    # injected / native
+POINT_TOL = {"injected": 1.0e-2, "native": 1.0e-2, "exact": 1e-6}
+MEAN_TOL = {"injected": 2e-3, "native": 5e-3, "exact": 1e-6}
 
 
 def synthetic_text(n_chars=400_000, seed=0):
@@ -141,7 +149,7 @@ def _eval(model, batches):
     return sum(float(model(x, y)) for x, y in batches) / len(batches)
 
 
-def _run(inject):
+def _run(inject, exact=False):
     torch.manual_seed(1234)
     data, vocab = synthetic_text()
     split = int(0.9 * len(data))
@@ -157,6 +165,8 @@ def _run(inject):
     cpu_b = [p.detach().cpu().clone() for p in params_b]
 
     opt = LUMA(_groups(params_a))
+    if exact:
+        opt._flags = L.FLAG_EXACT_ONLY
     oracle = O.OracleLUMA(_groups(cpu_b), opt._base_seed, math_mode="cr")
     order_a = [p for g in opt.param_groups for p in g["params"]]
 
@@ -191,15 +201,15 @@ def _run(inject):
 
 
 @pytest.mark.timeout(600)
-@pytest.mark.parametrize("inject", [True, False], ids=["injected", "native"])
-def test_loss_curves_match_oracle(inject):
-    print(f"case loss curve inject={inject}", flush=True)
-    curve = _run(inject)
+@pytest.mark.parametrize("mode", ["injected", "native", "exact"])
+def test_loss_curves_match_oracle(mode):
+    print(f"case loss curve {mode}", flush=True)
+    curve = _run(mode != "native", exact=mode == "exact")
     first, last = curve[0], curve[-1]
     assert last[2] < first[2] - 0.5, "the model did not train"
     for step, la, lb in curve:
-        assert abs(la - lb) / lb < POINT_TOL, (step, la, lb)
+        assert abs(la - lb) / lb <= POINT_TOL[mode], (step, la, lb)
     mean_a = sum(c[1] for c in curve) / len(curve)
     mean_b = sum(c[2] for c in curve) / len(curve)
     print(f"mean eval loss HIP {mean_a:.4f} oracle {mean_b:.4f}", flush=True)
-    assert abs(mean_a - mean_b) / mean_b < MEAN_TOL[inject]
+    assert abs(mean_a - mean_b) / mean_b <= MEAN_TOL[mode]
