@@ -117,43 +117,70 @@ def make_set(cfg, device):
 
 # ── CPU baseline: the oracle on a bounded sample ─────────────────────────────
 
-def cpu_baseline(cfg_name):
-    from oracle import luma_oracle as O
+def host_cores():
+    """CPU cores this process may use: its affinity set, capped by the cgroup's
+    CPU quota (cpu.max) when one is set."""
+    n = len(os.sched_getaffinity(0))
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            quota, period = f.read().split()
+        if quota != "max":
+            n = min(n, max(1, int(quota) // int(period)))
+    except (OSError, ValueError):
+        pass
+    return n
 
-    threads = min(16, os.cpu_count() or 1)
-    torch.set_num_threads(threads)
-    n = 4096 * 4096 if cfg_name != "many_small" else 4 * 1024 * 1024
-    gen = torch.Generator().manual_seed(1)
-    p = torch.randn(n, generator=gen) * 0.02
-    p.grad_dtype = None
-    gdt = CONFIGS[cfg_name]["grad"]
-    grads = [(torch.randn(n, generator=gen) * 1e-3).to(gdt) for _ in range(4)]
-    opt = O.OracleLUMA([dict(params=[p], lr=1e-3, betas=(0.9, 0.999), eps=1e-8,
-                             weight_decay=0.01)], 12345, "torch")
-    times = []
-    for i, g in enumerate(grads):
-        p.grad = g
-        t0 = time.perf_counter()
-        opt.step()
-        dt = time.perf_counter() - t0
-        if i >= 1:
-            times.append(dt)
-    times.sort()
-    med = times[len(times) // 2]
-    cpu_model = ""
+
+def cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
                 if line.startswith("model name"):
-                    cpu_model = line.split(":", 1)[1].strip()
-                    break
+                    return line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return {"value": round(n / med / 1e9, 6), "unit": "Gparams/s", "cores": threads,
-            "kind": "port",
-            "sample": f"oracle (reference PyTorch backend restated, torch CPU ops) on one "
-                      f"{n}-element fp32 tensor with {str(gdt).replace('torch.', '')} grads; "
-                      f"median of {len(times)} update steps after the init step; {cpu_model}"}
+    return ""
+
+
+def cpu_baseline(cfg_name, warmup=2, timed=5):
+    """The oracle in the reference's own math ("torch": ATen's CPU kernels) on
+    the configuration's largest tensor, with every core this process may use:
+    the init step and warmup - 1 update steps untimed, then the median of
+    ``timed`` update steps (time.perf_counter around each step)."""
+    from oracle import luma_oracle as O
+
+    cores = host_cores()
+    torch.set_num_threads(cores)
+    cfg = CONFIGS[cfg_name]
+    shape = max(cfg["shapes"](), key=math.prod)
+    n = math.prod(shape)
+    gen = torch.Generator().manual_seed(1)
+    p = torch.randn(n, generator=gen) * 0.02
+    p.grad_dtype = None
+    gdt = cfg["grad"]
+    grads = [(torch.randn(n, generator=gen) * 1e-3).to(gdt) for _ in range(2)]
+    opt = O.OracleLUMA([dict(params=[p], lr=1e-3, betas=(0.9, 0.999), eps=1e-8,
+                             weight_decay=0.01)], 12345, "torch")
+    times = []
+    for i in range(warmup + timed):
+        p.grad = grads[i % 2]
+        t0 = time.perf_counter()
+        opt.step()
+        dt = time.perf_counter() - t0
+        if i >= warmup:
+            times.append(dt)
+        print(f"bench: cpu baseline step {i + 1}/{warmup + timed} {dt:.2f} s", file=sys.stderr,
+              flush=True)
+    times.sort()
+    med = times[len(times) // 2]
+    return {"value": round(n / med / 1e9, 6), "unit": "Gparams/s", "cores": cores,
+            "kind": "port", "ms_per_step": round(med * 1e3, 1),
+            "sample": f"oracle (the reference's PyTorch backend restated, torch CPU ops) on the "
+                      f"configuration's largest tensor {tuple(shape)} ({n} fp32 params, "
+                      f"{str(gdt).replace('torch.', '')} grads); median of {timed} update steps "
+                      f"after the init step and {warmup - 1} untimed update step; "
+                      f"{cores} threads (all cores this process may use; os.cpu_count() "
+                      f"{os.cpu_count()}); {cpu_model()}"}
 
 
 # ── HBM traffic: rocprofv3 FETCH_SIZE / WRITE_SIZE, calibrated on a copy ─────
