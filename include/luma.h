@@ -57,7 +57,7 @@
 extern "C" {
 #endif
 
-#define LUMA_ABI_VERSION 5
+#define LUMA_ABI_VERSION 6
 
 /*
  * Elements per chunk-table entry (one workgroup's share of a tensor): the
@@ -75,6 +75,22 @@ extern "C" {
  * step is the reference's init step).  16-byte aligned.
  */
 #define LUMA_SLOT_BYTES 512
+
+/*
+ * Code summaries.  A tensor may carry a summary array of one uint32 per block
+ * of LUMA_SUMMARY_BLOCK elements (ceil(numel / LUMA_SUMMARY_BLOCK) entries,
+ * 4-byte aligned).  Each step's pass 2 writes, for every block, a bound on
+ * the codes it stored there: the largest |Q_m| and the smallest Q_w, widened
+ * by the step's certified decision margin.  The next step's pass 1 then
+ * bounds the block's |m'| and v' from the summary and the gradients alone,
+ * and reads the block's codes only when the block could hold the tensor's
+ * maximum.  Results do not depend on the summaries; they only save reads.
+ * The summaries are used only when the slot records that the previous step
+ * wrote them (luma_set_scales and luma_quantize clear that record).  A caller
+ * that rewrites a tensor's codes by other means between steps must also
+ * rewrite its slot with luma_set_scales, or pass a NULL summary.
+ */
+#define LUMA_SUMMARY_BLOCK 512
 
 /* Gradient element types. */
 #define LUMA_GRAD_F32 0
@@ -102,6 +118,8 @@ typedef struct LumaTensor {
   const float *u_m;     /* device [numel] injected uniforms, or NULL        */
   const float *u_w;     /* device [numel] injected uniforms, or NULL        */
   void *slot;           /* device, LUMA_SLOT_BYTES: this tensor's state     */
+  uint32_t *summary;    /* device [ceil(numel / LUMA_SUMMARY_BLOCK)] code
+                           summaries kept across steps, or NULL           */
   int64_t numel;        /* elements                                          */
   int64_t param_id;     /* position of the parameter in param_groups order  */
   int64_t elem_offset;  /* index of element 0 in the whole parameter when this

@@ -46,7 +46,7 @@ static_assert(sizeof(Grid) == 112, "grid layout");
 // decode reads grid[(t - 1) & 1].
 struct Slot {
   int64_t step;    // completed steps (0: no state yet, the next step is t = 1)
-  int64_t reserved;
+  int64_t summ_step;   // the step whose pass 2 wrote the tensor's code summaries (0: none)
   double s_m[2];
   double s_v[2];
   Hyper hyp;       // scalars of step `step` (written by the step's finalize)

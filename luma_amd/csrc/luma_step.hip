@@ -63,6 +63,7 @@ struct Tensor {
   const LUMA_GLOBAL float *u_m;
   const LUMA_GLOBAL float *u_w;
   LUMA_GLOBAL Slot *slot;
+  LUMA_GLOBAL uint32_t *summary;
   int64_t numel;
   int64_t param_id;
   int64_t elem_offset;
@@ -84,6 +85,7 @@ struct StepSrc {
   LumaGroup group;
   LumaScaling scaling;
   int32_t chunk_shift;   // log2 of the launch's chunk length
+  int32_t summaries;     // this launch's pass 2 writes the code summaries
 };
 
 // Elements [beg, end) of chunk ci of tensor T.
@@ -285,6 +287,7 @@ __global__ __launch_bounds__(64) void finalize_kernel(StepSrc src,
     s.grid[par] = g;
     s.hyp = h;
     s.step = t;
+    s.summ_step = (src.summaries && T.summary) ? t : 0;
   }
 }
 
@@ -649,6 +652,61 @@ __device__ __forceinline__ void unscale_group(Group8 &G, float inv) {
 // hardware exp2 that the margins cover).  When that bound is below the
 // thresholds Tm / Tv in every lane, no element of the iteration can be a
 // candidate and its per-element decode is skipped (am = av = 0).
+// Bound on the fast |m'| and v' of every element whose momentum code
+// magnitude is at most qa, preconditioner code at least qw_lo (kCodeFloat |
+// code) and gradient magnitude at most gb (float bits): the fast formulas
+// at those extremes (each non-decreasing in them, up to the few-ulp wobble
+// of the hardware exp2 that the margins cover).  Returns whether some lane's
+// bound reaches the thresholds Tm / Tv (float bits, wave-uniform).
+template <bool SMALL>
+__device__ __forceinline__ bool p1_reach(int qa, int qw_lo, uint32_t gb, const P1Const &K,
+                                         uint32_t Tm, uint32_t Tv) {
+  const FastEma fb = fast_ema<SMALL, false>(qa, qw_lo, __uint_as_float(gb), K.dm, K.ndw, K.nbias,
+                                            K.iwmin, K.eps, K.b1, K.omb1, K.b2, K.omb2, K.sign);
+  const uint32_t um = __float_as_uint(fb.mn * K.up_m) & 0x7FFFFFFFu;
+  const uint32_t uv = __float_as_uint(fmaf(fb.vn, K.up_v, K.abs_v)) & 0x7FFFFFFFu;
+  return __ballot(um >= Tm || uv >= Tv) != 0;
+}
+
+// Largest gradient magnitude of a group, as float bits (NaN above +Inf).
+__device__ __forceinline__ uint32_t group_gmax(const Group8 &G) {
+  uint32_t gb = 0;
+#pragma unroll
+  for (int j = 0; j < kVec; ++j) gb = max(gb, __float_as_uint(G.g[j]) & 0x7FFFFFFFu);
+  return gb;
+}
+
+// Fast |m'| and v' (float bits) of a group whose codes and gradients are in
+// G; elements j >= n give 0.  PRUNE: first the group bound at the lane's own
+// code extremes; when no lane reaches the thresholds, every value is 0 (no
+// element of the iteration can be a candidate) and the per-element decode is
+// skipped.
+template <bool SMALL, bool PRUNE>
+__device__ __forceinline__ void p1_compute(const Group8 &G, const P1Const &K, int n, uint32_t Tm,
+                                           uint32_t Tv, uint32_t (&am)[kVec], uint32_t (&av)[kVec]) {
+  if (PRUNE) {
+    int qa = 0, qw_lo = G.qw[0];
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) {
+      qa = max(qa, abs(G.qm[j]));
+      qw_lo = min(qw_lo, G.qw[j]);   // kCodeFloat | code: ordered as the codes
+    }
+    if (!p1_reach<SMALL>(qa, qw_lo, group_gmax(G), K, Tm, Tv)) {
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) am[j] = av[j] = 0u;
+      return;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kVec; ++j) {
+    const FastEma f = fast_ema<SMALL, false>(G.qm[j], G.qw[j], G.g[j], K.dm, K.ndw, K.nbias, K.iwmin,
+                                             K.eps, K.b1, K.omb1, K.b2, K.omb2, K.sign);
+    am[j] = __float_as_uint(f.mn) & 0x7FFFFFFFu;
+    av[j] = __float_as_uint(f.vn) & 0x7FFFFFFFu;
+    if (j >= n) am[j] = av[j] = 0u;
+  }
+}
+
 template <int GD, bool SMALL, bool SCALED, bool FULL, bool PRUNE>
 __device__ __forceinline__ void p1_iter(const Tensor &T, const P1Const &K, int64_t e0, int n,
                                         Raw8 &raw, int64_t en, uint32_t Tm, uint32_t Tv,
@@ -661,33 +719,33 @@ __device__ __forceinline__ void p1_iter(const Tensor &T, const P1Const &K, int64
     load_group<GD>(T, e0, n, false, G);
   }
   unscale_group<GD, SCALED>(G, K.inv);
-  if (PRUNE) {
-    int qa = 0, qw_lo = G.qw[0];
-    uint32_t gb = 0;
-#pragma unroll
-    for (int j = 0; j < kVec; ++j) {
-      qa = max(qa, abs(G.qm[j]));
-      qw_lo = min(qw_lo, G.qw[j]);   // kCodeFloat | code: ordered as the codes
-      gb = max(gb, __float_as_uint(G.g[j]) & 0x7FFFFFFFu);   // NaN above +Inf
-    }
-    const FastEma fb = fast_ema<SMALL, false>(qa, qw_lo, __uint_as_float(gb), K.dm, K.ndw,
-                                              K.nbias, K.iwmin, K.eps, K.b1, K.omb1, K.b2,
-                                              K.omb2, K.sign);
-    const uint32_t um = __float_as_uint(fb.mn * K.up_m) & 0x7FFFFFFFu;
-    const uint32_t uv = __float_as_uint(fmaf(fb.vn, K.up_v, K.abs_v)) & 0x7FFFFFFFu;
-    if (!__ballot(um >= Tm || uv >= Tv)) {
-#pragma unroll
-      for (int j = 0; j < kVec; ++j) am[j] = av[j] = 0u;
-      return;
-    }
+  p1_compute<SMALL, PRUNE>(G, K, FULL ? kVec : n, Tm, Tv, am, av);
+}
+
+// The gradient words of 8 consecutive elements (g1: float32 gradients only),
+// and their unpacking into G.g.
+template <int GD>
+__device__ __forceinline__ void load_grads(const Tensor &T, int64_t e0, Raw8 &r) {
+  if (GD == LUMA_GRAD_F32) {
+    r.g0 = load_stream((const LUMA_GLOBAL vu4 *)((const LUMA_GLOBAL float *)T.grad + e0));
+    r.g1 = load_stream((const LUMA_GLOBAL vu4 *)((const LUMA_GLOBAL float *)T.grad + e0 + 4));
+  } else {
+    r.g0 = load_stream((const LUMA_GLOBAL vu4 *)((const LUMA_GLOBAL uint16_t *)T.grad + e0));
   }
-#pragma unroll
-  for (int j = 0; j < kVec; ++j) {
-    const FastEma f = fast_ema<SMALL, false>(G.qm[j], G.qw[j], G.g[j], K.dm, K.ndw, K.nbias, K.iwmin,
-                                             K.eps, K.b1, K.omb1, K.b2, K.omb2, K.sign);
-    am[j] = __float_as_uint(f.mn) & 0x7FFFFFFFu;
-    av[j] = __float_as_uint(f.vn) & 0x7FFFFFFFu;
-    if (!FULL && j >= n) am[j] = av[j] = 0u;
+}
+
+template <int GD>
+__device__ __forceinline__ void unpack_grads(const Raw8 &r, Group8 &G) {
+  if (GD == LUMA_GRAD_F32) {
+    G.g[0] = __uint_as_float(r.g0.x); G.g[1] = __uint_as_float(r.g0.y);
+    G.g[2] = __uint_as_float(r.g0.z); G.g[3] = __uint_as_float(r.g0.w);
+    G.g[4] = __uint_as_float(r.g1.x); G.g[5] = __uint_as_float(r.g1.y);
+    G.g[6] = __uint_as_float(r.g1.z); G.g[7] = __uint_as_float(r.g1.w);
+  } else {
+    G.g[0] = grad_lo<GD>(r.g0.x); G.g[1] = grad_hi<GD>(r.g0.x);
+    G.g[2] = grad_lo<GD>(r.g0.y); G.g[3] = grad_hi<GD>(r.g0.y);
+    G.g[4] = grad_lo<GD>(r.g0.z); G.g[5] = grad_hi<GD>(r.g0.z);
+    G.g[6] = grad_lo<GD>(r.g0.w); G.g[7] = grad_hi<GD>(r.g0.w);
   }
 }
 
@@ -697,7 +755,12 @@ __device__ __forceinline__ void p1_iter(const Tensor &T, const P1Const &K, int64
 // whose fast value is below the threshold cannot be the exact maximum; the
 // others (in practice a few per chunk) go through the wave's queue to the
 // exact path.
-template <int GD, bool SMALL, bool SCALED>
+// SUMM: the tensor's code summaries of the previous step are valid (and
+// old != null, the tensor 16-byte aligned).  Then each whole-group
+// iteration first bounds its block from the summary and the gradients, and
+// loads the block's codes only when some lane's bound reaches the
+// thresholds: most blocks cost their gradients alone.
+template <int GD, bool SMALL, bool SCALED, bool SUMM>
 __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOBAL Grid *old,
                                 float inv, int64_t beg, int64_t end, float &exm, float &exv,
                                 uint32_t *queue) {
@@ -783,7 +846,43 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   // whole group, so that every iteration issues the same loads).
   const int n_whole = vec_ok ? (int)((end - beg) / kStride) : 0;
   int it = 0;
-  if (n_whole > 0) {
+  if (SUMM && n_whole > 0) {
+    // this wave's summary block in iteration 0; one block per iteration
+    static_assert(LUMA_SUMMARY_BLOCK == 64 * kVec, "a summary block is one wave iteration");
+    const LUMA_GLOBAL uint32_t *summ =
+        T.summary + (beg + (int64_t)(threadIdx.x >> 6) * LUMA_SUMMARY_BLOCK) / LUMA_SUMMARY_BLOCK;
+    constexpr int kBlocksPerIt = (int)(kStride / LUMA_SUMMARY_BLOCK);
+    Raw8 raw;   // gradients of the lane's next group, loaded one iteration ahead
+    load_grads<GD>(T, beg + (int64_t)threadIdx.x * kVec, raw);
+    uint32_t sw = summ[0];
+    for (; it < n_whole; ++it) {
+      const int64_t e0 = beg + ((int64_t)it * kThreads + threadIdx.x) * kVec;
+      const int nx = it + 1 < n_whole ? it + 1 : it;
+      Group8 G;
+      unpack_grads<GD>(raw, G);
+      const uint32_t s_cur = sw;
+      load_grads<GD>(T, beg + ((int64_t)nx * kThreads + threadIdx.x) * kVec, raw);
+      sw = summ[(int64_t)nx * kBlocksPerIt];
+      unscale_group<GD, SCALED>(G, K.inv);
+      // bound at the block's code extremes and the lane's largest |g|
+      if (!p1_reach<SMALL>((int)(s_cur & 0xFFFFu), (int)(kCodeFloat | (s_cur >> 16)),
+                           group_gmax(G), K, Tm, Tv))
+        continue;   // no element of the block can be a candidate: codes not read
+      const vu4 a = *(const LUMA_GLOBAL vu4 *)(T.q_m + e0);
+      const vu4 b = *(const LUMA_GLOBAL vu4 *)(T.q_w + e0);
+      unpack_i16(a.x, G.qm[0], G.qm[1]);
+      unpack_i16(a.y, G.qm[2], G.qm[3]);
+      unpack_i16(a.z, G.qm[4], G.qm[5]);
+      unpack_i16(a.w, G.qm[6], G.qm[7]);
+      unpack_u16(b.x, G.qw[0], G.qw[1]);
+      unpack_u16(b.y, G.qw[2], G.qw[3]);
+      unpack_u16(b.z, G.qw[4], G.qw[5]);
+      unpack_u16(b.w, G.qw[6], G.qw[7]);
+      uint32_t am[kVec], av[kVec];
+      p1_compute<SMALL, true>(G, K, kVec, Tm, Tv, am, av);
+      take(e0, kVec, am, av);
+    }
+  } else if (n_whole > 0) {
     Raw8 raw;
     load_raw<GD>(T, beg + (int64_t)threadIdx.x * kVec, raw);
     for (; it < n_whole; ++it) {
@@ -814,18 +913,38 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   }
 }
 
+template <int GD, bool SUMM>
+__device__ __forceinline__ void pass1_dispatch_s(const Tensor &T, const Hyper &h,
+                                                 const LUMA_GLOBAL Grid *old, float inv,
+                                                 int64_t beg, int64_t end, bool small,
+                                                 bool scaled, float &exm, float &exv,
+                                                 uint32_t *q) {
+  if (scaled) {
+    if (small) pass1_fast_body<GD, true, true, SUMM>(T, h, old, inv, beg, end, exm, exv, q);
+    else pass1_fast_body<GD, false, true, SUMM>(T, h, old, inv, beg, end, exm, exv, q);
+  } else {
+    if (small) pass1_fast_body<GD, true, false, SUMM>(T, h, old, inv, beg, end, exm, exv, q);
+    else pass1_fast_body<GD, false, false, SUMM>(T, h, old, inv, beg, end, exm, exv, q);
+  }
+}
+
 template <int GD>
 __device__ __forceinline__ void pass1_dispatch(const Tensor &T, const Hyper &h,
                                                const LUMA_GLOBAL Grid *old, float inv,
                                                int64_t beg, int64_t end, bool small, bool scaled,
-                                               float &exm, float &exv, uint32_t *q) {
-  if (scaled) {
-    if (small) pass1_fast_body<GD, true, true>(T, h, old, inv, beg, end, exm, exv, q);
-    else pass1_fast_body<GD, false, true>(T, h, old, inv, beg, end, exm, exv, q);
-  } else {
-    if (small) pass1_fast_body<GD, true, false>(T, h, old, inv, beg, end, exm, exv, q);
-    else pass1_fast_body<GD, false, false>(T, h, old, inv, beg, end, exm, exv, q);
-  }
+                                               bool summ, float &exm, float &exv, uint32_t *q) {
+  if (summ) pass1_dispatch_s<GD, true>(T, h, old, inv, beg, end, small, scaled, exm, exv, q);
+  else pass1_dispatch_s<GD, false>(T, h, old, inv, beg, end, small, scaled, exm, exv, q);
+}
+
+// Whether pass 1 may use the tensor's code summaries: the previous step's
+// pass 2 wrote them (the slot records it), its grid is finite, and the
+// tensor's streams are 16-byte aligned (the whole-group loop).
+__device__ __forceinline__ bool summaries_valid(const Tensor &T, const LUMA_GLOBAL Grid *old,
+                                                int64_t prev) {
+  return T.summary != nullptr && old != nullptr && T.slot->summ_step == prev &&
+         __builtin_isfinite(old->dm) && __builtin_isfinite(old->dw) &&
+         __builtin_isfinite(old->fast[kIwmin]) && tensor_vec_ok(T);
 }
 
 __global__ __launch_bounds__(kThreads, 4) void pass1_fast_kernel(StepSrc src,
@@ -846,13 +965,14 @@ __global__ __launch_bounds__(kThreads, 4) void pass1_fast_kernel(StepSrc src,
   const float inv = inv_scale(src);
   __shared__ uint32_t qbuf[kThreads / 64][kQueueCap];
   uint32_t *q = qbuf[threadIdx.x >> 6];
+  const bool summ = summaries_valid(T, old, prev);
   float exm = 0.0f, exv = 0.0f;
   if (T.grad_dtype == LUMA_GRAD_BF16)
-    pass1_dispatch<LUMA_GRAD_BF16>(T, h, old, inv, beg, end, small, scaled, exm, exv, q);
+    pass1_dispatch<LUMA_GRAD_BF16>(T, h, old, inv, beg, end, small, scaled, summ, exm, exv, q);
   else if (T.grad_dtype == LUMA_GRAD_F16)
-    pass1_dispatch<LUMA_GRAD_F16>(T, h, old, inv, beg, end, small, scaled, exm, exv, q);
+    pass1_dispatch<LUMA_GRAD_F16>(T, h, old, inv, beg, end, small, scaled, summ, exm, exv, q);
   else
-    pass1_dispatch<LUMA_GRAD_F32>(T, h, old, inv, beg, end, small, scaled, exm, exv, q);
+    pass1_dispatch<LUMA_GRAD_F32>(T, h, old, inv, beg, end, small, scaled, summ, exm, exv, q);
   block_max2(exm, exv);
   if (threadIdx.x == 0) {
     partials[2 * (int64_t)blockIdx.x] = exm;
@@ -975,10 +1095,61 @@ __device__ __forceinline__ void launder(P2Const &C) {
 // code); Q and coarse are kept for the queues.
 // STAGE (FULL only): the preconditioner codes go to *stage (LDS) instead
 // of HBM.
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// Extremes of 8 stored codes as one word: the largest momentum code
+// magnitude in the low half, 65535 - the smallest preconditioner code in the
+// high half, so that the halfwise maximum of such words over a wave
+// (wave_max_u16x2) gives both extremes.  From the packed 16-byte store
+// vectors: packed 16-bit integer max/min, two codes per instruction.
+// (The words are copied into scalars first: this compiler's
+// __builtin_bit_cast of a vector element such as a.y reads the vector's
+// first word instead.)
+__device__ __forceinline__ uint32_t code_extremes(vu4 a, vu4 b) {
+  const uint32_t ax = a.x, ay = a.y, az = a.z, aw = a.w;
+  const uint32_t bx = b.x, by = b.y, bz = b.z, bw = b.w;
+  const s16x2 a0 = __builtin_bit_cast(s16x2, ax), a1 = __builtin_bit_cast(s16x2, ay);
+  const s16x2 a2 = __builtin_bit_cast(s16x2, az), a3 = __builtin_bit_cast(s16x2, aw);
+  const s16x2 mx = __builtin_elementwise_max(__builtin_elementwise_max(a0, a1),
+                                             __builtin_elementwise_max(a2, a3));
+  const s16x2 mn = __builtin_elementwise_min(__builtin_elementwise_min(a0, a1),
+                                             __builtin_elementwise_min(a2, a3));
+  const u16x2 b0 = __builtin_bit_cast(u16x2, bx), b1 = __builtin_bit_cast(u16x2, by);
+  const u16x2 b2 = __builtin_bit_cast(u16x2, bz), b3 = __builtin_bit_cast(u16x2, bw);
+  const u16x2 wn = __builtin_elementwise_min(__builtin_elementwise_min(b0, b1),
+                                             __builtin_elementwise_min(b2, b3));
+  const int qa = max(max((int)mx.x, (int)mx.y), -min((int)mn.x, (int)mn.y));
+  const uint32_t qw = min((uint32_t)wn.x, (uint32_t)wn.y);
+  return (uint32_t)qa | ((65535u - qw) << 16);
+}
+
+__device__ __forceinline__ uint32_t max_u16x2(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, a),
+                                                                __builtin_bit_cast(u16x2, b)));
+}
+
+// Halfwise maximum over the wave of two unsigned 16-bit halves, valid in
+// lane 63: DPP row shifts by 1, 2, 4 and 8, then the broadcasts of lanes 15
+// and 31 into the rows above (no LDS traffic; lanes with no source read 0,
+// the identity).
+__device__ __forceinline__ uint32_t wave_max_u16x2(uint32_t v) {
+  v = max_u16x2(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, true));
+  v = max_u16x2(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, true));
+  v = max_u16x2(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, true));
+  v = max_u16x2(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, true));
+  v = max_u16x2(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false));
+  v = max_u16x2(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false));
+  return v;
+}
+
+// summ: the code extremes (code_extremes) of the lane's valid elements, as
+// stored by the fast path; the code summaries widen them by the decision
+// margin.
 template <int GD, bool INJ, bool SMALL, bool SCALED, bool FULL, bool STAGE>
 __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, int64_t e0, int n,
                                             uint32_t k0, uint32_t k1, Group8 &Q, U4 &coarse,
-                                            uint4 *stage) {
+                                            uint4 *stage, uint32_t &summ) {
   load_group<GD, true>(T, e0, n, FULL, Q);
   unscale_group<GD, SCALED>(Q, C.inv);
   float p[kVec];
@@ -1072,15 +1243,21 @@ __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, i
       *stage = make_uint4(b.x, b.y, b.z, b.w);
     else
       *(LUMA_GLOBAL vu4 *)(T.q_w + e0) = b;
+    summ = code_extremes(a, b);
   } else {
+    int qa = 0;
+    uint32_t qw = 65535u;
 #pragma unroll
     for (int j = 0; j < kVec; ++j) {
       if (j < n) {
         T.param[e0 + j] = p[j];
         T.q_m[e0 + j] = (int16_t)(uint16_t)om[j];
         T.q_w[e0 + j] = (int16_t)(uint16_t)ow[j];
+        qa = max(qa, abs((int)(int16_t)(uint16_t)om[j]));
+        qw = min(qw, ow[j] & 0xFFFFu);
       }
     }
+    summ = (uint32_t)qa | ((65535u - qw) << 16);
   }
   return flags;
 }
@@ -1136,6 +1313,15 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   C.hk3 = 0.5f - C.k3;
   C.nk7 = -C.k7;
   C.hk8 = 0.5f - C.k8;
+  // Code summaries: a fast code differs from the exact one by at most
+  // ceil(e), e the decision bound (momentum: |m| k1 + z k2 + k3 with
+  // |m| <= 1.01 S_m(old), z <= 32769; preconditioner: |A| k7 + k8 with
+  // |A| <= 150 |C_hi|), and by at most 1 when e < 1.  A non-finite bound
+  // gives the widest margin (the summary then bounds nothing).
+  const float em = (old ? old->sm * 1.01f : 0.0f) * B.k1 + 32769.0f * B.k2 + C.k3;
+  const float ew = 150.0f * fabsf(C.ch) * B.k7 + C.k8;
+  const uint32_t marg_m = em < 32767.0f ? (uint32_t)fmaxf(1.0f, ceilf(em)) : 32767u;
+  const uint32_t marg_w = ew < 65535.0f ? (uint32_t)fmaxf(1.0f, ceilf(ew)) : 65535u;
   launder(C);
   const bool vec_ok = tensor_vec_ok(T);
   const uint32_t lane = lane_id();
@@ -1276,6 +1462,21 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   // n = 0), so the ballots and the queue lengths stay uniform across the wave.
   constexpr int64_t kStride = (int64_t)kThreads * kVec;
   const int n_it = (int)((end - beg + kStride - 1) / kStride);
+  // The summary of this wave's block of iteration it (LUMA_SUMMARY_BLOCK =
+  // 64 lanes x 8 elements): max |Q_m| + margin, max(min Q_w - margin, 0).
+  static_assert(LUMA_SUMMARY_BLOCK == 64 * kVec, "a summary block is one wave iteration");
+  const bool summ = T.summary != nullptr;
+  const int64_t wave_off = (int64_t)(threadIdx.x >> 6) * LUMA_SUMMARY_BLOCK;
+  auto put_summary = [&](int it, uint32_t x) {
+    const int64_t b0 = beg + (int64_t)it * kStride + wave_off;
+    if (!summ || b0 >= end) return;   // wave-uniform
+    x = wave_max_u16x2(x);
+    if (lane == 63) {
+      const uint32_t a = min((x & 0xFFFFu) + marg_m, 32767u);
+      const uint32_t w = 65535u - (x >> 16);
+      T.summary[b0 / LUMA_SUMMARY_BLOCK] = a | ((w > marg_w ? w - marg_w : 0u) << 16);
+    }
+  };
   // Iterations in which every lane's group is whole stage their
   // preconditioner codes; before a slot is reused, the iteration it holds has
   // its queued entries run and is written back.
@@ -1285,10 +1486,12 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     const int64_t e0 = beg + ((int64_t)it * kThreads + threadIdx.x) * kVec;
     Group8 Q;
     U4 coarse{};
+    uint32_t sx;
     const uint32_t flags = p2_iter<GD, INJ, SMALL, SCALED, true, true>(
-        T, C, e0, kVec, k0, k1, Q, coarse, &stage[(it % kStage) * 64 + lane]);
+        T, C, e0, kVec, k0, k1, Q, coarse, &stage[(it % kStage) * 64 + lane], sx);
     staged_hi = it + 1;
     take(e0, flags, Q, coarse);
+    put_summary(it, sx);
     const int wb = it + 1 - kStage;   // the slot iteration it + 1 will use
     if (wb >= 0) {
       while (qlen_w > 0 && oldest_w() <= wb) batch_w();
@@ -1306,11 +1509,15 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     const int n = rem <= 0 ? 0 : (rem < kVec ? (int)rem : kVec);
     Group8 Q;
     U4 coarse{};
+    uint32_t sx;
     const uint32_t flags =
         (vec_ok && n == kVec)
-            ? p2_iter<GD, INJ, SMALL, SCALED, true, false>(T, C, e0, n, k0, k1, Q, coarse, nullptr)
-            : p2_iter<GD, INJ, SMALL, SCALED, false, false>(T, C, e0, n, k0, k1, Q, coarse, nullptr);
+            ? p2_iter<GD, INJ, SMALL, SCALED, true, false>(T, C, e0, n, k0, k1, Q, coarse, nullptr,
+                                                           sx)
+            : p2_iter<GD, INJ, SMALL, SCALED, false, false>(T, C, e0, n, k0, k1, Q, coarse,
+                                                            nullptr, sx);
     take(e0, flags, Q, coarse);
+    put_summary(it, sx);
   }
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   if (lane < qlen_m) run_m(queue_m[(head_m + lane) & (kQueueCapM - 1)]);
@@ -1384,6 +1591,7 @@ __device__ void write_slot(Slot &s, int64_t t, double s_m, double s_v, double ep
   make_grid(s_m, s_v, eps, s.grid[par]);
   make_fast(s.grid[par], (float)eps);
   s.step = t;
+  s.summ_step = 0;   // codes written by other means: no summaries for them
 }
 
 __global__ void set_scales_kernel(const LumaScaleInit *__restrict__ items, int n) {
@@ -1563,11 +1771,13 @@ void luma_layout(int32_t out[8]) {
 
 // The three launches of one step over `n_chunks` chunks of `n_tensors`
 // tensors, with optional event records between them.
-static int launch_step(const StepSrc &src, int32_t n_tensors, int32_t n_chunks, float *partials,
+static int launch_step(StepSrc src, int32_t n_tensors, int32_t n_chunks, float *partials,
                        uint64_t base_seed, int32_t noise_mode, int32_t flags, hipStream_t s,
                        void *const *events) {
   if (noise_mode != LUMA_NOISE_PHILOX && noise_mode != LUMA_NOISE_INJECTED)
     return fail("luma_step: unknown noise_mode");
+  // only the fast pass 2 writes code summaries
+  src.summaries = (flags & LUMA_FLAG_EXACT_ONLY) == 0;
   auto mark = [&](int i) -> int {
     if (!events || !events[i]) return 0;
     const hipError_t e = hipEventRecord(static_cast<hipEvent_t>(events[i]), s);

@@ -111,6 +111,16 @@ def state_arena(params, device):
     return views
 
 
+def summary_arena(params, device):
+    """One code-summary array per parameter (int32, one entry per
+    SUMMARY_BLOCK elements), as views of one allocation.  The step's pass 2
+    writes them; the next step's pass 1 reads them to skip the codes of blocks
+    that cannot hold the tensor's maximum."""
+    sizes = [-(-p.numel() // L.SUMMARY_BLOCK) for p in params]
+    arena = torch.empty(max(sum(sizes), 1), dtype=torch.int32, device=device)
+    return list(arena.split(sizes)) if params else []
+
+
 class _Engine:
     """Device-side tables of one optimizer: tensor, chunk and group tables and
     the chunk-maxima workspace.  Tables are uploaded only when their contents
@@ -171,7 +181,8 @@ class _Engine:
 
     def table(self, rows) -> np.ndarray:
         """Tensor table of rows: (param, grad, q_m, q_w, u_m, u_w, slot, param_id,
-        grad_code, group, elem_offset) per tensor, chunks numbered consecutively."""
+        grad_code, group, elem_offset, summary) per tensor, chunks numbered
+        consecutively."""
         n = len(rows)
         tt = np.zeros(n, dtype=L.TENSOR_DTYPE)
         numels = np.fromiter((r[0].numel() for r in rows), dtype=np.int64, count=n)
@@ -188,6 +199,7 @@ class _Engine:
         tt["u_m"] = [_ptr(r[4]) for r in rows]
         tt["u_w"] = [_ptr(r[5]) for r in rows]
         tt["slot"] = [r[6].data_ptr() for r in rows]
+        tt["summary"] = [_ptr(r[11]) for r in rows]
         tt["numel"] = numels
         tt["param_id"] = [r[7] for r in rows]
         tt["elem_offset"] = [r[10] for r in rows]
@@ -419,6 +431,7 @@ class LUMA(Optimizer):
         self._noise: Optional[Dict[int, Tuple[torch.Tensor, torch.Tensor]]] = None
         self._noise_strict = True
         self._flags = 0
+        self._summaries = True   # pass per-parameter code summaries to the step
         self._plan: Optional[_Plan] = None
         self._scaling_keep = []
 
@@ -711,6 +724,13 @@ class LUMA(Optimizer):
                                                               engine.device)):
                 state["Q_m"] = qm
                 state["Q_w"] = qw
+        no_summ = [(self.state[w[1]], w[2]) for w in work if "_summary" not in self.state[w[1]]]
+        if no_summ:
+            if capturing:
+                raise engine._capture_error("the set of parameters with optimizer state")
+            for (state, _), sm in zip(no_summ, summary_arena([p for _, p in no_summ],
+                                                             engine.device)):
+                state["_summary"] = sm
         rows, states = [], []
         for gi, p, param, grad, pidx in work:
             self._get_engine(param.device)   # one device for all parameters
@@ -736,8 +756,11 @@ class LUMA(Optimizer):
             if grad.stride() != param.stride() or not _is_dense(grad):
                 grad = torch.empty_like(param, dtype=grad.dtype).copy_(grad)
             u_m, u_w = self._take_noise(p, param)
+            summ = state["_summary"] if self._summaries else None
+            if summ is not None and summ.numel() * L.SUMMARY_BLOCK < param.numel():
+                raise ValueError("LUMA: code summary smaller than its parameter")
             rows.append((param, grad, state["Q_m"], state["Q_w"], u_m, u_w, state["_slot"],
-                         state["param_id"], code, gi, shard_offset(p)))
+                         state["param_id"], code, gi, shard_offset(p), summ))
         tt = engine.table(rows)
         engine.launch(tt, self._group_table(), self._base_seed, noise_mode, self._flags,
                       self._scaling(engine.device))
