@@ -225,7 +225,7 @@ int luma_step_profiled(const LumaStepArgs *args, void *stream, void *const event
 
 /*
  * Largest n_chunks luma_step_noalloc takes: its workspace is a fixed device
- * array of 2 floats per chunk (2 MiB per GPU).
+ * array of 16 bytes per chunk (4 MiB per GPU).
  */
 #define LUMA_NOALLOC_MAX_CHUNKS 262144
 

@@ -51,7 +51,11 @@ struct Slot {
   double s_v[2];
   Hyper hyp;       // scalars of step `step` (written by the step's finalize)
   Grid grid[2];
-  uint8_t pad[LUMA_SLOT_BYTES - 88 - 2 * sizeof(Grid)];
+  // Elements of the tensor that held the largest |m'| and v' at step `step`
+  // (-1: none).  Their exact values at the next step are lower bounds of
+  // that step's maxima, whichever elements they are.
+  int64_t seed_m, seed_v;
+  uint8_t pad[LUMA_SLOT_BYTES - 88 - 2 * sizeof(Grid) - 16];
 };
 static_assert(sizeof(Hyper) == 40, "hyper layout");
 static_assert(offsetof(Slot, grid) == 88, "slot layout");

@@ -206,6 +206,68 @@ __device__ __forceinline__ void block_max2(float &a, float &b) {
   }
 }
 
+// Pass 1's record of one chunk (the step's workspace, kPartialWords words
+// per chunk): the exact max |m'| and max v' of the chunk and the offsets in
+// the chunk of the elements that hold them (kNoArg: not known).
+constexpr int kPartialWords = 4;
+constexpr uint32_t kNoArg = 0xFFFFFFFFu;
+
+__device__ __forceinline__ void put_partial(float *partials, int64_t chunk, float am, float av,
+                                            uint32_t im, uint32_t iv) {
+  float *p = partials + kPartialWords * chunk;
+  p[0] = am;
+  p[1] = av;
+  p[2] = __uint_as_float(im);
+  p[3] = __uint_as_float(iv);
+}
+
+// Whether (a, ia) should replace (b, ib) in a NaN-propagating max: a is
+// NaN and b is not, or a > b.
+__device__ __forceinline__ bool beats(float a, float b) {
+  return (a != a && b == b) || a > b;
+}
+
+// Wave-wide (value, index) max; the result in every lane.
+__device__ __forceinline__ void wave_argmax(float &v, uint32_t &i) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(v, off, 64);
+    const uint32_t oi = (uint32_t)__shfl_xor((int)i, off, 64);
+    if (beats(ov, v) || (__float_as_uint(ov) == __float_as_uint(v) && oi < i)) {
+      v = ov;
+      i = oi;
+    }
+  }
+}
+
+// Block-wide argmax of two (value, index) pairs; result valid in thread 0.
+__device__ __forceinline__ void block_argmax2(float &a, uint32_t &ia, float &b, uint32_t &ib) {
+  __shared__ float sa[kThreads / 64], sb[kThreads / 64];
+  __shared__ uint32_t sia[kThreads / 64], sib[kThreads / 64];
+  wave_argmax(a, ia);
+  wave_argmax(b, ib);
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  if (l == 0) {
+    sa[w] = a;
+    sb[w] = b;
+    sia[w] = ia;
+    sib[w] = ib;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int k = 1; k < kThreads / 64; ++k) {
+      if (beats(sa[k], a)) {
+        a = sa[k];
+        ia = sia[k];
+      }
+      if (beats(sb[k], b)) {
+        b = sb[k];
+        ib = sib[k];
+      }
+    }
+  }
+}
+
 // m', v' of element i of tensor T (exact path).
 __device__ __forceinline__ void element_ema(const Tensor &T, const Hyper &h, const Grid *old,
                                             int64_t i, bool scaled, float inv, float &mn,
@@ -237,21 +299,25 @@ __global__ __launch_bounds__(kThreads) void pass1_exact_kernel(StepSrc src,
   chunk_range(src, T, ci, beg, end);
 
   float am = 0.0f, av = 0.0f;
+  uint32_t im = kNoArg, iv = kNoArg;
   for (int64_t e0 = beg + (int64_t)threadIdx.x * kVec; e0 < end; e0 += (int64_t)kThreads * kVec) {
     for (int j = 0; j < kVec; ++j) {
       const int64_t i = e0 + j;
       if (i >= end) break;
       float mn, vn;
       element_ema(T, h, old, i, scaled, inv, mn, vn);
-      am = nan_max(am, fabsf(mn));
-      av = nan_max(av, vn);
+      if (beats(fabsf(mn), am)) {
+        am = fabsf(mn);
+        im = (uint32_t)(i - beg);
+      }
+      if (beats(vn, av)) {
+        av = vn;
+        iv = (uint32_t)(i - beg);
+      }
     }
   }
-  block_max2(am, av);
-  if (threadIdx.x == 0) {
-    partials[2 * (int64_t)blockIdx.x] = am;
-    partials[2 * (int64_t)blockIdx.x + 1] = av;
-  }
+  block_argmax2(am, im, av, iv);
+  if (threadIdx.x == 0) put_partial(partials, blockIdx.x, am, av, im, iv);
 }
 
 // S' = max(max, floor) with Python's max() semantics (a NaN maximum stays NaN).
@@ -265,14 +331,29 @@ __global__ __launch_bounds__(64) void finalize_kernel(StepSrc src,
   tensor_job(src, T, grp);
   const int nch = (int)(((T.numel - 1) >> src.chunk_shift) + 1);
   float am = 0.0f, av = 0.0f;
+  uint32_t cm = kNoArg, cv = kNoArg;   // chunk (within the tensor) of each maximum
   for (int i = threadIdx.x; i < nch; i += 64) {
-    const int64_t c = (int64_t)T.first_chunk + i;
-    am = nan_max(am, partials[2 * c]);
-    av = nan_max(av, partials[2 * c + 1]);
+    const float *p = partials + kPartialWords * ((int64_t)T.first_chunk + i);
+    if (beats(p[0], am)) {
+      am = p[0];
+      cm = (uint32_t)i;
+    }
+    if (beats(p[1], av)) {
+      av = p[1];
+      cv = (uint32_t)i;
+    }
   }
-  am = wave_max(am);
-  av = wave_max(av);
+  wave_argmax(am, cm);
+  wave_argmax(av, cv);
   if (threadIdx.x == 0) {
+    // the seeds: chunk * C + the offset pass 1 recorded in that chunk
+    auto seed = [&](uint32_t c, int word) -> int64_t {
+      if (c == kNoArg) return -1;
+      const uint32_t off =
+          __float_as_uint(partials[kPartialWords * ((int64_t)T.first_chunk + c) + word]);
+      return off == kNoArg ? -1 : ((int64_t)c << src.chunk_shift) + off;
+    };
+    const int64_t seed_m = seed(cm, 2), seed_v = seed(cv, 3);
     const double s_m = py_max((double)am, 1e-9);  // SCALE_FLOOR_M (config.py:25)
     const double s_v = py_max((double)av, 0.0);
     LUMA_GLOBAL Slot &s = *T.slot;
@@ -288,6 +369,8 @@ __global__ __launch_bounds__(64) void finalize_kernel(StepSrc src,
     s.hyp = h;
     s.step = t;
     s.summ_step = (src.summaries && T.summary) ? t : 0;
+    s.seed_m = seed_m;
+    s.seed_v = seed_v;
   }
 }
 
@@ -763,7 +846,7 @@ __device__ __forceinline__ void unpack_grads(const Raw8 &r, Group8 &G) {
 template <int GD, bool SMALL, bool SCALED, bool SUMM>
 __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOBAL Grid *old,
                                 float inv, int64_t beg, int64_t end, float &exm, float &exv,
-                                uint32_t *queue) {
+                                uint32_t &exi_m, uint32_t &exi_v, uint32_t *queue) {
   const Bounds B = make_bounds((const Grid *)old, nullptr, h.beta1, h.beta2);
   const DecodeK D = decode_consts(old, h.eps);
   P1Const K;
@@ -791,16 +874,33 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   const float sub_m = 2.0f * B.abs_m, sub_v = 2.0f * B.abs_v;
   const uint32_t lane = lane_id();
   uint32_t Mm = 0, Mv = 0, Tm = 0, Tv = 0;  // wave maxima / thresholds (bits)
+  uint32_t T0m = 0, T0v = 0;                 // thresholds from the seeds (below)
+  // Thresholds from exact values: an element whose fast value is below
+  // (x - abs) / (1 + dlt) has an exact value below x (zero for a
+  // non-finite or non-positive x).
+  auto exact_threshold = [](float x, float abs_, float hi) -> uint32_t {
+    const float t = (x - abs_) * hi;
+    return (t > 0.0f && t < INFINITY) ? __float_as_uint(t) : 0u;
+  };
   const bool exact_fast = old == nullptr;
   uint32_t xbm = 0, xbv = 0;                 // exact maxima when exact_fast (bits)
   uint32_t qlen = 0;
-  auto run = [&](uint32_t off) {
-    const int64_t i = beg + off;
+  // exact m', v' of element i (any element of the tensor)
+  auto exact_at = [&](int64_t i) -> float2 {
     float g = load_grad(T.grad, i, GD);
     if (SCALED) g = unscale<GD>(g, inv);
-    const float2 e = exact_mv(T.q_m[i], (int)(uint16_t)T.q_w[i], g, old, h);
-    exm = nan_max(exm, fabsf(e.x));
-    exv = nan_max(exv, e.y);
+    return exact_mv(T.q_m[i], (int)(uint16_t)T.q_w[i], g, old, h);
+  };
+  auto run = [&](uint32_t off) {
+    const float2 e = exact_at(beg + off);
+    if (beats(fabsf(e.x), exm)) {
+      exm = fabsf(e.x);
+      exi_m = off;
+    }
+    if (beats(e.y, exv)) {
+      exv = e.y;
+      exi_v = off;
+    }
   };
   // The fast values of one iteration: fold them into the wave maximum and
   // queue the candidates.
@@ -820,8 +920,8 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     // the elements that still reach the new threshold
     Mm = max(Mm, wave_max_u32(im));
     Mv = max(Mv, wave_max_u32(iv));
-    Tm = threshold_bits(Mm, lo_m, sub_m, hi_m);
-    Tv = threshold_bits(Mv, lo_v, sub_v, hi_v);
+    Tm = max(T0m, threshold_bits(Mm, lo_m, sub_m, hi_m));
+    Tv = max(T0v, threshold_bits(Mv, lo_v, sub_v, hi_v));
     const uint32_t off0 = (uint32_t)(e0 - beg);
 #pragma unroll
     for (int j = 0; j < kVec; ++j) {
@@ -836,6 +936,23 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
       run(queue[qlen + lane]);
     }
   };
+  // Seeds: the elements that held the tensor's maxima at the previous step
+  // (recorded by its finalize).  Their exact m', v' now are lower bounds of
+  // this step's maxima, whichever elements hold those, so they start the
+  // thresholds high: blocks below them are skipped from the first iteration.
+  // Lane 0 evaluates the momentum seed, lane 1 the preconditioner seed.
+  if (old) {
+    const LUMA_GLOBAL Slot &S = *T.slot;
+    const int64_t sm = S.seed_m, sv = S.seed_v;
+    const int64_t si = lane == 0 ? sm : sv;
+    float2 e = make_float2(0.0f, 0.0f);
+    if (lane < 2 && si >= 0 && si < T.numel) e = exact_at(si);
+    const float lbm = __shfl(e.x, 0, 64), lbv = __shfl(e.y, 1, 64);
+    T0m = exact_threshold(fabsf(lbm), B.abs_m, hi_m);
+    T0v = exact_threshold(lbv, B.abs_v, hi_v);
+    Tm = T0m;
+    Tv = T0v;
+  }
   // Every lane runs the same number of iterations (lanes past the end carry
   // n = 0), so the ballots and the queue length stay uniform across the wave.
   constexpr int64_t kStride = (int64_t)kThreads * kVec;
@@ -908,8 +1025,15 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   if (lane < qlen) run(queue[lane]);
   if (exact_fast) {
-    exm = nan_max(exm, __uint_as_float(xbm));
-    exv = nan_max(exv, __uint_as_float(xbv));
+    // t = 1: the maxima of the fast values (exact here), positions not kept
+    if (beats(__uint_as_float(xbm), exm)) {
+      exm = __uint_as_float(xbm);
+      exi_m = kNoArg;
+    }
+    if (beats(__uint_as_float(xbv), exv)) {
+      exv = __uint_as_float(xbv);
+      exi_v = kNoArg;
+    }
   }
 }
 
@@ -918,13 +1042,13 @@ __device__ __forceinline__ void pass1_dispatch_s(const Tensor &T, const Hyper &h
                                                  const LUMA_GLOBAL Grid *old, float inv,
                                                  int64_t beg, int64_t end, bool small,
                                                  bool scaled, float &exm, float &exv,
-                                                 uint32_t *q) {
+                                                 uint32_t &im, uint32_t &iv, uint32_t *q) {
   if (scaled) {
-    if (small) pass1_fast_body<GD, true, true, SUMM>(T, h, old, inv, beg, end, exm, exv, q);
-    else pass1_fast_body<GD, false, true, SUMM>(T, h, old, inv, beg, end, exm, exv, q);
+    if (small) pass1_fast_body<GD, true, true, SUMM>(T, h, old, inv, beg, end, exm, exv, im, iv, q);
+    else pass1_fast_body<GD, false, true, SUMM>(T, h, old, inv, beg, end, exm, exv, im, iv, q);
   } else {
-    if (small) pass1_fast_body<GD, true, false, SUMM>(T, h, old, inv, beg, end, exm, exv, q);
-    else pass1_fast_body<GD, false, false, SUMM>(T, h, old, inv, beg, end, exm, exv, q);
+    if (small) pass1_fast_body<GD, true, false, SUMM>(T, h, old, inv, beg, end, exm, exv, im, iv, q);
+    else pass1_fast_body<GD, false, false, SUMM>(T, h, old, inv, beg, end, exm, exv, im, iv, q);
   }
 }
 
@@ -932,9 +1056,10 @@ template <int GD>
 __device__ __forceinline__ void pass1_dispatch(const Tensor &T, const Hyper &h,
                                                const LUMA_GLOBAL Grid *old, float inv,
                                                int64_t beg, int64_t end, bool small, bool scaled,
-                                               bool summ, float &exm, float &exv, uint32_t *q) {
-  if (summ) pass1_dispatch_s<GD, true>(T, h, old, inv, beg, end, small, scaled, exm, exv, q);
-  else pass1_dispatch_s<GD, false>(T, h, old, inv, beg, end, small, scaled, exm, exv, q);
+                                               bool summ, float &exm, float &exv, uint32_t &im,
+                                               uint32_t &iv, uint32_t *q) {
+  if (summ) pass1_dispatch_s<GD, true>(T, h, old, inv, beg, end, small, scaled, exm, exv, im, iv, q);
+  else pass1_dispatch_s<GD, false>(T, h, old, inv, beg, end, small, scaled, exm, exv, im, iv, q);
 }
 
 // Whether pass 1 may use the tensor's code summaries: the previous step's
@@ -967,17 +1092,18 @@ __global__ __launch_bounds__(kThreads, 4) void pass1_fast_kernel(StepSrc src,
   uint32_t *q = qbuf[threadIdx.x >> 6];
   const bool summ = summaries_valid(T, old, prev);
   float exm = 0.0f, exv = 0.0f;
+  uint32_t exi_m = kNoArg, exi_v = kNoArg;
   if (T.grad_dtype == LUMA_GRAD_BF16)
-    pass1_dispatch<LUMA_GRAD_BF16>(T, h, old, inv, beg, end, small, scaled, summ, exm, exv, q);
+    pass1_dispatch<LUMA_GRAD_BF16>(T, h, old, inv, beg, end, small, scaled, summ, exm, exv, exi_m,
+                                   exi_v, q);
   else if (T.grad_dtype == LUMA_GRAD_F16)
-    pass1_dispatch<LUMA_GRAD_F16>(T, h, old, inv, beg, end, small, scaled, summ, exm, exv, q);
+    pass1_dispatch<LUMA_GRAD_F16>(T, h, old, inv, beg, end, small, scaled, summ, exm, exv, exi_m,
+                                  exi_v, q);
   else
-    pass1_dispatch<LUMA_GRAD_F32>(T, h, old, inv, beg, end, small, scaled, summ, exm, exv, q);
-  block_max2(exm, exv);
-  if (threadIdx.x == 0) {
-    partials[2 * (int64_t)blockIdx.x] = exm;
-    partials[2 * (int64_t)blockIdx.x + 1] = exv;
-  }
+    pass1_dispatch<LUMA_GRAD_F32>(T, h, old, inv, beg, end, small, scaled, summ, exm, exv, exi_m,
+                                  exi_v, q);
+  block_argmax2(exm, exi_m, exv, exi_v);
+  if (threadIdx.x == 0) put_partial(partials, blockIdx.x, exm, exv, exi_m, exi_v);
 }
 
 // Inclusive prefix sum over the 64 lanes of a wave (all lanes active): three
@@ -1592,6 +1718,7 @@ __device__ void write_slot(Slot &s, int64_t t, double s_m, double s_v, double ep
   make_fast(s.grid[par], (float)eps);
   s.step = t;
   s.summ_step = 0;   // codes written by other means: no summaries for them
+  s.seed_m = s.seed_v = -1;
 }
 
 __global__ void set_scales_kernel(const LumaScaleInit *__restrict__ items, int n) {
@@ -1725,11 +1852,12 @@ __global__ void hyper_rows_kernel(LumaGroup g, int64_t t0, int n, float *__restr
 
 using namespace luma;
 
-// Workspace of luma_step_noalloc: pass 1's two maxima per chunk, for at most
-// LUMA_NOALLOC_MAX_CHUNKS chunks (2 MiB).  Each GPU the library runs on holds
+// Workspace of luma_step_noalloc: pass 1's record of each chunk (its two
+// maxima and their positions), for at most LUMA_NOALLOC_MAX_CHUNKS chunks
+// (4 MiB).  Each GPU the library runs on holds
 // its own copy until the process ends.  In host code `scratch` only names the
 // symbol; its device address (one per device) comes from hipGetSymbolAddress.
-static __device__ __align__(256) float scratch[2 * (size_t)LUMA_NOALLOC_MAX_CHUNKS];
+static __device__ __align__(256) float scratch[kPartialWords * (size_t)LUMA_NOALLOC_MAX_CHUNKS];
 
 constexpr int kMaxDevices = 64;
 static std::mutex g_scratch_mu;
@@ -1756,7 +1884,9 @@ int luma_abi_version(void) { return LUMA_ABI_VERSION; }
 
 const char *luma_last_error(void) { return g_err; }
 
-size_t luma_workspace_bytes(int32_t n_chunks) { return (size_t)(n_chunks > 0 ? n_chunks : 0) * 2 * sizeof(float); }
+size_t luma_workspace_bytes(int32_t n_chunks) {
+  return (size_t)(n_chunks > 0 ? n_chunks : 0) * kPartialWords * sizeof(float);
+}
 
 void luma_layout(int32_t out[8]) {
   out[0] = (int32_t)sizeof(LumaTensor);
@@ -1862,7 +1992,7 @@ int luma_step_noalloc(const LumaStepArgs *a, void *stream) {
   float *ws = nullptr;
   if (int r = scratch_for(static_cast<hipStream_t>(stream), &ws)) return r;
   LumaStepArgs b = *a;
-  b.partials = ws;   // every chunk writes its two maxima before finalize reads them
+  b.partials = ws;   // every chunk writes its record before finalize reads it
   return step_impl(&b, stream, nullptr);
 }
 

@@ -110,7 +110,8 @@ def _luma_step_op(param: torch.Tensor, grad: torch.Tensor, Q_m: torch.Tensor,
     tt["grad_dtype"] = _GRAD_CODES[grad.dtype]
     gg = np.array([(lr, beta1, beta2, eps, weight_decay, 0.0)], dtype=L.GROUP_DTYPE)
     nch = (n + L.STEP_TENSOR_CHUNK_MIN - 1) // L.STEP_TENSOR_CHUNK_MIN   # at most this many chunks
-    partials = torch.empty(max(2 * nch, 2), dtype=torch.float32, device=param.device)
+    partials = torch.empty(max(lib.luma_workspace_bytes(nch) // 4, 4), dtype=torch.float32,
+                           device=param.device)
     noise = L.NOISE_PHILOX if u_m is None else L.NOISE_INJECTED
     stream = torch.cuda.current_stream(param.device).cuda_stream
     scaling = L.Scaling(None if grad_scale is None else grad_scale.data_ptr(),

@@ -246,7 +246,7 @@ class _Engine:
                 raise self._capture_error("a param group's hyper-parameters")
             self._d_groups = self._upload(groups)
             self._group_key = gkey
-        need = max(2 * n_chunks, 2)
+        need = max(self.lib.luma_workspace_bytes(n_chunks) // 4, 4)
         if self._partials is None or self._partials.numel() < need:
             if capturing:
                 raise self._capture_error("the chunk count")

@@ -35,7 +35,7 @@ def test_layout_and_version():
     lib = L.load()
     assert lib.luma_abi_version() == L.ABI_VERSION
     L.check_layout(lib)
-    assert lib.luma_workspace_bytes(10) == 80
+    assert lib.luma_workspace_bytes(10) == 160
 
 
 # Random123 known-answer vectors for philox4x32_10 (kat_vectors).
