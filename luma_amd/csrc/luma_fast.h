@@ -136,6 +136,7 @@ struct FastEma {
   float mn;   // m'
   float vn;   // v'
   float am;   // |m| decoded (for the error bound)
+  float v;    // v decoded
 };
 
 // ndw = -dw, nbias = 2^23 dw; sign = 0x80000000 (passed in so that callers
@@ -170,6 +171,7 @@ __device__ __forceinline__ FastEma fast_ema(int qm, int qw, float g, float dm, f
   }
   const float rr = fmaf(iwmin, ex, -eps);  // 1/w - eps
   const float v = rr * rr;
+  r.v = v;
   const float c1g = omb1 * g;
   const float g2 = g * g;
   const float c2g2 = omb2 * g2;

@@ -751,6 +751,39 @@ __device__ __forceinline__ bool p1_reach(int qa, int qw_lo, uint32_t gb, const P
   return __ballot(um >= Tm || uv >= Tv) != 0;
 }
 
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t max_u16x2(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, a),
+                                                                __builtin_bit_cast(u16x2, b)));
+}
+
+// Largest gradient magnitude of the 8 raw gradients in r, unscaled (the
+// magnitude order of float32, bfloat16 and float16 bit patterns is their
+// integer order, NaN above +Inf, and unscaling is monotone, so only the
+// largest is unscaled).  16-bit gradients: packed 16-bit max, two per
+// instruction.
+template <int GD, bool SCALED>
+__device__ __forceinline__ float raw_gmax(const Raw8 &r, float inv) {
+  float g;
+  if (GD == LUMA_GRAD_F32) {
+    const uint32_t m = max(max(max(r.g0.x & 0x7FFFFFFFu, r.g0.y & 0x7FFFFFFFu),
+                               max(r.g0.z & 0x7FFFFFFFu, r.g0.w & 0x7FFFFFFFu)),
+                           max(max(r.g1.x & 0x7FFFFFFFu, r.g1.y & 0x7FFFFFFFu),
+                               max(r.g1.z & 0x7FFFFFFFu, r.g1.w & 0x7FFFFFFFu)));
+    g = __uint_as_float(m);
+  } else {
+    const uint32_t x = r.g0.x & 0x7FFF7FFFu, y = r.g0.y & 0x7FFF7FFFu;
+    const uint32_t z = r.g0.z & 0x7FFF7FFFu, w = r.g0.w & 0x7FFF7FFFu;
+    const uint32_t m2 = max_u16x2(max_u16x2(x, y), max_u16x2(z, w));
+    const uint32_t m = max(m2 & 0xFFFFu, m2 >> 16);
+    g = grad_lo<GD>(m);
+  }
+  if (SCALED) g = unscale<GD>(g, inv);
+  return g;
+}
+
 // Largest gradient magnitude of a group, as float bits (NaN above +Inf).
 __device__ __forceinline__ uint32_t group_gmax(const Group8 &G) {
   uint32_t gb = 0;
@@ -975,16 +1008,28 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     for (; it < n_whole; ++it) {
       const int64_t e0 = beg + ((int64_t)it * kThreads + threadIdx.x) * kVec;
       const int nx = it + 1 < n_whole ? it + 1 : it;
-      Group8 G;
-      unpack_grads<GD>(raw, G);
+      const Raw8 cur = raw;
       const uint32_t s_cur = sw;
       load_grads<GD>(T, beg + ((int64_t)nx * kThreads + threadIdx.x) * kVec, raw);
       sw = summ[(int64_t)nx * kBlocksPerIt];
+      // The bound at the block's code extremes and the lane's largest |g|:
+      // the operations of p1_reach, with the decode done once per block.
+      {
+        const FastEma d = fast_ema<SMALL, false>((int)(s_cur & 0xFFFFu),
+                                                 (int)(kCodeFloat | (s_cur >> 16)), 0.0f, K.dm,
+                                                 K.ndw, K.nbias, K.iwmin, K.eps, K.b1, K.omb1,
+                                                 K.b2, K.omb2, K.sign);
+        const float g = raw_gmax<GD, SCALED>(cur, K.inv);
+        const float mn = fmaf(K.b1, d.am, K.omb1 * g);
+        const float vn = fmaf(K.b2, d.v, K.omb2 * (g * g));
+        const uint32_t um = __float_as_uint(mn * K.up_m) & 0x7FFFFFFFu;
+        const uint32_t uv = __float_as_uint(fmaf(vn, K.up_v, K.abs_v)) & 0x7FFFFFFFu;
+        if (!__ballot(um >= Tm || uv >= Tv))
+          continue;   // no element of the block can be a candidate: codes not read
+      }
+      Group8 G;
+      unpack_grads<GD>(cur, G);
       unscale_group<GD, SCALED>(G, K.inv);
-      // bound at the block's code extremes and the lane's largest |g|
-      if (!p1_reach<SMALL>((int)(s_cur & 0xFFFFu), (int)(kCodeFloat | (s_cur >> 16)),
-                           group_gmax(G), K, Tm, Tv))
-        continue;   // no element of the block can be a candidate: codes not read
       const vu4 a = *(const LUMA_GLOBAL vu4 *)(T.q_m + e0);
       const vu4 b = *(const LUMA_GLOBAL vu4 *)(T.q_w + e0);
       unpack_i16(a.x, G.qm[0], G.qm[1]);
@@ -1221,8 +1266,6 @@ __device__ __forceinline__ void launder(P2Const &C) {
 // code); Q and coarse are kept for the queues.
 // STAGE (FULL only): the preconditioner codes go to *stage (LDS) instead
 // of HBM.
-typedef short s16x2 __attribute__((ext_vector_type(2)));
-typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 // Extremes of 8 stored codes as one word: the largest momentum code
 // magnitude in the low half, 65535 - the smallest preconditioner code in the
@@ -1250,10 +1293,6 @@ __device__ __forceinline__ uint32_t code_extremes(vu4 a, vu4 b) {
   return (uint32_t)qa | ((65535u - qw) << 16);
 }
 
-__device__ __forceinline__ uint32_t max_u16x2(uint32_t a, uint32_t b) {
-  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, a),
-                                                                __builtin_bit_cast(u16x2, b)));
-}
 
 // Halfwise maximum over the wave of two unsigned 16-bit halves, valid in
 // lane 63: DPP row shifts by 1, 2, 4 and 8, then the broadcasts of lanes 15
