@@ -57,7 +57,7 @@
 extern "C" {
 #endif
 
-#define LUMA_ABI_VERSION 6
+#define LUMA_ABI_VERSION 7
 
 /*
  * Elements per chunk-table entry (one workgroup's share of a tensor): the
@@ -77,20 +77,23 @@ extern "C" {
 #define LUMA_SLOT_BYTES 512
 
 /*
- * Code summaries.  A tensor may carry a summary array of one uint32 per block
- * of LUMA_SUMMARY_BLOCK elements (ceil(numel / LUMA_SUMMARY_BLOCK) entries,
- * 4-byte aligned).  Each step's pass 2 writes, for every block, a bound on
- * the codes it stored there: the largest |Q_m| and the smallest Q_w, widened
- * by the step's certified decision margin.  The next step's pass 1 then
- * bounds the block's |m'| and v' from the summary and the gradients alone,
- * and reads the block's codes only when the block could hold the tensor's
- * maximum.  Results do not depend on the summaries; they only save reads.
- * The summaries are used only when the slot records that the previous step
- * wrote them (luma_set_scales and luma_quantize clear that record).  A caller
- * that rewrites a tensor's codes by other means between steps must also
- * rewrite its slot with luma_set_scales, or pass a NULL summary.
+ * Code summaries.  A tensor may carry a summary array that its steps keep:
+ * one uint32 per thread of each chunk's workgroup, LUMA_SUMMARY_WORDS words
+ * per chunk, chunk c of the tensor at words [c * LUMA_SUMMARY_WORDS,
+ * (c + 1) * LUMA_SUMMARY_WORDS).  Each step's pass 2 writes, for every
+ * thread, a bound on the codes it stored in its share of the chunk: the
+ * largest |Q_m| and the smallest Q_w, widened by the step's certified
+ * decision margin.  The next step's pass 1 bounds each thread's |m'| and v'
+ * from that word and the gradients alone, and reads a wave's codes only when
+ * some thread could hold the tensor's maximum.  Results do not depend on the
+ * summaries; they only save reads.  They are used only when the slot records
+ * that the previous step wrote them with the same chunk length (luma_set_scales
+ * and luma_quantize clear that record), and only for chunks whose words fit
+ * in summary_words.  A caller that rewrites a tensor's codes by other means
+ * between steps must also rewrite its slot with luma_set_scales, or pass a
+ * NULL summary.  luma_summary_words gives the words a tensor needs.
  */
-#define LUMA_SUMMARY_BLOCK 512
+#define LUMA_SUMMARY_WORDS 256
 
 /* Gradient element types. */
 #define LUMA_GRAD_F32 0
@@ -118,8 +121,8 @@ typedef struct LumaTensor {
   const float *u_m;     /* device [numel] injected uniforms, or NULL        */
   const float *u_w;     /* device [numel] injected uniforms, or NULL        */
   void *slot;           /* device, LUMA_SLOT_BYTES: this tensor's state     */
-  uint32_t *summary;    /* device [ceil(numel / LUMA_SUMMARY_BLOCK)] code
-                           summaries kept across steps, or NULL           */
+  uint32_t *summary;    /* device code summaries kept across steps, or NULL */
+  int64_t summary_words;/* words at summary (see luma_summary_words)       */
   int64_t numel;        /* elements                                          */
   int64_t param_id;     /* position of the parameter in param_groups order  */
   int64_t elem_offset;  /* index of element 0 in the whole parameter when this
@@ -204,6 +207,9 @@ void luma_layout(int32_t out[8]);
 
 /* Bytes of workspace luma_step / luma_step_tensor / luma_quantize need for n_chunks chunks. */
 size_t luma_workspace_bytes(int32_t n_chunks);
+
+/* Summary words a tensor of numel elements needs for chunks of chunk_elems elements. */
+int64_t luma_summary_words(int64_t numel, int32_t chunk_elems);
 
 /*
  * One optimizer step for every tensor in the table: pass 1 (decode + EMA +

@@ -21,8 +21,8 @@ CHUNK_ELEMS_MIN = 2048       # LUMA_CHUNK_ELEMS_MIN
 STEP_TENSOR_CHUNK_MIN = 16384  # LUMA_STEP_TENSOR_CHUNK_MIN
 SLOT_BYTES = 512             # LUMA_SLOT_BYTES
 NOALLOC_MAX_CHUNKS = 262144  # LUMA_NOALLOC_MAX_CHUNKS
-SUMMARY_BLOCK = 512          # LUMA_SUMMARY_BLOCK
-ABI_VERSION = 6              # LUMA_ABI_VERSION
+SUMMARY_WORDS = 256          # LUMA_SUMMARY_WORDS (per chunk)
+ABI_VERSION = 7              # LUMA_ABI_VERSION
 
 GRAD_F32, GRAD_BF16, GRAD_F16 = 0, 1, 2
 NOISE_PHILOX, NOISE_INJECTED = 0, 1
@@ -30,7 +30,7 @@ FLAG_EXACT_ONLY = 1
 
 TENSOR_DTYPE = np.dtype([
     ("param", "<u8"), ("grad", "<u8"), ("q_m", "<u8"), ("q_w", "<u8"),
-    ("u_m", "<u8"), ("u_w", "<u8"), ("slot", "<u8"), ("summary", "<u8"),
+    ("u_m", "<u8"), ("u_w", "<u8"), ("slot", "<u8"), ("summary", "<u8"), ("summary_words", "<i8"),
     ("numel", "<i8"), ("param_id", "<i8"), ("elem_offset", "<i8"),
     ("grad_dtype", "<i4"), ("group", "<i4"), ("first_chunk", "<i4"), ("reserved", "<i4"),
 ])
@@ -79,6 +79,7 @@ _SIGNATURES = {
     "luma_abi_version": (ctypes.c_int, []),
     "luma_last_error": (ctypes.c_char_p, []),
     "luma_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int32]),
+    "luma_summary_words": (ctypes.c_int64, [ctypes.c_int64, ctypes.c_int32]),
     "luma_layout": (None, [ctypes.POINTER(ctypes.c_int32)]),
     "luma_step": (ctypes.c_int, [ctypes.POINTER(StepArgs), _VP]),
     "luma_step_noalloc": (ctypes.c_int, [ctypes.POINTER(StepArgs), _VP]),

@@ -55,7 +55,9 @@ struct Slot {
   // (-1: none).  Their exact values at the next step are lower bounds of
   // that step's maxima, whichever elements they are.
   int64_t seed_m, seed_v;
-  uint8_t pad[LUMA_SLOT_BYTES - 88 - 2 * sizeof(Grid) - 16];
+  int32_t summ_shift;   // log2 of the chunk length the code summaries were written with
+  int32_t reserved2;
+  uint8_t pad[LUMA_SLOT_BYTES - 88 - 2 * sizeof(Grid) - 24];
 };
 static_assert(sizeof(Hyper) == 40, "hyper layout");
 static_assert(offsetof(Slot, grid) == 88, "slot layout");

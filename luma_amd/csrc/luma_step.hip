@@ -64,6 +64,7 @@ struct Tensor {
   const LUMA_GLOBAL float *u_w;
   LUMA_GLOBAL Slot *slot;
   LUMA_GLOBAL uint32_t *summary;
+  int64_t summary_words;
   int64_t numel;
   int64_t param_id;
   int64_t elem_offset;
@@ -369,6 +370,7 @@ __global__ __launch_bounds__(64) void finalize_kernel(StepSrc src,
     s.hyp = h;
     s.step = t;
     s.summ_step = (src.summaries && T.summary) ? t : 0;
+    s.summ_shift = src.chunk_shift;
     s.seed_m = seed_m;
     s.seed_v = seed_v;
   }
@@ -878,8 +880,8 @@ __device__ __forceinline__ void unpack_grads(const Raw8 &r, Group8 &G) {
 // thresholds: most blocks cost their gradients alone.
 template <int GD, bool SMALL, bool SCALED, bool SUMM>
 __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOBAL Grid *old,
-                                float inv, int64_t beg, int64_t end, float &exm, float &exv,
-                                uint32_t &exi_m, uint32_t &exi_v, uint32_t *queue) {
+                                float inv, int64_t ci, int64_t beg, int64_t end, float &exm,
+                                float &exv, uint32_t &exi_m, uint32_t &exi_v, uint32_t *queue) {
   const Bounds B = make_bounds((const Grid *)old, nullptr, h.beta1, h.beta2);
   const DecodeK D = decode_consts(old, h.eps);
   P1Const K;
@@ -997,35 +999,31 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   const int n_whole = vec_ok ? (int)((end - beg) / kStride) : 0;
   int it = 0;
   if (SUMM && n_whole > 0) {
-    // this wave's summary block in iteration 0; one block per iteration
-    static_assert(LUMA_SUMMARY_BLOCK == 64 * kVec, "a summary block is one wave iteration");
-    const LUMA_GLOBAL uint32_t *summ =
-        T.summary + (beg + (int64_t)(threadIdx.x >> 6) * LUMA_SUMMARY_BLOCK) / LUMA_SUMMARY_BLOCK;
-    constexpr int kBlocksPerIt = (int)(kStride / LUMA_SUMMARY_BLOCK);
+    // This thread's summary word (written by the previous pass 2 for the
+    // same thread of the same chunk) and, once, the decode of its code
+    // bound; each iteration then bounds with the lane's largest |g| alone.
+    static_assert(LUMA_SUMMARY_WORDS == kThreads, "one summary word per thread of a chunk");
+    const uint32_t sw = T.summary[ci * LUMA_SUMMARY_WORDS + threadIdx.x];
+    const FastEma d = fast_ema<SMALL, false>((int)(sw & 0xFFFFu), (int)(kCodeFloat | (sw >> 16)),
+                                             0.0f, K.dm, K.ndw, K.nbias, K.iwmin, K.eps, K.b1,
+                                             K.omb1, K.b2, K.omb2, K.sign);
     Raw8 raw;   // gradients of the lane's next group, loaded one iteration ahead
     load_grads<GD>(T, beg + (int64_t)threadIdx.x * kVec, raw);
-    uint32_t sw = summ[0];
     for (; it < n_whole; ++it) {
       const int64_t e0 = beg + ((int64_t)it * kThreads + threadIdx.x) * kVec;
       const int nx = it + 1 < n_whole ? it + 1 : it;
       const Raw8 cur = raw;
-      const uint32_t s_cur = sw;
       load_grads<GD>(T, beg + ((int64_t)nx * kThreads + threadIdx.x) * kVec, raw);
-      sw = summ[(int64_t)nx * kBlocksPerIt];
-      // The bound at the block's code extremes and the lane's largest |g|:
-      // the operations of p1_reach, with the decode done once per block.
+      // The bound at the thread's code extremes and its largest |g|: the
+      // operations of p1_reach.
       {
-        const FastEma d = fast_ema<SMALL, false>((int)(s_cur & 0xFFFFu),
-                                                 (int)(kCodeFloat | (s_cur >> 16)), 0.0f, K.dm,
-                                                 K.ndw, K.nbias, K.iwmin, K.eps, K.b1, K.omb1,
-                                                 K.b2, K.omb2, K.sign);
         const float g = raw_gmax<GD, SCALED>(cur, K.inv);
         const float mn = fmaf(K.b1, d.am, K.omb1 * g);
         const float vn = fmaf(K.b2, d.v, K.omb2 * (g * g));
         const uint32_t um = __float_as_uint(mn * K.up_m) & 0x7FFFFFFFu;
         const uint32_t uv = __float_as_uint(fmaf(vn, K.up_v, K.abs_v)) & 0x7FFFFFFFu;
         if (!__ballot(um >= Tm || uv >= Tv))
-          continue;   // no element of the block can be a candidate: codes not read
+          continue;   // no element of the wave's groups can be a candidate: codes not read
       }
       Group8 G;
       unpack_grads<GD>(cur, G);
@@ -1085,34 +1083,42 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
 template <int GD, bool SUMM>
 __device__ __forceinline__ void pass1_dispatch_s(const Tensor &T, const Hyper &h,
                                                  const LUMA_GLOBAL Grid *old, float inv,
-                                                 int64_t beg, int64_t end, bool small,
+                                                 int64_t ci, int64_t beg, int64_t end, bool small,
                                                  bool scaled, float &exm, float &exv,
                                                  uint32_t &im, uint32_t &iv, uint32_t *q) {
   if (scaled) {
-    if (small) pass1_fast_body<GD, true, true, SUMM>(T, h, old, inv, beg, end, exm, exv, im, iv, q);
-    else pass1_fast_body<GD, false, true, SUMM>(T, h, old, inv, beg, end, exm, exv, im, iv, q);
+    if (small)
+      pass1_fast_body<GD, true, true, SUMM>(T, h, old, inv, ci, beg, end, exm, exv, im, iv, q);
+    else
+      pass1_fast_body<GD, false, true, SUMM>(T, h, old, inv, ci, beg, end, exm, exv, im, iv, q);
   } else {
-    if (small) pass1_fast_body<GD, true, false, SUMM>(T, h, old, inv, beg, end, exm, exv, im, iv, q);
-    else pass1_fast_body<GD, false, false, SUMM>(T, h, old, inv, beg, end, exm, exv, im, iv, q);
+    if (small)
+      pass1_fast_body<GD, true, false, SUMM>(T, h, old, inv, ci, beg, end, exm, exv, im, iv, q);
+    else
+      pass1_fast_body<GD, false, false, SUMM>(T, h, old, inv, ci, beg, end, exm, exv, im, iv, q);
   }
 }
 
 template <int GD>
 __device__ __forceinline__ void pass1_dispatch(const Tensor &T, const Hyper &h,
-                                               const LUMA_GLOBAL Grid *old, float inv,
+                                               const LUMA_GLOBAL Grid *old, float inv, int64_t ci,
                                                int64_t beg, int64_t end, bool small, bool scaled,
                                                bool summ, float &exm, float &exv, uint32_t &im,
                                                uint32_t &iv, uint32_t *q) {
-  if (summ) pass1_dispatch_s<GD, true>(T, h, old, inv, beg, end, small, scaled, exm, exv, im, iv, q);
-  else pass1_dispatch_s<GD, false>(T, h, old, inv, beg, end, small, scaled, exm, exv, im, iv, q);
+  if (summ)
+    pass1_dispatch_s<GD, true>(T, h, old, inv, ci, beg, end, small, scaled, exm, exv, im, iv, q);
+  else
+    pass1_dispatch_s<GD, false>(T, h, old, inv, ci, beg, end, small, scaled, exm, exv, im, iv, q);
 }
 
-// Whether pass 1 may use the tensor's code summaries: the previous step's
-// pass 2 wrote them (the slot records it), its grid is finite, and the
-// tensor's streams are 16-byte aligned (the whole-group loop).
+// Whether pass 1 may use chunk ci's code summaries: the previous step's
+// pass 2 wrote them with this chunk length (the slot records both), they
+// fit in the array, its grid is finite, and the tensor's streams are 16-byte
+// aligned (the whole-group loop).
 __device__ __forceinline__ bool summaries_valid(const Tensor &T, const LUMA_GLOBAL Grid *old,
-                                                int64_t prev) {
-  return T.summary != nullptr && old != nullptr && T.slot->summ_step == prev &&
+                                                int64_t prev, int64_t ci, int32_t shift) {
+  return T.summary != nullptr && (ci + 1) * LUMA_SUMMARY_WORDS <= T.summary_words &&
+         old != nullptr && T.slot->summ_step == prev && T.slot->summ_shift == shift &&
          __builtin_isfinite(old->dm) && __builtin_isfinite(old->dw) &&
          __builtin_isfinite(old->fast[kIwmin]) && tensor_vec_ok(T);
 }
@@ -1135,18 +1141,18 @@ __global__ __launch_bounds__(kThreads, 4) void pass1_fast_kernel(StepSrc src,
   const float inv = inv_scale(src);
   __shared__ uint32_t qbuf[kThreads / 64][kQueueCap];
   uint32_t *q = qbuf[threadIdx.x >> 6];
-  const bool summ = summaries_valid(T, old, prev);
+  const bool summ = summaries_valid(T, old, prev, ci, src.chunk_shift);
   float exm = 0.0f, exv = 0.0f;
   uint32_t exi_m = kNoArg, exi_v = kNoArg;
   if (T.grad_dtype == LUMA_GRAD_BF16)
-    pass1_dispatch<LUMA_GRAD_BF16>(T, h, old, inv, beg, end, small, scaled, summ, exm, exv, exi_m,
-                                   exi_v, q);
+    pass1_dispatch<LUMA_GRAD_BF16>(T, h, old, inv, ci, beg, end, small, scaled, summ, exm, exv,
+                                   exi_m, exi_v, q);
   else if (T.grad_dtype == LUMA_GRAD_F16)
-    pass1_dispatch<LUMA_GRAD_F16>(T, h, old, inv, beg, end, small, scaled, summ, exm, exv, exi_m,
-                                  exi_v, q);
+    pass1_dispatch<LUMA_GRAD_F16>(T, h, old, inv, ci, beg, end, small, scaled, summ, exm, exv,
+                                  exi_m, exi_v, q);
   else
-    pass1_dispatch<LUMA_GRAD_F32>(T, h, old, inv, beg, end, small, scaled, summ, exm, exv, exi_m,
-                                  exi_v, q);
+    pass1_dispatch<LUMA_GRAD_F32>(T, h, old, inv, ci, beg, end, small, scaled, summ, exm, exv,
+                                  exi_m, exi_v, q);
   block_argmax2(exm, exi_m, exv, exi_v);
   if (threadIdx.x == 0) put_partial(partials, blockIdx.x, exm, exv, exi_m, exi_v);
 }
@@ -1267,54 +1273,46 @@ __device__ __forceinline__ void launder(P2Const &C) {
 // STAGE (FULL only): the preconditioner codes go to *stage (LDS) instead
 // of HBM.
 
-// Extremes of 8 stored codes as one word: the largest momentum code
-// magnitude in the low half, 65535 - the smallest preconditioner code in the
-// high half, so that the halfwise maximum of such words over a wave
-// (wave_max_u16x2) gives both extremes.  From the packed 16-byte store
-// vectors: packed 16-bit integer max/min, two codes per instruction.
+// Running extremes of the codes one thread stores in its share of a chunk:
+// packed 16-bit signed max and min of the momentum codes and unsigned min of
+// the preconditioner codes, two codes per word and per instruction, from the
+// 16-byte store vectors.
+struct CodeAcc {
+  uint32_t mx, mn, wn;
+};
+
+__device__ __forceinline__ uint32_t max_i16x2(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(s16x2, a),
+                                                                __builtin_bit_cast(s16x2, b)));
+}
+
+__device__ __forceinline__ uint32_t min_i16x2(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_min(__builtin_bit_cast(s16x2, a),
+                                                                __builtin_bit_cast(s16x2, b)));
+}
+
+__device__ __forceinline__ uint32_t min_u16x2(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_min(__builtin_bit_cast(u16x2, a),
+                                                                __builtin_bit_cast(u16x2, b)));
+}
+
 // (The words are copied into scalars first: this compiler's
 // __builtin_bit_cast of a vector element such as a.y reads the vector's
 // first word instead.)
-__device__ __forceinline__ uint32_t code_extremes(vu4 a, vu4 b) {
+__device__ __forceinline__ void acc_codes(CodeAcc &acc, vu4 a, vu4 b) {
   const uint32_t ax = a.x, ay = a.y, az = a.z, aw = a.w;
   const uint32_t bx = b.x, by = b.y, bz = b.z, bw = b.w;
-  const s16x2 a0 = __builtin_bit_cast(s16x2, ax), a1 = __builtin_bit_cast(s16x2, ay);
-  const s16x2 a2 = __builtin_bit_cast(s16x2, az), a3 = __builtin_bit_cast(s16x2, aw);
-  const s16x2 mx = __builtin_elementwise_max(__builtin_elementwise_max(a0, a1),
-                                             __builtin_elementwise_max(a2, a3));
-  const s16x2 mn = __builtin_elementwise_min(__builtin_elementwise_min(a0, a1),
-                                             __builtin_elementwise_min(a2, a3));
-  const u16x2 b0 = __builtin_bit_cast(u16x2, bx), b1 = __builtin_bit_cast(u16x2, by);
-  const u16x2 b2 = __builtin_bit_cast(u16x2, bz), b3 = __builtin_bit_cast(u16x2, bw);
-  const u16x2 wn = __builtin_elementwise_min(__builtin_elementwise_min(b0, b1),
-                                             __builtin_elementwise_min(b2, b3));
-  const int qa = max(max((int)mx.x, (int)mx.y), -min((int)mn.x, (int)mn.y));
-  const uint32_t qw = min((uint32_t)wn.x, (uint32_t)wn.y);
-  return (uint32_t)qa | ((65535u - qw) << 16);
+  acc.mx = max_i16x2(acc.mx, max_i16x2(max_i16x2(ax, ay), max_i16x2(az, aw)));
+  acc.mn = min_i16x2(acc.mn, min_i16x2(min_i16x2(ax, ay), min_i16x2(az, aw)));
+  acc.wn = min_u16x2(acc.wn, min_u16x2(min_u16x2(bx, by), min_u16x2(bz, bw)));
 }
 
-
-// Halfwise maximum over the wave of two unsigned 16-bit halves, valid in
-// lane 63: DPP row shifts by 1, 2, 4 and 8, then the broadcasts of lanes 15
-// and 31 into the rows above (no LDS traffic; lanes with no source read 0,
-// the identity).
-__device__ __forceinline__ uint32_t wave_max_u16x2(uint32_t v) {
-  v = max_u16x2(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, true));
-  v = max_u16x2(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, true));
-  v = max_u16x2(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, true));
-  v = max_u16x2(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, true));
-  v = max_u16x2(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false));
-  v = max_u16x2(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false));
-  return v;
-}
-
-// summ: the code extremes (code_extremes) of the lane's valid elements, as
-// stored by the fast path; the code summaries widen them by the decision
-// margin.
+// acc: folds in the codes the fast path stores for the lane's valid
+// elements (the code summaries widen them by the decision margin).
 template <int GD, bool INJ, bool SMALL, bool SCALED, bool FULL, bool STAGE>
 __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, int64_t e0, int n,
                                             uint32_t k0, uint32_t k1, Group8 &Q, U4 &coarse,
-                                            uint4 *stage, uint32_t &summ) {
+                                            uint4 *stage, CodeAcc &acc) {
   load_group<GD, true>(T, e0, n, FULL, Q);
   unscale_group<GD, SCALED>(Q, C.inv);
   float p[kVec];
@@ -1408,7 +1406,7 @@ __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, i
       *stage = make_uint4(b.x, b.y, b.z, b.w);
     else
       *(LUMA_GLOBAL vu4 *)(T.q_w + e0) = b;
-    summ = code_extremes(a, b);
+    acc_codes(acc, a, b);
   } else {
     int qa = 0;
     uint32_t qw = 65535u;
@@ -1422,15 +1420,16 @@ __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, i
         qw = min(qw, ow[j] & 0xFFFFu);
       }
     }
-    summ = (uint32_t)qa | ((65535u - qw) << 16);
+    acc.mx = max_i16x2(acc.mx, (uint32_t)qa * 0x10001u);
+    acc.wn = min_u16x2(acc.wn, qw * 0x10001u);
   }
   return flags;
 }
 
 template <int GD, bool INJ, bool SMALL, bool SCALED>
 __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOBAL Grid *old,
-                                const LUMA_GLOBAL Grid *nw, float inv, int64_t beg, int64_t end,
-                                uint32_t k0, uint32_t k1, uint4 *queue) {
+                                const LUMA_GLOBAL Grid *nw, float inv, int64_t ci, int64_t beg,
+                                int64_t end, uint32_t k0, uint32_t k1, uint4 *queue) {
   const Bounds B = make_bounds((const Grid *)old, (const Grid *)nw, h.beta1, h.beta2);
   P2Const C;
   C.D = decode_consts(old, h.eps);
@@ -1627,21 +1626,7 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   // n = 0), so the ballots and the queue lengths stay uniform across the wave.
   constexpr int64_t kStride = (int64_t)kThreads * kVec;
   const int n_it = (int)((end - beg + kStride - 1) / kStride);
-  // The summary of this wave's block of iteration it (LUMA_SUMMARY_BLOCK =
-  // 64 lanes x 8 elements): max |Q_m| + margin, max(min Q_w - margin, 0).
-  static_assert(LUMA_SUMMARY_BLOCK == 64 * kVec, "a summary block is one wave iteration");
-  const bool summ = T.summary != nullptr;
-  const int64_t wave_off = (int64_t)(threadIdx.x >> 6) * LUMA_SUMMARY_BLOCK;
-  auto put_summary = [&](int it, uint32_t x) {
-    const int64_t b0 = beg + (int64_t)it * kStride + wave_off;
-    if (!summ || b0 >= end) return;   // wave-uniform
-    x = wave_max_u16x2(x);
-    if (lane == 63) {
-      const uint32_t a = min((x & 0xFFFFu) + marg_m, 32767u);
-      const uint32_t w = 65535u - (x >> 16);
-      T.summary[b0 / LUMA_SUMMARY_BLOCK] = a | ((w > marg_w ? w - marg_w : 0u) << 16);
-    }
-  };
+  CodeAcc acc{0u, 0u, 0xFFFFFFFFu};
   // Iterations in which every lane's group is whole stage their
   // preconditioner codes; before a slot is reused, the iteration it holds has
   // its queued entries run and is written back.
@@ -1651,12 +1636,10 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     const int64_t e0 = beg + ((int64_t)it * kThreads + threadIdx.x) * kVec;
     Group8 Q;
     U4 coarse{};
-    uint32_t sx;
     const uint32_t flags = p2_iter<GD, INJ, SMALL, SCALED, true, true>(
-        T, C, e0, kVec, k0, k1, Q, coarse, &stage[(it % kStage) * 64 + lane], sx);
+        T, C, e0, kVec, k0, k1, Q, coarse, &stage[(it % kStage) * 64 + lane], acc);
     staged_hi = it + 1;
     take(e0, flags, Q, coarse);
-    put_summary(it, sx);
     const int wb = it + 1 - kStage;   // the slot iteration it + 1 will use
     if (wb >= 0) {
       while (qlen_w > 0 && oldest_w() <= wb) batch_w();
@@ -1674,15 +1657,22 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     const int n = rem <= 0 ? 0 : (rem < kVec ? (int)rem : kVec);
     Group8 Q;
     U4 coarse{};
-    uint32_t sx;
     const uint32_t flags =
         (vec_ok && n == kVec)
             ? p2_iter<GD, INJ, SMALL, SCALED, true, false>(T, C, e0, n, k0, k1, Q, coarse, nullptr,
-                                                           sx)
+                                                           acc)
             : p2_iter<GD, INJ, SMALL, SCALED, false, false>(T, C, e0, n, k0, k1, Q, coarse,
-                                                            nullptr, sx);
+                                                            nullptr, acc);
     take(e0, flags, Q, coarse);
-    put_summary(it, sx);
+  }
+  // The thread's summary word: its largest |Q_m| + margin, its smallest
+  // Q_w - margin (clamped to the code ranges).
+  if (T.summary != nullptr && (ci + 1) * LUMA_SUMMARY_WORDS <= T.summary_words) {
+    const int mx = max((int)(int16_t)(acc.mx & 0xFFFFu), (int)(int16_t)(acc.mx >> 16));
+    const int mn = min((int)(int16_t)(acc.mn & 0xFFFFu), (int)(int16_t)(acc.mn >> 16));
+    const uint32_t qa = (uint32_t)max(mx, -mn), qw = min(acc.wn & 0xFFFFu, acc.wn >> 16);
+    const uint32_t a = min(qa + marg_m, 32767u), w = qw > marg_w ? qw - marg_w : 0u;
+    T.summary[ci * LUMA_SUMMARY_WORDS + threadIdx.x] = a | (w << 16);
   }
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   if (lane < qlen_m) run_m(queue_m[(head_m + lane) & (kQueueCapM - 1)]);
@@ -1692,15 +1682,19 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
 template <int GD, bool SCALED>
 __device__ __forceinline__ void pass2_dispatch_s(const Tensor &T, const Hyper &h,
                                                  const LUMA_GLOBAL Grid *old,
-                                                 const LUMA_GLOBAL Grid *nw, float inv,
+                                                 const LUMA_GLOBAL Grid *nw, float inv, int64_t ci,
                                                  int64_t beg, int64_t end, uint32_t k0,
                                                  uint32_t k1, bool inj, bool small, uint4 *q) {
   if (inj) {
-    if (small) pass2_fast_body<GD, true, true, SCALED>(T, h, old, nw, inv, beg, end, k0, k1, q);
-    else pass2_fast_body<GD, true, false, SCALED>(T, h, old, nw, inv, beg, end, k0, k1, q);
+    if (small)
+      pass2_fast_body<GD, true, true, SCALED>(T, h, old, nw, inv, ci, beg, end, k0, k1, q);
+    else
+      pass2_fast_body<GD, true, false, SCALED>(T, h, old, nw, inv, ci, beg, end, k0, k1, q);
   } else {
-    if (small) pass2_fast_body<GD, false, true, SCALED>(T, h, old, nw, inv, beg, end, k0, k1, q);
-    else pass2_fast_body<GD, false, false, SCALED>(T, h, old, nw, inv, beg, end, k0, k1, q);
+    if (small)
+      pass2_fast_body<GD, false, true, SCALED>(T, h, old, nw, inv, ci, beg, end, k0, k1, q);
+    else
+      pass2_fast_body<GD, false, false, SCALED>(T, h, old, nw, inv, ci, beg, end, k0, k1, q);
   }
 }
 
@@ -1708,10 +1702,10 @@ template <int GD>
 __device__ __forceinline__ void pass2_dispatch(const Tensor &T, const Hyper &h,
                                                const LUMA_GLOBAL Grid *old,
                                                const LUMA_GLOBAL Grid *nw, float inv, bool scaled,
-                                               int64_t beg, int64_t end, uint32_t k0, uint32_t k1,
-                                               bool inj, bool small, uint4 *q) {
-  if (scaled) pass2_dispatch_s<GD, true>(T, h, old, nw, inv, beg, end, k0, k1, inj, small, q);
-  else pass2_dispatch_s<GD, false>(T, h, old, nw, inv, beg, end, k0, k1, inj, small, q);
+                                               int64_t ci, int64_t beg, int64_t end, uint32_t k0,
+                                               uint32_t k1, bool inj, bool small, uint4 *q) {
+  if (scaled) pass2_dispatch_s<GD, true>(T, h, old, nw, inv, ci, beg, end, k0, k1, inj, small, q);
+  else pass2_dispatch_s<GD, false>(T, h, old, nw, inv, ci, beg, end, k0, k1, inj, small, q);
 }
 
 __global__ __launch_bounds__(kThreads) void pass2_fast_kernel(StepSrc src, uint64_t base_seed,
@@ -1737,11 +1731,11 @@ __global__ __launch_bounds__(kThreads) void pass2_fast_kernel(StepSrc src, uint6
   __shared__ uint4 qbuf[kThreads / 64][kQueueCapM + kQueueCapW + kStage * 64];
   uint4 *q = qbuf[threadIdx.x >> 6];
   if (T.grad_dtype == LUMA_GRAD_BF16)
-    pass2_dispatch<LUMA_GRAD_BF16>(T, h, old, nw, inv, scaled, beg, end, k0, k1, inj, small, q);
+    pass2_dispatch<LUMA_GRAD_BF16>(T, h, old, nw, inv, scaled, ci, beg, end, k0, k1, inj, small, q);
   else if (T.grad_dtype == LUMA_GRAD_F16)
-    pass2_dispatch<LUMA_GRAD_F16>(T, h, old, nw, inv, scaled, beg, end, k0, k1, inj, small, q);
+    pass2_dispatch<LUMA_GRAD_F16>(T, h, old, nw, inv, scaled, ci, beg, end, k0, k1, inj, small, q);
   else
-    pass2_dispatch<LUMA_GRAD_F32>(T, h, old, nw, inv, scaled, beg, end, k0, k1, inj, small, q);
+    pass2_dispatch<LUMA_GRAD_F32>(T, h, old, nw, inv, scaled, ci, beg, end, k0, k1, inj, small, q);
 }
 
 // ---------------------------------------------------------------------------
@@ -1757,6 +1751,7 @@ __device__ void write_slot(Slot &s, int64_t t, double s_m, double s_v, double ep
   make_fast(s.grid[par], (float)eps);
   s.step = t;
   s.summ_step = 0;   // codes written by other means: no summaries for them
+  s.summ_shift = 0;
   s.seed_m = s.seed_v = -1;
 }
 
@@ -1922,6 +1917,12 @@ extern "C" {
 int luma_abi_version(void) { return LUMA_ABI_VERSION; }
 
 const char *luma_last_error(void) { return g_err; }
+
+int64_t luma_summary_words(int64_t numel, int32_t chunk_elems) {
+  if (numel <= 0) return 0;
+  if (chunk_elems <= 0) chunk_elems = LUMA_CHUNK_ELEMS;
+  return ((numel - 1) / chunk_elems + 1) * LUMA_SUMMARY_WORDS;
+}
 
 size_t luma_workspace_bytes(int32_t n_chunks) {
   return (size_t)(n_chunks > 0 ? n_chunks : 0) * kPartialWords * sizeof(float);

@@ -111,12 +111,12 @@ def state_arena(params, device):
     return views
 
 
-def summary_arena(params, device):
-    """One code-summary array per parameter (int32, one entry per
-    SUMMARY_BLOCK elements), as views of one allocation.  The step's pass 2
-    writes them; the next step's pass 1 reads them to skip the codes of blocks
+def summary_arena(params, device, chunk):
+    """One code-summary array per parameter (int32, SUMMARY_WORDS words per
+    chunk of `chunk` elements), as views of one allocation.  The step's pass 2
+    writes them; the next step's pass 1 reads them to skip the codes of groups
     that cannot hold the tensor's maximum."""
-    sizes = [-(-p.numel() // L.SUMMARY_BLOCK) for p in params]
+    sizes = [-(-p.numel() // chunk) * L.SUMMARY_WORDS for p in params]
     arena = torch.empty(max(sum(sizes), 1), dtype=torch.int32, device=device)
     return list(arena.split(sizes)) if params else []
 
@@ -200,6 +200,7 @@ class _Engine:
         tt["u_w"] = [_ptr(r[5]) for r in rows]
         tt["slot"] = [r[6].data_ptr() for r in rows]
         tt["summary"] = [_ptr(r[11]) for r in rows]
+        tt["summary_words"] = [0 if r[11] is None else r[11].numel() for r in rows]
         tt["numel"] = numels
         tt["param_id"] = [r[7] for r in rows]
         tt["elem_offset"] = [r[10] for r in rows]
@@ -724,12 +725,16 @@ class LUMA(Optimizer):
                                                               engine.device)):
                 state["Q_m"] = qm
                 state["Q_w"] = qw
-        no_summ = [(self.state[w[1]], w[2]) for w in work if "_summary" not in self.state[w[1]]]
-        if no_summ:
-            if capturing:
-                raise engine._capture_error("the set of parameters with optimizer state")
+        # code summaries: SUMMARY_WORDS words per chunk at this step's chunk length
+        chunk = engine.chunk_for(np.fromiter((w[2].numel() for w in work), dtype=np.int64,
+                                             count=len(work)))
+        no_summ = [(self.state[w[1]], w[2]) for w in work
+                   if self.state[w[1]].get("_summary") is None
+                   or self.state[w[1]]["_summary"].numel() < -(-w[2].numel() // chunk)
+                   * L.SUMMARY_WORDS]
+        if no_summ and not capturing:   # (under capture, a short array is only used less)
             for (state, _), sm in zip(no_summ, summary_arena([p for _, p in no_summ],
-                                                             engine.device)):
+                                                             engine.device, chunk)):
                 state["_summary"] = sm
         rows, states = [], []
         for gi, p, param, grad, pidx in work:
@@ -756,9 +761,7 @@ class LUMA(Optimizer):
             if grad.stride() != param.stride() or not _is_dense(grad):
                 grad = torch.empty_like(param, dtype=grad.dtype).copy_(grad)
             u_m, u_w = self._take_noise(p, param)
-            summ = state["_summary"] if self._summaries else None
-            if summ is not None and summ.numel() * L.SUMMARY_BLOCK < param.numel():
-                raise ValueError("LUMA: code summary smaller than its parameter")
+            summ = state.get("_summary") if self._summaries else None
             rows.append((param, grad, state["Q_m"], state["Q_w"], u_m, u_w, state["_slot"],
                          state["param_id"], code, gi, shard_offset(p), summ))
         tt = engine.table(rows)

@@ -1,7 +1,7 @@
-"""Code summaries: pass 2 records, per block of LUMA_SUMMARY_BLOCK elements,
-a bound on the codes it stored (max |Q_m| widened upward, min Q_w widened
-downward), and the next pass 1 reads a block's codes only when the bound
-lets the block hold the tensor's maximum.
+"""Code summaries: pass 2 records, per thread of each chunk's workgroup, a
+bound on the codes that thread stored (max |Q_m| widened upward, min Q_w
+widened downward), and the next pass 1 reads a wave's codes only when some
+thread's bound lets its groups hold the tensor's maximum.
 
 * the bound holds for every block of every tensor after every step (the
   final codes, exact-path corrections included);
@@ -68,22 +68,32 @@ def _pair(dtype, kind, steps, between=None):
 
 
 def _check_bounds(opt, params, t):
+    chunk = opt._engine._chunk
     for p in params:
         st = opt.state[p]
-        summ_step = int(st["_slot"][8:16].view(torch.int64).item())
+        slot = st["_slot"]
+        summ_step = int(slot[8:16].view(torch.int64).item())
+        summ_shift = int(slot[328:332].view(torch.int32).item())
         assert summ_step == st["step"], (summ_step, st["step"])
+        assert 1 << summ_shift == chunk, (summ_shift, chunk)
         n = p.numel()
-        nb = -(-n // L.SUMMARY_BLOCK)
-        s = st["_summary"][:nb].to(torch.int64) & 0xFFFFFFFF
-        pad = nb * L.SUMMARY_BLOCK - n
+        # the word of element e: its chunk's words, then its thread in the chunk
+        e = torch.arange(n, device=DEV)
+        word = (e // chunk) * L.SUMMARY_WORDS + (e % chunk) % 2048 // 8
+        nw = -(-n // chunk) * L.SUMMARY_WORDS
+        assert st["_summary"].numel() >= nw
+        s = st["_summary"][:nw].to(torch.int64) & 0xFFFFFFFF
         qm = st["Q_m"].reshape(-1).to(torch.int64).abs()
         qw = st["Q_w"].reshape(-1).to(torch.int64) & 0xFFFF
-        qm = torch.cat([qm, qm.new_zeros(pad)]).view(nb, -1).amax(dim=1)
-        qw = torch.cat([qw, qw.new_full((pad,), 65535)]).view(nb, -1).amin(dim=1)
-        assert bool(((s & 0xFFFF) >= qm).all()), f"step {t}: max |Q_m| above its summary"
-        assert bool(((s >> 16) <= qw).all()), f"step {t}: min Q_w below its summary"
+        mx = torch.zeros(nw, dtype=torch.int64, device=DEV).scatter_reduce(0, word, qm, "amax")
+        mn = torch.full((nw,), 65535, dtype=torch.int64, device=DEV).scatter_reduce(0, word, qw,
+                                                                                   "amin")
+        used = torch.zeros(nw, dtype=torch.bool, device=DEV).index_fill(0, word, True)
+        lo, hi = (s & 0xFFFF)[used], (s >> 16)[used]
+        assert bool((lo >= mx[used]).all()), f"step {t}: max |Q_m| above its summary"
+        assert bool((hi <= mn[used]).all()), f"step {t}: min Q_w below its summary"
         # the margin is small: the summary is within a few codes of the codes
-        assert int(((s & 0xFFFF) - qm).max()) <= 4 and int((qw - (s >> 16)).max()) <= 4
+        assert int((lo - mx[used]).max()) <= 4 and int((mn[used] - hi).max()) <= 4
 
 
 @pytest.mark.parametrize("kind", ["moving_max", "outliers", "shrinking"])
