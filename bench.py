@@ -9,9 +9,14 @@ gradients already resident in HBM.  Prints one JSON line with:
                average launch time (HIP events on the launch stream) vs 8 TB/s
   cpu_baseline the CPU oracle (the reference's PyTorch backend restated) timed
                on this host on a bounded sample of the same workload
-Bytes model per parameter: pass 1 reads grad + Q_m + Q_w (G + 4 bytes), pass 2
-reads grad + Q_m + Q_w + param and writes Q_m + Q_w + param (G + 16), so a
-step moves 2G + 20 bytes (G = gradient element size).
+Bytes per parameter (G = gradient element size):
+  reference algorithm  pass 1 reads grad + Q_m + Q_w (G + 4), pass 2 reads grad +
+                       Q_m + Q_w + param and writes Q_m + Q_w + param (G + 16):
+                       2G + 20 per step (the reference's own traffic model)
+  this implementation  pass 1 reads the gradients and one summary word per 256
+                       threads x chunk, and reads codes only for the groups that
+                       can hold a tensor's maximum (a few per tensor once the
+                       step has run twice): G + 1024 / chunk; pass 2 as above
 """
 
 from __future__ import annotations
@@ -183,6 +188,30 @@ def cpu_baseline(cfg_name, warmup=2, timed=5):
                       f"{os.cpu_count()}); {cpu_model()}"}
 
 
+# ── bytes model ───────────────────────────────────────────────────────────────
+
+def chunk_elems(shapes):
+    """The chunk length the optimizer picks for this set (luma_amd.optimizer
+    _Engine.chunk_for)."""
+    import numpy as np
+    from luma_amd import _lib as L
+    from luma_amd.config import STEP_CHUNK_MIN, STEP_TARGET_CHUNKS
+    numels = np.array([math.prod(s) for s in shapes], dtype=np.int64)
+    c = L.CHUNK_ELEMS
+    while c > STEP_CHUNK_MIN and int(((numels + c - 1) // c).sum()) < STEP_TARGET_CHUNKS:
+        c //= 2
+    return c
+
+
+def pass1_bytes(cfg, n_params, gbytes):
+    """Pass 1's algorithmic bytes per launch in steady state: the gradients
+    and one 4-byte summary word per thread (256) of every chunk."""
+    shapes = cfg["shapes"]()
+    c = chunk_elems(shapes)
+    words = sum(-(-math.prod(s) // c) * 256 for s in shapes)
+    return n_params * gbytes + 4 * words
+
+
 # ── HBM traffic: rocprofv3 FETCH_SIZE / WRITE_SIZE, calibrated on a copy ─────
 
 TRAFFIC_DIR = os.path.join(ROOT, "profiles")
@@ -218,7 +247,8 @@ def traffic_report(config, kernel, fetch_csv, write_csv, copy_fetch_csv, copy_wr
     cfg = CONFIGS[config]
     n_params = sum(math.prod(s) for s in cfg["shapes"]())
     gbytes = torch.tensor([], dtype=cfg["grad"]).element_size()
-    algo = {"luma::pass1": n_params * (gbytes + 4), "luma::pass2": n_params * (gbytes + 16)}[kernel]
+    algo = {"luma::pass1": pass1_bytes(cfg, n_params, gbytes),
+            "luma::pass2": n_params * (gbytes + 16)}[kernel]
     copy_bytes = COPY_ELEMS * 4
     cf = _pmc_per_dispatch(copy_fetch_csv, "void at::native::vectorized_elementwise_kernel", "FETCH_SIZE")
     cw = _pmc_per_dispatch(copy_write_csv, "void at::native::vectorized_elementwise_kernel", "WRITE_SIZE")
@@ -227,16 +257,17 @@ def traffic_report(config, kernel, fetch_csv, write_csv, copy_fetch_csv, copy_wr
     w_scale = copy_bytes / (max(cw) * 1024.0)
     kf = _pmc_per_dispatch(fetch_csv, kernel, "FETCH_SIZE")
     kw = _pmc_per_dispatch(write_csv, kernel, "WRITE_SIZE")
-    # steady-state launches: drop the first (init step, no decode reads)
-    kf_ss, kw_ss = (kf[1:] or kf), (kw[1:] or kw)
+    # steady-state launches: from the third on (t = 1 is the init step, and
+    # t = 2 has no code summaries or seeds yet)
+    kf_ss, kw_ss = (kf[2:] or kf[1:] or kf), (kw[2:] or kw[1:] or kw)
     fetch = sum(kf_ss) / len(kf_ss) * 1024.0 * f_scale
     write = sum(kw_ss) / len(kw_ss) * 1024.0 * w_scale
     lines = [
         f"# HBM traffic of {kernel} on {config} ({n_params} params, {gbytes}-byte grads)",
         "",
         "Commands (each a separate rocprofv3 run):",
-        f"    rocprofv3 --pmc FETCH_SIZE --output-format csv -d <dir> -- python bench.py --config {config} --steps 2 --warmup 1 --no-cpu",
-        f"    rocprofv3 --pmc WRITE_SIZE --output-format csv -d <dir> -- python bench.py --config {config} --steps 2 --warmup 1 --no-cpu",
+        f"    rocprofv3 --pmc FETCH_SIZE --output-format csv -d <dir> -- python bench.py --config {config} --steps 3 --warmup 1 --no-cpu",
+        f"    rocprofv3 --pmc WRITE_SIZE --output-format csv -d <dir> -- python bench.py --config {config} --steps 3 --warmup 1 --no-cpu",
         "    rocprofv3 --pmc FETCH_SIZE --output-format csv -d <dir> -- python bench.py --copy-calibration 3",
         "    rocprofv3 --pmc WRITE_SIZE --output-format csv -d <dir> -- python bench.py --copy-calibration 3",
         f"    python bench.py --traffic-report {config} {kernel} <fetch.csv> <write.csv> <copy_fetch.csv> <copy_write.csv>",
@@ -246,7 +277,7 @@ def traffic_report(config, kernel, fetch_csv, write_csv, copy_fetch_csv, copy_wr
         f"{kernel}: FETCH_SIZE per launch (KiB) {', '.join(f'{v:.0f}' for v in kf)}",
         f"{kernel}: WRITE_SIZE per launch (KiB) {', '.join(f'{v:.0f}' for v in kw)}",
         f"algorithmic bytes per launch: {algo}",
-        f"calibrated fetch bytes per launch: {fetch:.0f} ({fetch / (n_params * (gbytes + 8 if kernel.endswith('2') else gbytes + 4)):.3f} x algorithmic reads)",
+        f"calibrated fetch bytes per launch: {fetch:.0f} ({fetch / (n_params * (gbytes + 8) if kernel.endswith('2') else algo):.3f} x algorithmic reads)",
         f"calibrated write bytes per launch: {write:.0f}",
         f"traffic_bytes_per_launch: {fetch + write:.0f}",
         f"traffic_over_algorithmic: {(fetch + write) / algo:.4f}",
@@ -259,8 +290,9 @@ def traffic_report(config, kernel, fetch_csv, write_csv, copy_fetch_csv, copy_wr
 def stats_report(config, trace_csv, bench_json, out):
     """Write the kernel-time summary of a `rocprofv3 --kernel-trace --stats` run of
     bench.py: per LUMA kernel, the average over every launch and over the
-    steady-state launches (all but the first, the init step), next to the
-    bench's own HIP-event averages from the same run."""
+    steady-state launches (from the third on: t = 1 is the init step, t = 2
+    has no code summaries or seeds yet), next to the bench's own HIP-event
+    averages from the same run."""
     import csv
     durs = {}
     with open(trace_csv) as f:
@@ -290,14 +322,14 @@ def stats_report(config, trace_csv, bench_json, out):
         f"{bench['warmup'] + bench['steps']} launches of each kernel: {bench['warmup']} warm-up + "
         f"{bench['steps']} timed steps; the first is the init step (t = 1).",
         "",
-        "| kernel | launches | avg ms (all) | avg ms (t >= 2) | min ms | max ms | % of GPU time | bench HIP events ms |",
+        "| kernel | launches | avg ms (all) | avg ms (t >= 3) | min ms | max ms | % of GPU time | bench HIP events ms |",
         "|---|---|---|---|---|---|---|---|",
     ]
     ev = {"luma::pass1_fast_kernel": "luma_pass1", "luma::finalize_kernel": "luma_finalize",
           "luma::pass2_fast_kernel": "luma_pass2"}
     for key in sorted(durs, key=lambda k: -sum(durs[k])):
         d = durs[key]
-        ss = d[1:] or d
+        ss = d[2:] or d[1:] or d
         bev = bench["kernel_ms"].get(ev.get(key, ""), None)
         lines.append(f"| `{key}` | {len(d)} | {sum(d) / len(d):.3f} | {sum(ss) / len(ss):.3f} | "
                      f"{min(d):.3f} | {max(d):.3f} | {100 * sum(d) / total:.2f} | "
@@ -317,15 +349,15 @@ ISSUE_COUNTERS = ("SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_WAIT_ANY SQ_WAIT_INST_ANY SQ
 
 def issue_report(config, kernel, pmc_csv, out):
     """Write the instruction-issue summary of a kernel from one rocprofv3 run
-    of bench.py with ISSUE_COUNTERS (steady-state launches: all but the
-    first).  The SQ counters are summed over the shader engines; cycle
-    counts other than SQ_BUSY_CYCLES are in quad-cycles."""
+    of bench.py with ISSUE_COUNTERS (steady-state launches: from the third
+    on).  The SQ counters are summed over the shader engines; cycle counts
+    other than SQ_BUSY_CYCLES are in quad-cycles."""
     cfg = CONFIGS[config]
     n_params = sum(math.prod(s) for s in cfg["shapes"]())
     c = {}
     for name in ISSUE_COUNTERS.split():
         v = _pmc_per_dispatch(pmc_csv, kernel, name)
-        v = v[1:] or v
+        v = v[2:] or v[1:] or v
         c[name] = sum(v) / len(v)
     n_se = 32                      # MI355X: 8 XCDs x 4 shader engines, 8 CUs each
     se_cycles = c["SQ_BUSY_CYCLES"] / n_se
@@ -335,7 +367,7 @@ def issue_report(config, kernel, pmc_csv, out):
         "",
         "Commands (MI355X, one GPU):",
         f"    rocprofv3 --pmc {ISSUE_COUNTERS} --output-format csv -d <dir> -- "
-        f"python bench.py --config {config} --steps 2 --warmup 1 --no-cpu",
+        f"python bench.py --config {config} --steps 3 --warmup 1 --no-cpu",
         f"    python bench.py --issue-report {config} {kernel} <counter_collection.csv> <out.md>",
         "",
         f"kernel time from SQ_BUSY_CYCLES at 2.4 GHz: {se_cycles / 2.4e6:.2f} ms",
@@ -448,11 +480,12 @@ def main():
     ms = wall * 1e3 / args.steps
 
     avg = [sum(v) / len(v) for v in k_times]
-    pass_bytes = [n_params * (gbytes + 4), 0, n_params * (gbytes + 16)]
+    pass_bytes = [pass1_bytes(cfg, n_params, gbytes), 0, n_params * (gbytes + 16)]
     dom = 0 if avg[0] > avg[2] else 2
     achieved = pass_bytes[dom] / (avg[dom] * 1e-3)
-    step_bytes = n_params * (2 * gbytes + 20)
+    step_bytes = pass_bytes[0] + pass_bytes[2]
     step_gbps = step_bytes / (ms * 1e-3)
+    ref_gbps = n_params * (2 * gbytes + 20) / (ms * 1e-3)
     names = ["luma_pass1", "luma_finalize", "luma_pass2"]
     print(f"bench: kernel ms pass1 {avg[0]:.3f} finalize {avg[1]:.3f} pass2 {avg[2]:.3f}; "
           f"step {ms:.3f} ms", file=sys.stderr, flush=True)
@@ -474,9 +507,11 @@ def main():
         "data": "synthetic",
         "config": {"workload": cfg["desc"], "params": n_params, "tensors": len(params),
                    "grad_dtype": str(cfg["grad"]).replace("torch.", ""),
-                   "bytes_per_param": 2 * gbytes + 20},
+                   "bytes_per_param": round(step_bytes / n_params, 3),
+                   "reference_bytes_per_param": 2 * gbytes + 20},
         "step_hbm_gbps": round(step_gbps / 1e9, 1),
         "step_hbm_frac": round(step_gbps / HBM_PEAK, 4),
+        "step_reference_model_gbps": round(ref_gbps / 1e9, 1),
         "kernel_ms": {names[i]: round(avg[i], 4) for i in range(3)},
         "roofline": {"bound": "hbm", "kernel": names[dom],
                      "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9,
