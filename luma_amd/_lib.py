@@ -121,6 +121,18 @@ def load(path: str = LIB_PATH):
     return lib
 
 
+def load_host():
+    """The host bookkeeping module (luma_amd/_luma_host*.so, built with the
+    library): pointer refresh of a re-used step table and the step counts."""
+    try:
+        from . import _luma_host
+    except ImportError as e:
+        raise LumaLibraryError(
+            "luma_amd._luma_host not found or not loadable; build it with "
+            "`python -c 'import luma_amd.build as b; b.build()'`") from e
+    return _luma_host
+
+
 def check_layout(lib) -> None:
     out = (ctypes.c_int32 * 8)()
     lib.luma_layout(out)

@@ -25,7 +25,6 @@ reference's own draws).
 from __future__ import annotations
 
 import ctypes
-import operator
 from typing import Dict, Optional, Tuple
 
 import numpy as np
@@ -34,8 +33,6 @@ from torch.optim import Optimizer
 
 from . import _lib as L
 
-_GRAD = operator.attrgetter("grad")
-_DTYPE = operator.attrgetter("dtype")
 from .config import SCALE_FLOOR_M  # noqa: F401  (re-exported constant)
 from .config import STEP_CHUNK_MIN, STEP_TARGET_CHUNKS
 
@@ -130,8 +127,10 @@ class _Engine:
 
     def __init__(self, device: torch.device):
         self.lib = L.load()
+        self.host = L.load_host()
         self.device = device
         self._tensor_key = None      # bytes of the uploaded tensor table
+        self._tensor_src = None      # (table array, chunk setting) last uploaded or matched
         self._numel_key = None       # bytes of its numel column and chunk length (chunk table)
         self._chunk = L.CHUNK_ELEMS  # chunk length of the uploaded chunk table
         self.chunk_elems = 0         # fixed chunk length (a power of two), 0: chunk_for's choice
@@ -210,36 +209,18 @@ class _Engine:
         return tt
 
     def launch(self, tt: np.ndarray, groups: np.ndarray, base_seed: int, noise_mode: int,
-               flags: int = 0, scaling: Tuple[int, int] = (0, 0)):
+               flags: int = 0, scaling: Tuple[int, int] = (0, 0), same_table: bool = False):
         """One step over the tensors of table tt (luma_step), uploading only the
-        tables whose contents changed since the previous launch."""
+        tables whose contents changed since the previous launch.  With
+        ``same_table`` the caller vouches that tt is the array of the previous
+        launch, unchanged since: the comparison of its contents is skipped."""
         capturing = torch.cuda.is_current_stream_capturing()
         n = len(tt)
-        # first_chunk follows the chunk length of this launch (a cached table
-        # may have been built for another)
-        numels = tt["numel"]
-        c = self.chunk_for(numels)
-        nch = (numels + c - 1) // c
-        first = np.zeros(n, dtype=np.int64)
-        np.cumsum(nch[:-1], out=first[1:])
-        tt["first_chunk"] = first
-        key = tt.tobytes()
-        if key != self._tensor_key:
-            if capturing:
-                raise self._capture_error("the parameter or gradient set")
-            nkey = numels.tobytes() + c.to_bytes(4, "little")
-            if nkey != self._numel_key:
-                n_chunks = int(nch.sum())
-                ch = np.empty(n_chunks, dtype=L.CHUNK_DTYPE)
-                ch["tensor"] = np.repeat(np.arange(n, dtype=np.int32), nch)
-                ch["index"] = (np.arange(n_chunks, dtype=np.int64)
-                               - np.repeat(tt["first_chunk"].astype(np.int64), nch))
-                self._d_chunks = self._upload(ch)
-                self._n_chunks = n_chunks
-                self._chunk = c
-                self._numel_key = nkey
-            self._d_tensors = self._upload(tt)
-            self._tensor_key = key
+        if not (same_table and self._tensor_src is not None and self._tensor_src[0] is tt
+                and self._tensor_src[1] == self.chunk_elems):
+            self._tensor_src = None     # stays unset if the upload fails
+            self._match_table(tt, capturing)
+            self._tensor_src = (tt, self.chunk_elems)
         n_chunks = self._n_chunks
         gkey = groups.tobytes()
         if gkey != self._group_key:
@@ -269,6 +250,35 @@ class _Engine:
             evs = (ctypes.c_void_p * 4)(*[e.cuda_event for e in self.profile_events])
             L.check(self.lib.luma_step_profiled(ctypes.byref(args), self._stream(), evs),
                     "luma_step_profiled")
+
+    def _match_table(self, tt: np.ndarray, capturing: bool):
+        """Upload tt (and its chunk table) unless the device holds it already."""
+        n = len(tt)
+        # first_chunk follows the chunk length of this launch (a cached table
+        # may have been built for another)
+        numels = tt["numel"]
+        c = self.chunk_for(numels)
+        nch = (numels + c - 1) // c
+        first = np.zeros(n, dtype=np.int64)
+        np.cumsum(nch[:-1], out=first[1:])
+        tt["first_chunk"] = first
+        key = tt.tobytes()
+        if key != self._tensor_key:
+            if capturing:
+                raise self._capture_error("the parameter or gradient set")
+            nkey = numels.tobytes() + c.to_bytes(4, "little")
+            if nkey != self._numel_key:
+                n_chunks = int(nch.sum())
+                ch = np.empty(n_chunks, dtype=L.CHUNK_DTYPE)
+                ch["tensor"] = np.repeat(np.arange(n, dtype=np.int32), nch)
+                ch["index"] = (np.arange(n_chunks, dtype=np.int64)
+                               - np.repeat(tt["first_chunk"].astype(np.int64), nch))
+                self._d_chunks = self._upload(ch)
+                self._n_chunks = n_chunks
+                self._chunk = c
+                self._numel_key = nkey
+            self._d_tensors = self._upload(tt)
+            self._tensor_key = key
 
     def set_scales(self, items):
         """items: list of (slot tensor, step, S_m, S_v, eps)."""
@@ -315,27 +325,37 @@ class _Plan:
     A step may re-use it when the parameter list is the same objects, the
     same parameters have a gradient, and every gradient is a plain dense
     tensor of the planned dtype, strides and device.  Then only the gradient
-    and parameter pointers are re-read (about 1 us per tensor, against the
-    full per-parameter bookkeeping), and nothing is uploaded unless they
-    moved.  Invalidated by load_state_dict, import_adamw_state and
-    add_param_group.
+    and parameter pointers are re-read, by the host module (_luma_host.refresh),
+    and nothing is uploaded unless they moved.
+    Invalidated by load_state_dict, import_adamw_state and add_param_group.
     """
 
-    __slots__ = ("all_params", "has_grad", "work_idx", "params", "grads", "gdtypes", "strides",
-                 "numels", "device_index", "states", "tt")
+    __slots__ = ("all_params", "has_grad", "work_idx", "layout_at", "layout", "gdtypes",
+                 "device_index", "states", "tt", "host")
 
-    def __init__(self, param_groups, work, rows, states, tt):
+    _FIELDS = (L.TENSOR_DTYPE.itemsize, L.TENSOR_DTYPE.fields["grad"][1],
+               L.TENSOR_DTYPE.fields["param"][1])
+
+    def __init__(self, param_groups, work, rows, states, tt, host):
         self.all_params = [p for g in param_groups for p in g["params"]]
-        self.has_grad = [p.grad is not None for p in self.all_params]
-        self.work_idx = [w[4] for w in work]
-        self.params = [r[0] for r in rows]
-        self.grads = [r[1] for r in rows]
-        self.gdtypes = [g.dtype for g in self.grads]
-        self.strides = [g.stride() for g in self.grads]   # == the parameter's strides
-        self.numels = [p.numel() for p in self.params]
-        self.device_index = self.params[0].get_device()
+        self.has_grad = np.fromiter((p.grad is not None for p in self.all_params),
+                                    dtype=np.uint8, count=len(self.all_params))
+        self.work_idx = np.fromiter((w[4] for w in work), dtype=np.int64, count=len(work))
+        # per row [ndim, sizes..., strides...] of the parameter (and of its
+        # gradient and Q_m, which the step checked against it)
+        lay, at = [], []
+        for r in rows:
+            at.append(len(lay))
+            lay.append(r[0].dim())
+            lay.extend(r[0].shape)
+            lay.extend(r[0].stride())
+        self.layout_at = np.asarray(at, dtype=np.int64)
+        self.layout = np.asarray(lay, dtype=np.int64)
+        self.gdtypes = np.ascontiguousarray(tt["grad_dtype"], dtype=np.int32)
+        self.device_index = rows[0][0].get_device()
         self.states = states
         self.tt = tt
+        self.host = host
 
     @staticmethod
     def usable(work, rows) -> bool:
@@ -346,40 +366,13 @@ class _Plan:
                    for w in work) and all(
             r[1] is w[1].grad and type(r[1]) is torch.Tensor for w, r in zip(work, rows))
 
-    def refresh(self, param_groups) -> bool:
-        # The common case (the same gradient tensors as last step) is checked
-        # with C-level map/all passes; the per-tensor loop runs only when some
-        # gradient object or dtype changed.
-        flat = [p for g in param_groups for p in g["params"]]
-        if len(flat) != len(self.all_params) or not all(map(operator.is_, flat, self.all_params)):
-            return False
-        grads = list(map(_GRAD, flat))
-        if [g is not None for g in grads] != self.has_grad:
-            return False
-        wg = list(map(grads.__getitem__, self.work_idx))
-        dev = self.device_index
-        if not (all(map(operator.is_, wg, self.grads))
-                and all(map(operator.is_, map(_DTYPE, wg), self.gdtypes))):
-            for i, (g, old) in enumerate(zip(wg, self.grads)):
-                if g is old and g.dtype is self.gdtypes[i]:
-                    continue
-                if (type(g) is not torch.Tensor or g.dtype is not self.gdtypes[i]
-                        or g.stride() != self.strides[i] or g.numel() != self.numels[i]
-                        or g.get_device() != dev):
-                    return False
-        n = len(wg)
-        pptr = np.fromiter(map(torch.Tensor.data_ptr, self.params), dtype=np.uint64, count=n)
-        # a parameter whose storage was replaced (p.data = ...) must still be a
-        # dense float32 tensor of the planned size and layout
-        for i in np.nonzero(pptr != self.tt["param"])[0].tolist():
-            p = self.params[i]
-            if (p.dtype is not torch.float32 or p.numel() != self.numels[i]
-                    or p.stride() != self.strides[i] or p.get_device() != dev):
-                return False
-        self.grads = wg
-        self.tt["grad"] = np.fromiter(map(torch.Tensor.data_ptr, wg), dtype=np.uint64, count=n)
-        self.tt["param"] = pptr
-        return True
+    def refresh(self, param_groups) -> int:
+        """0: the plan no longer applies; 1: it applies and the table is
+        unchanged; 2: it applies with new gradient or parameter pointers
+        (written into the table)."""
+        return self.host.refresh(param_groups, self.all_params, self.has_grad, self.work_idx,
+                                 self.layout_at, self.layout, self.gdtypes, self.tt.ctypes.data,
+                                 *self._FIELDS, self.device_index)
 
 
 class LUMA(Optimizer):
@@ -672,12 +665,14 @@ class LUMA(Optimizer):
                 loss = closure()
 
         plan = self._plan
-        if plan is not None and self._noise is None and plan.refresh(self.param_groups):
-            self._engine.launch(plan.tt, self._group_table(), self._base_seed, L.NOISE_PHILOX,
-                                self._flags, self._scaling(self._engine.device))
-            for state in plan.states:
-                state["step"] += 1
-            return loss
+        if plan is not None and self._noise is None:
+            r = plan.refresh(self.param_groups)
+            if r:
+                self._engine.launch(plan.tt, self._group_table(), self._base_seed,
+                                    L.NOISE_PHILOX, self._flags,
+                                    self._scaling(self._engine.device), same_table=(r == 1))
+                plan.host.bump_steps(plan.states)
+                return loss
         self._plan = None
 
         work = []
@@ -771,6 +766,6 @@ class LUMA(Optimizer):
         for state in states:
             state["step"] += 1
         if noise_mode == L.NOISE_PHILOX and _Plan.usable(work, rows):
-            self._plan = _Plan(self.param_groups, work, rows, states, tt)
+            self._plan = _Plan(self.param_groups, work, rows, states, tt, engine.host)
         self._noise = None
         return loss
