@@ -133,16 +133,36 @@ __device__ __forceinline__ float exact_log_sr(float y, float delta, float z, flo
   return clamp_t(q, 0.0f, kmax);
 }
 
-// LogSR up to its decision: the code is qhi when u < p, else qlo (the same
-// float32 operations as exact_log_sr, for callers that know u only to an
-// interval).
-__device__ __forceinline__ void exact_log_sr_pair(float y, float delta, float z, float kmax,
-                                                  float &p, float &qlo, float &qhi) {
+// LogSR up to its decision: the code is qhi when u < p, else qlo, where
+// p = exact_sr_prob(a, z) (the same float32 operations as exact_log_sr,
+// for callers that know u only to an interval or bracket p first).
+__device__ __forceinline__ void exact_log_sr_pair(float y, float delta, float kmax, float &a,
+                                                  float &qlo, float &qhi) {
   const float k = floorf(y);
   const float fr = y - k;
-  p = cr_expm1(fr * delta) / z;
+  a = fr * delta;
   qlo = clamp_t(k + 0.0f, 0.0f, kmax);
   qhi = clamp_t(k + 1.0f, 0.0f, kmax);
+}
+
+// LogSR's probability p* = expm1(a) / z as exact_log_sr rounds it.
+__device__ __forceinline__ float exact_sr_prob(float a, float z) { return cr_expm1(a) / z; }
+
+// Bounds pl <= p <= ph of p = exact_sr_prob(a, z) without the double
+// expm1, for 0 <= a < 2^-8 and z > 2^-100 (else false).  expm1 by its cubic
+// Taylor polynomial (truncation below a^3/24 < 0.05u relative, u = 2^-24),
+// its three roundings (2.01u), v_rcp_f32 (1 ulp, 2u) and the product (u):
+// |P - p/z| <= 5.01u; the exact path's correctly rounded expm1 and division
+// add u each, so |P - p| <= 7.1u p.  The bracket is 16u P wide on each side,
+// plus 2^-126 for subnormal p.
+__device__ __forceinline__ bool sr_prob_bracket(float a, float z, float &pl, float &ph) {
+  if (!(a >= 0.0f && a < 0x1p-8f && z > 0x1p-100f)) return false;
+  const float t = fmaf(a, fmaf(a, 1.0f / 6.0f, 0.5f), 1.0f);
+  const float P = (a * t) * __builtin_amdgcn_rcpf(z);
+  const float d = fmaf(P, 0x1p-20f, 0x1p-126f);
+  pl = P - d;
+  ph = P + d;
+  return true;
 }
 
 // The momentum code's sign and int16 conversion (functional.py:146-150).
@@ -159,13 +179,14 @@ __device__ __forceinline__ int exact_quant_m(float mn, const Grid &g, float u) {
   return signed_code_m(mc, q);
 }
 
-// exact_quant_m before the draw: codes for u >= p (lo) and u < p (hi).
-__device__ __forceinline__ void exact_quant_m_pair(float mn, const Grid &g, float &p, int &lo,
+// exact_quant_m before the draw: codes for u >= p (lo) and u < p (hi), with
+// p = exact_sr_prob(a, g.zm).
+__device__ __forceinline__ void exact_quant_m_pair(float mn, const Grid &g, float &a, int &lo,
                                                    int &hi) {
   const float mc = clamp_t(mn, -g.sm, g.sm);
   const float y = cr_log1p(fabsf(mc)) / g.dm;
   float qlo, qhi;
-  exact_log_sr_pair(y, g.dm, g.zm, kKM, p, qlo, qhi);
+  exact_log_sr_pair(y, g.dm, kKM, a, qlo, qhi);
   lo = signed_code_m(mc, qlo);
   hi = signed_code_m(mc, qhi);
 }
@@ -181,11 +202,12 @@ __device__ __forceinline__ int exact_quant_w(float vn, const Grid &g, float eps,
   return (int)q;
 }
 
-// exact_quant_w before the draw: codes for u >= p (lo) and u < p (hi).
-__device__ __forceinline__ void exact_quant_w_pair(float vn, const Grid &g, float eps, float &p,
+// exact_quant_w before the draw: codes for u >= p (lo) and u < p (hi), with
+// p = exact_sr_prob(a, g.zw).
+__device__ __forceinline__ void exact_quant_w_pair(float vn, const Grid &g, float eps, float &a,
                                                    int &lo, int &hi) {
   if (!g.dwpos) {
-    p = 0.0f;
+    a = 0.0f;
     lo = hi = 0;
     return;
   }
@@ -194,7 +216,7 @@ __device__ __forceinline__ void exact_quant_w_pair(float vn, const Grid &g, floa
   const float wc = clamp_t(w, g.wmin, g.wmax);
   const float y = cr_log(wc / g.wmin) / g.dw;
   float qlo, qhi;
-  exact_log_sr_pair(y, g.dw, g.zw, kKW, p, qlo, qhi);
+  exact_log_sr_pair(y, g.dw, kKW, a, qlo, qhi);
   lo = (int)qlo;
   hi = (int)qhi;
 }

@@ -585,50 +585,81 @@ __device__ __noinline__ float2 exact_mv(int qm, int qw, float g, const LUMA_GLOB
   return make_float2(mn, vn);
 }
 
-// New code of one element before its draw (exact path): the 16-bit code
-// when the uniform u >= p (lo) and when u < p (hi), and p.  Returned packed
-// in one 64-bit value (lo | hi << 16 | bits(p) << 32) so that the call
-// needs no stack.
+// New code of one element before its draw is final (exact path): the
+// 16-bit code when the uniform u >= p (lo) and when u < p (hi), and the
+// argument a of p = exact_sr_prob(a, z).  The caller knows u to an interval
+// [ulo, uhi] (the injected u itself, or with Philox its top byte's
+// interval); codes that interval decides come back as lo = hi.  p is first
+// bracketed without the double expm1, which then runs only when the bracket
+// overlaps the interval.  Returned packed in one 64-bit value (lo | hi << 16
+// | bits(a) << 32) so that the call needs no stack.
 struct CodePair {
   int lo, hi;
-  float p;
+  float a;
 };
 
-__device__ __forceinline__ uint64_t pack_pair(int lo, int hi, float p) {
-  return (uint64_t)(((uint32_t)lo & 0xFFFFu) | ((uint32_t)hi << 16)) |
-         ((uint64_t)__float_as_uint(p) << 32);
+__device__ __forceinline__ uint64_t pack_pair(int lo, int hi, float a) {
+  return (uint64_t)(((uint32_t)lo & 0xFFFFu) | (((uint32_t)hi & 0xFFFFu) << 16)) |
+         ((uint64_t)__float_as_uint(a) << 32);
 }
 
 __device__ __forceinline__ CodePair unpack_pair(uint64_t v) {
   CodePair c;
   c.lo = (int)(v & 0xFFFFu);
   c.hi = (int)((v >> 16) & 0xFFFFu);
-  c.p = __uint_as_float((uint32_t)(v >> 32));
+  c.a = __uint_as_float((uint32_t)(v >> 32));
   return c;
+}
+
+__device__ __forceinline__ uint64_t sr_resolve(int lo, int hi, float a, float z, float ulo,
+                                               float uhi) {
+  if (lo == hi) return pack_pair(lo, lo, 0.0f);
+  float pl, ph;
+  if (!sr_prob_bracket(a, z, pl, ph)) pl = ph = exact_sr_prob(a, z);
+  if (uhi < pl) return pack_pair(hi, hi, 0.0f);     // u <= uhi < pl <= p
+  if (!(ulo < ph)) return pack_pair(lo, lo, 0.0f);  // u >= ulo >= ph >= p (NaN p: lo)
+  if (ulo == uhi) {                                  // u known: p itself decides
+    const float p = pl == ph ? pl : exact_sr_prob(a, z);
+    return ulo < p ? pack_pair(hi, hi, 0.0f) : pack_pair(lo, lo, 0.0f);
+  }
+  return pack_pair(lo, hi, a);   // the caller draws u's low bits (sr_below)
+}
+
+// u < exact_sr_prob(a, z) for a u known exactly; the double expm1 runs only
+// when u falls inside sr_prob_bracket's bracket.  A call, so that the
+// streaming loops keep their registers.
+__device__ __noinline__ bool sr_below(float a, float z, float u) {
+  float pl, ph;
+  if (!sr_prob_bracket(a, z, pl, ph)) return u < exact_sr_prob(a, z);
+  if (u < pl) return true;
+  if (!(u < ph)) return false;
+  return u < exact_sr_prob(a, z);
 }
 
 // Momentum: the same float32 sequence as exact_mv's m' then exact_quant_m.
 __device__ __noinline__ uint64_t exact_pair_m(int qm, float g, const LUMA_GLOBAL Grid *old,
-                                              const LUMA_GLOBAL Grid *nw, Hyper h) {
+                                              const LUMA_GLOBAL Grid *nw, Hyper h, float ulo,
+                                              float uhi) {
   const float m = old ? exact_decode_m(qm, old->dm) : 0.0f;
   const float mn = h.beta1 * m + h.omb1 * g;
   const Grid G = *nw;
-  float p;
+  float a;
   int lo, hi;
-  exact_quant_m_pair(mn, G, p, lo, hi);
-  return pack_pair(lo, hi, p);
+  exact_quant_m_pair(mn, G, a, lo, hi);
+  return sr_resolve(lo, hi, a, G.zm, ulo, uhi);
 }
 
 // Preconditioner: exact_mv's v' then exact_quant_w.
 __device__ __noinline__ uint64_t exact_pair_w(int qw, float g, const LUMA_GLOBAL Grid *old,
-                                              const LUMA_GLOBAL Grid *nw, Hyper h) {
+                                              const LUMA_GLOBAL Grid *nw, Hyper h, float ulo,
+                                              float uhi) {
   const float v = old ? exact_decode_v(qw, old->wmin, old->dw, h.eps) : 0.0f;
   const float vn = h.beta2 * v + h.omb2 * (g * g);
   const Grid G = *nw;
-  float p;
+  float a;
   int lo, hi;
-  exact_quant_w_pair(vn, G, h.eps, p, lo, hi);
-  return pack_pair(lo, hi, p);
+  exact_quant_w_pair(vn, G, h.eps, a, lo, hi);
+  return sr_resolve(lo, hi, a, G.zw, ulo, uhi);
 }
 
 // Per-wave queues of elements whose fast result is not certified.  Elements
@@ -1499,18 +1530,22 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   // (no second read of HBM), w = the old code's 16 bits.  The fast codes were
   // already stored (or staged); the exact ones overwrite them (same
   // wavefront, so the stores stay in program order).
-  // The code is c.hi when u < c.p.  With Philox the top 8 bits of u are
-  // known: u lies in [top/256, (top + 1)/256 - 2^-24], which decides unless
-  // c.p falls inside (then the fine block gives the low 16 bits).
-  auto below = [&](float p, int64_t i, uint32_t top, int which) -> bool {  // u < p
-    const float lo = (float)(top << 16) * 0x1p-24f;
-    const float hi = (float)((top << 16) | 0xFFFFu) * 0x1p-24f;
-    bool b = p > hi;                  // u <= hi < p
-    if (p > lo && !b) {               // else u >= lo >= p (a NaN p also: false)
-      const U4 fine = philox_fine_block((uint64_t)i, pb, k0, k1);
-      b = (float)((top << 16) | u4_half(fine, 2 * (int)(i & 3) + which)) * 0x1p-24f < p;
-    }
-    return b;
+  // The code of a queued element from its pair: lo = hi when the uniform's
+  // interval decided it; else (Philox) the fine block gives u's low 16 bits.
+  const float zm_new = nw->zm, zw_new = nw->zw;
+  auto draw = [&](const CodePair &c, float z, int64_t i, uint32_t top, int which) -> int {
+    if (c.lo == c.hi) return c.lo;
+    const U4 fine = philox_fine_block((uint64_t)i, pb, k0, k1);
+    const float u = (float)((top << 16) | u4_half(fine, 2 * (int)(i & 3) + which)) * 0x1p-24f;
+    return sr_below(c.a, z, u) ? c.hi : c.lo;
+  };
+  // The interval of an entry's uniform: the injected u itself, or (Philox)
+  // the interval of its top byte.
+  auto u_lo = [&](uint32_t top, const LUMA_GLOBAL float *u, int64_t i) -> float {
+    return INJ ? u[i] : (float)(top << 16) * 0x1p-24f;
+  };
+  auto u_hi = [&](uint32_t top, const LUMA_GLOBAL float *u, int64_t i) -> float {
+    return INJ ? u[i] : (float)((top << 16) | 0xFFFFu) * 0x1p-24f;
   };
   // Staging: whole-group iterations [staged_lo, staged_hi) keep their
   // preconditioner codes in stage[(it % kStage) * 64 + lane] until written
@@ -1520,18 +1555,17 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   int staged_lo = 0, staged_hi = 0;
   auto run_m = [&](uint4 ent) {
     const int64_t i = beg + ent.x;
-    const CodePair c =
-        unpack_pair(exact_pair_m((int)(int16_t)ent.w, __uint_as_float(ent.z), old, nw, h));
-    const bool b = INJ ? T.u_m[i] < c.p : below(c.p, i, ent.y, 0);
-    T.q_m[i] = (int16_t)(b ? c.hi : c.lo);
+    const CodePair c = unpack_pair(exact_pair_m((int)(int16_t)ent.w, __uint_as_float(ent.z), old,
+                                                nw, h, u_lo(ent.y, T.u_m, i),
+                                                u_hi(ent.y, T.u_m, i)));
+    T.q_m[i] = (int16_t)draw(c, zm_new, i, ent.y, 0);
   };
   auto run_w = [&](uint4 ent) {
     const uint32_t o = ent.x;
     const int64_t i = beg + o;
-    const CodePair c =
-        unpack_pair(exact_pair_w((int)ent.w, __uint_as_float(ent.z), old, nw, h));
-    const bool b = INJ ? T.u_w[i] < c.p : below(c.p, i, ent.y, 1);
-    const uint16_t code = (uint16_t)(b ? c.hi : c.lo);
+    const CodePair c = unpack_pair(exact_pair_w((int)ent.w, __uint_as_float(ent.z), old, nw, h,
+                                                u_lo(ent.y, T.u_w, i), u_hi(ent.y, T.u_w, i)));
+    const uint16_t code = (uint16_t)draw(c, zw_new, i, ent.y, 1);
     const int it_e = (int)(o >> 11);
     if (it_e >= staged_lo && it_e < staged_hi) {
       uint16_t *slot = (uint16_t *)&stage[(it_e % kStage) * 64 + ((o >> 3) & 63u)];
