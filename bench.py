@@ -27,6 +27,7 @@ import math
 import os
 import sys
 import time
+import types
 
 import torch
 
@@ -194,13 +195,9 @@ def chunk_elems(shapes):
     """The chunk length the optimizer picks for this set (luma_amd.optimizer
     _Engine.chunk_for)."""
     import numpy as np
-    from luma_amd import _lib as L
-    from luma_amd.config import STEP_CHUNK_MIN, STEP_TARGET_CHUNKS
+    from luma_amd.optimizer import _Engine
     numels = np.array([math.prod(s) for s in shapes], dtype=np.int64)
-    c = L.CHUNK_ELEMS
-    while c > STEP_CHUNK_MIN and int(((numels + c - 1) // c).sum()) < STEP_TARGET_CHUNKS:
-        c //= 2
-    return c
+    return _Engine.chunk_for(types.SimpleNamespace(chunk_elems=0), numels)
 
 
 def pass1_bytes(cfg, n_params, gbytes):

@@ -1019,8 +1019,9 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     Tm = T0m;
     Tv = T0v;
   }
-  // Every lane runs the same number of iterations (lanes past the end carry
-  // n = 0), so the ballots and the queue length stay uniform across the wave.
+  // Every lane of a wave runs the same iterations (lanes past the end carry
+  // n = 0), so the ballots and the queue length stay uniform across the wave;
+  // a wave stops once all its groups lie past the end.
   constexpr int64_t kStride = (int64_t)kThreads * kVec;
   const int n_it = (int)((end - beg + kStride - 1) / kStride);
   // Iterations in which every lane's group is whole run in a loop of their
@@ -1088,6 +1089,8 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     }
   }
   for (; it < n_it; ++it) {
+    // a wave whose groups all lie past the end is done (small tensors)
+    if (beg + ((int64_t)it * kThreads + (threadIdx.x & ~63u)) * kVec >= end) break;
     const int64_t e0 = beg + ((int64_t)it * kThreads + threadIdx.x) * kVec;
     const int64_t rem = end - e0;
     const int n = rem <= 0 ? 0 : (rem < kVec ? (int)rem : kVec);
@@ -1656,8 +1659,9 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     w.x = v.x; w.y = v.y; w.z = v.z; w.w = v.w;
     store_stream(w, (LUMA_GLOBAL vu4 *)(T.q_w + e));
   };
-  // Every lane runs the same number of iterations (lanes past the end carry
-  // n = 0), so the ballots and the queue lengths stay uniform across the wave.
+  // Every lane of a wave runs the same iterations (lanes past the end carry
+  // n = 0), so the ballots and the queue lengths stay uniform across the wave;
+  // a wave stops once all its groups lie past the end.
   constexpr int64_t kStride = (int64_t)kThreads * kVec;
   const int n_it = (int)((end - beg + kStride - 1) / kStride);
   CodeAcc acc{0u, 0u, 0xFFFFFFFFu};
@@ -1686,6 +1690,8 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   for (int j = staged_lo; j < staged_hi; ++j) write_back(j);
   staged_lo = staged_hi = 0;
   for (; it < n_it; ++it) {
+    // a wave whose groups all lie past the end is done (small tensors)
+    if (beg + ((int64_t)it * kThreads + (threadIdx.x & ~63u)) * kVec >= end) break;
     const int64_t e0 = beg + ((int64_t)it * kThreads + threadIdx.x) * kVec;
     const int64_t rem = end - e0;
     const int n = rem <= 0 ? 0 : (rem < kVec ? (int)rem : kVec);

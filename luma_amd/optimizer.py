@@ -167,14 +167,17 @@ class _Engine:
     # -- entry points -------------------------------------------------------
     def chunk_for(self, numels: np.ndarray) -> int:
         """Chunk length of a step over tensors of these sizes: the largest power
-        of two from CHUNK_ELEMS down to STEP_CHUNK_MIN that still gives
-        STEP_TARGET_CHUNKS workgroups (small sets get more, shorter chunks).
-        The result does not depend on it: every element is computed alone and
-        the per-tensor maxima are exact."""
+        of two from CHUNK_ELEMS down to STEP_CHUNK_MIN with STEP_TARGET_CHUNKS
+        chunks of it at most the set's total size.  Small sets get shorter
+        chunks; so do sets of many tensors whose total is small, where one
+        chunk per tensor would leave the largest tensors' workgroups running
+        alone at the end of the launch.  The result does not depend on it:
+        every element is computed alone and the per-tensor maxima are exact."""
         if self.chunk_elems:
             return self.chunk_elems
+        total = int(numels.sum())
         c = L.CHUNK_ELEMS
-        while c > STEP_CHUNK_MIN and int(((numels + c - 1) // c).sum()) < STEP_TARGET_CHUNKS:
+        while c > STEP_CHUNK_MIN and c * STEP_TARGET_CHUNKS > total:
             c //= 2
         return c
 

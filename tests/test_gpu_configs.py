@@ -99,9 +99,11 @@ def test_cfg3_many_small():
         gen = _gen(3000 + t)
         gd = [normal_grad(p.shape, 1e-4, gen, DEV, torch.float32, zeros=0.01) for p in params]
         pair.step(gd, {i: g.cpu() for i, g in enumerate(gd)})
-        # 20,000 tensors already make 20,000 chunks, so the automatic choice
-        # keeps the longest chunk: one chunk per tensor
-        assert pair.opt._engine._chunk == 131072 and pair.opt._engine._n_chunks == 20000
+        # 4096 chunks of 16384 exceed the set's total: the automatic choice
+        # is the shortest chunk, so the largest tensors take up to 4 chunks
+        n_chunks = sum(-(-p.numel() // 16384) for p in params)
+        assert pair.opt._engine._chunk == 16384 and pair.opt._engine._n_chunks == n_chunks
+        assert n_chunks > len(params)
         rows = pair.check()
         assert sum(r["n"] for r in rows) == total
 

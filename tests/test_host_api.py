@@ -138,20 +138,22 @@ def test_sparse_grad_rejected():
 
 
 def test_step_chunk_policy():
-    """The step's chunk length: 131072 while that gives 4096 workgroups, else
-    halved down to 16384; a fixed length overrides it."""
+    """The step's chunk length: 131072 while 4096 chunks of it fit in the
+    set's total size, else halved down to 16384; a fixed length overrides it."""
     import types
     import numpy as np
     from luma_amd.optimizer import _Engine
     pick = _Engine.chunk_for
     auto = types.SimpleNamespace(chunk_elems=0)
     assert pick(auto, np.array([4096 * 4096], dtype=np.int64)) == 16384
-    assert pick(auto, np.array([65536] * 4096, dtype=np.int64)) == 131072
+    assert pick(auto, np.array([65536] * 4096, dtype=np.int64)) == 65536
+    assert pick(auto, np.array([65536] * 8192, dtype=np.int64)) == 131072
     assert pick(auto, np.array([131072] * 2048, dtype=np.int64)) == 65536
     assert pick(auto, np.array([65536] * 4095, dtype=np.int64)) == 32768
     assert pick(auto, np.array([65536] * 2048, dtype=np.int64)) == 32768
     assert pick(auto, np.array([65536] * 2047, dtype=np.int64)) == 16384
-    assert pick(auto, np.array([1] * 20000, dtype=np.int64)) == 131072
+    assert pick(auto, np.array([1] * 20000, dtype=np.int64)) == 16384
+    assert pick(auto, np.array([65536] * 1000 + [1] * 20000, dtype=np.int64)) == 16384
     assert pick(types.SimpleNamespace(chunk_elems=2048), np.array([10], dtype=np.int64)) == 2048
 
 
