@@ -57,7 +57,7 @@
 extern "C" {
 #endif
 
-#define LUMA_ABI_VERSION 7
+#define LUMA_ABI_VERSION 8
 
 /*
  * Elements per chunk-table entry (one workgroup's share of a tensor): the
@@ -68,6 +68,13 @@ extern "C" {
 #define LUMA_CHUNK_ELEMS 131072
 #define LUMA_CHUNK_ELEMS_MIN 2048
 #define LUMA_STEP_TENSOR_CHUNK_MIN 16384   /* shortest chunk luma_step_tensor uses */
+
+/*
+ * Tensors of at most this many elements are best stepped one wavefront each
+ * (LumaStepArgs.small_chunks): a workgroup of their own would spend most of
+ * its time in set-up.
+ */
+#define LUMA_SMALL_TENSOR 512
 
 /*
  * Bytes of one slot: a tensor's persistent device state (step count, S_m,
@@ -183,7 +190,11 @@ typedef struct LumaStepArgs {
   int32_t flags;             /* LUMA_FLAG_* */
   int32_t chunk_elems;       /* chunk length C of the chunk table: a power of two in
                                 [LUMA_CHUNK_ELEMS_MIN, LUMA_CHUNK_ELEMS]; 0 = LUMA_CHUNK_ELEMS */
-  int32_t reserved;          /* 0 */
+  int32_t small_chunks;      /* the last small_chunks records of the chunk table, one
+                                chunk per tensor, are stepped one wavefront each (four
+                                per workgroup) by the exact path; meant for tensors of at
+                                most LUMA_SMALL_TENSOR elements (any tensor is stepped
+                                correctly).  0: every chunk takes a workgroup */
   LumaScaling scaling;       /* both NULL: unscaled gradients, always step */
 } LumaStepArgs;
 
@@ -216,7 +227,7 @@ int64_t luma_summary_words(int64_t numel, int32_t chunk_elems);
  * per-chunk maxima), per-tensor finalize (new S_m/S_v and grid in float64,
  * step count + 1, step scalars), pass 2 (re-decode + EMA + AdamW update +
  * LogSR re-quantisation).  A tensor whose slot holds step count 0 takes the
- * init step.  Three kernel launches on `stream` (a hipStream_t), no host
+ * init step.  Three to five kernel launches on `stream` (a hipStream_t), no host
  * synchronisation; no device table is written, so the sequence may be
  * captured into a HIP graph and replayed.
  */

@@ -18,11 +18,12 @@ LIB_PATH = os.path.join(HERE, LIB_NAME)
 
 CHUNK_ELEMS = 131072         # LUMA_CHUNK_ELEMS (default and largest chunk length)
 CHUNK_ELEMS_MIN = 2048       # LUMA_CHUNK_ELEMS_MIN
+SMALL_TENSOR = 512           # LUMA_SMALL_TENSOR
 STEP_TENSOR_CHUNK_MIN = 16384  # LUMA_STEP_TENSOR_CHUNK_MIN
 SLOT_BYTES = 512             # LUMA_SLOT_BYTES
 NOALLOC_MAX_CHUNKS = 262144  # LUMA_NOALLOC_MAX_CHUNKS
 SUMMARY_WORDS = 256          # LUMA_SUMMARY_WORDS (per chunk)
-ABI_VERSION = 7              # LUMA_ABI_VERSION
+ABI_VERSION = 8              # LUMA_ABI_VERSION
 
 GRAD_F32, GRAD_BF16, GRAD_F16 = 0, 1, 2
 NOISE_PHILOX, NOISE_INJECTED = 0, 1
@@ -63,7 +64,7 @@ class StepArgs(ctypes.Structure):
         ("noise_mode", ctypes.c_int32),
         ("flags", ctypes.c_int32),
         ("chunk_elems", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("small_chunks", ctypes.c_int32),
         ("scaling", Scaling),
     ]
 

@@ -87,6 +87,8 @@ struct StepSrc {
   LumaScaling scaling;
   int32_t chunk_shift;   // log2 of the launch's chunk length
   int32_t summaries;     // this launch's pass 2 writes the code summaries
+  int32_t small_from;    // chunks from here on: small tensors, one wavefront each
+  int32_t n_chunks;
 };
 
 // Elements [beg, end) of chunk ci of tensor T.
@@ -213,6 +215,10 @@ __device__ __forceinline__ void block_max2(float &a, float &b) {
 constexpr int kPartialWords = 4;
 constexpr uint32_t kNoArg = 0xFFFFFFFFu;
 
+__device__ __forceinline__ uint32_t lane_id() {
+  return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+}
+
 __device__ __forceinline__ void put_partial(float *partials, int64_t chunk, float am, float av,
                                             uint32_t im, uint32_t iv) {
   float *p = partials + kPartialWords * chunk;
@@ -321,6 +327,68 @@ __global__ __launch_bounds__(kThreads) void pass1_exact_kernel(StepSrc src,
   if (threadIdx.x == 0) put_partial(partials, blockIdx.x, am, av, im, iv);
 }
 
+// ---------------------------------------------------------------------------
+//  Small tensors: one wavefront per chunk
+// ---------------------------------------------------------------------------
+// The chunk records from src.small_from on belong to tensors of at most
+// LUMA_SMALL_TENSOR elements, one chunk each.  Each is stepped by one
+// wavefront (four per workgroup) through the exact path: a workgroup of its
+// own would spend most of its time in the fast path's set-up while three of
+// its four wavefronts hold the CU with nothing to do.  The exact path's codes
+// are the fast path's (which certifies each of its codes against them).  The
+// loops cover any chunk length, so a larger tensor routed here is stepped
+// correctly, only slowly.
+
+// The chunk of this wavefront (false: none, the wavefront exits).
+__device__ __forceinline__ bool small_job(const StepSrc &src, Tensor &T, LumaGroup &g,
+                                          int64_t &ci, int64_t &cidx) {
+  cidx = (int64_t)src.small_from + (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (cidx >= src.n_chunks) return false;
+  const LumaChunk c = src.chunks[cidx];
+  T = src.tensors[c.tensor];
+  g = src.groups[T.group];
+  ci = c.index;
+  return true;
+}
+
+__global__ __launch_bounds__(kThreads) void pass1_small_kernel(StepSrc src,
+                                                               float *__restrict__ partials) {
+  if (skip_step(src)) return;
+  Tensor T;
+  LumaGroup grp;
+  int64_t ci, cidx;
+  if (!small_job(src, T, grp, ci, cidx)) return;   // no barriers below
+  const Hyper h = group_hyper(grp);
+  const bool scaled = src.scaling.grad_scale != nullptr;
+  const float inv = inv_scale(src);
+  const int64_t prev = T.slot->step;
+  const Grid *old = prev >= 1 ? (const Grid *)&T.slot->grid[prev & 1] : nullptr;
+  int64_t beg, end;
+  chunk_range(src, T, ci, beg, end);
+  const uint32_t lane = lane_id();
+  float am = 0.0f, av = 0.0f;
+  uint32_t im = kNoArg, iv = kNoArg;
+  for (int64_t e0 = beg + (int64_t)lane * kVec; e0 < end; e0 += 64 * kVec) {
+    for (int j = 0; j < kVec; ++j) {
+      const int64_t i = e0 + j;
+      if (i >= end) break;
+      float mn, vn;
+      element_ema(T, h, old, i, scaled, inv, mn, vn);
+      if (beats(fabsf(mn), am)) {
+        am = fabsf(mn);
+        im = (uint32_t)(i - beg);
+      }
+      if (beats(vn, av)) {
+        av = vn;
+        iv = (uint32_t)(i - beg);
+      }
+    }
+  }
+  wave_argmax(am, im);
+  wave_argmax(av, iv);
+  if (lane == 0) put_partial(partials, cidx, am, av, im, iv);
+}
+
 // S' = max(max, floor) with Python's max() semantics (a NaN maximum stays NaN).
 __device__ __forceinline__ double py_max(double a, double floor_) { return floor_ > a ? floor_ : a; }
 
@@ -369,10 +437,44 @@ __global__ __launch_bounds__(64) void finalize_kernel(StepSrc src,
     s.grid[par] = g;
     s.hyp = h;
     s.step = t;
-    s.summ_step = (src.summaries && T.summary) ? t : 0;
+    // (the small-tensor kernels write no summaries)
+    s.summ_step = (src.summaries && T.summary && T.first_chunk < src.small_from) ? t : 0;
     s.summ_shift = src.chunk_shift;
     s.seed_m = seed_m;
     s.seed_v = seed_v;
+  }
+}
+
+// The exact pass 2 of elements e0 .. min(e0 + 8, end) - 1: update, draws
+// (Philox or injected), new codes.
+__device__ __forceinline__ void exact_group(const Tensor &T, const Hyper &h, const Grid *old,
+                                            const Grid &G, int64_t e0, int64_t end, bool scaled,
+                                            float inv, bool inj, const PhiloxBase &pb, uint32_t k0,
+                                            uint32_t k1) {
+  U4 coarse{}, fine0{}, fine1{};
+  if (!inj) {
+    coarse = philox_coarse_block((uint64_t)e0, pb, k0, k1);
+    fine0 = philox_fine_block((uint64_t)e0, pb, k0, k1);
+    fine1 = philox_fine_block((uint64_t)e0 + 4, pb, k0, k1);
+  }
+  for (int j = 0; j < kVec; ++j) {
+    const int64_t i = e0 + j;
+    if (i >= end) break;
+    float mn, vn;
+    element_ema(T, h, old, i, scaled, inv, mn, vn);
+    T.param[i] = exact_param_update(T.param[i], mn, vn, h);
+    float um, uw;
+    if (!inj) {
+      uint32_t bm, bw;
+      philox_uniform_bits(coarse, j < 4 ? fine0 : fine1, (uint64_t)i, bm, bw);
+      um = (float)bm * 0x1p-24f;
+      uw = (float)bw * 0x1p-24f;
+    } else {
+      um = T.u_m[i];
+      uw = T.u_w[i];
+    }
+    T.q_m[i] = (int16_t)exact_quant_m(mn, G, um);
+    T.q_w[i] = (int16_t)(uint16_t)exact_quant_w(vn, G, h.eps, uw);
   }
 }
 
@@ -397,33 +499,33 @@ __global__ __launch_bounds__(kThreads) void pass2_exact_kernel(StepSrc src, uint
   const PhiloxBase pb = philox_base(T.elem_offset);
   const bool inj = injected(T, noise_mode);
 
-  for (int64_t e0 = beg + (int64_t)threadIdx.x * kVec; e0 < end; e0 += (int64_t)kThreads * kVec) {
-    U4 coarse{}, fine0{}, fine1{};
-    if (!inj) {
-      coarse = philox_coarse_block((uint64_t)e0, pb, k0, k1);
-      fine0 = philox_fine_block((uint64_t)e0, pb, k0, k1);
-      fine1 = philox_fine_block((uint64_t)e0 + 4, pb, k0, k1);
-    }
-    for (int j = 0; j < kVec; ++j) {
-      const int64_t i = e0 + j;
-      if (i >= end) break;
-      float mn, vn;
-      element_ema(T, h, old, i, scaled, inv, mn, vn);
-      T.param[i] = exact_param_update(T.param[i], mn, vn, h);
-      float um, uw;
-      if (!inj) {
-        uint32_t bm, bw;
-        philox_uniform_bits(coarse, j < 4 ? fine0 : fine1, (uint64_t)i, bm, bw);
-        um = (float)bm * 0x1p-24f;
-        uw = (float)bw * 0x1p-24f;
-      } else {
-        um = T.u_m[i];
-        uw = T.u_w[i];
-      }
-      T.q_m[i] = (int16_t)exact_quant_m(mn, G, um);
-      T.q_w[i] = (int16_t)(uint16_t)exact_quant_w(vn, G, h.eps, uw);
-    }
-  }
+  for (int64_t e0 = beg + (int64_t)threadIdx.x * kVec; e0 < end; e0 += (int64_t)kThreads * kVec)
+    exact_group(T, h, old, G, e0, end, scaled, inv, inj, pb, k0, k1);
+}
+
+// Pass 2 of the small tensors (see pass1_small_kernel).
+__global__ __launch_bounds__(kThreads) void pass2_small_kernel(StepSrc src, uint64_t base_seed,
+                                                               int noise_mode) {
+  if (skip_step(src)) return;
+  Tensor T;
+  LumaGroup grp;
+  int64_t ci, cidx;
+  if (!small_job(src, T, grp, ci, cidx)) return;
+  const bool scaled = src.scaling.grad_scale != nullptr;
+  const float inv = inv_scale(src);
+  const Slot &S = *(const Slot *)T.slot;
+  const int64_t t = S.step;   // advanced by finalize
+  const Hyper h = S.hyp;
+  const Grid *old = t >= 2 ? &S.grid[(t - 1) & 1] : nullptr;
+  const Grid G = S.grid[t & 1];
+  int64_t beg, end;
+  chunk_range(src, T, ci, beg, end);
+  uint32_t k0, k1;
+  step_key(base_seed, t, T.param_id, k0, k1);
+  const PhiloxBase pb = philox_base(T.elem_offset);
+  const bool inj = injected(T, noise_mode);
+  for (int64_t e0 = beg + (int64_t)lane_id() * kVec; e0 < end; e0 += 64 * kVec)
+    exact_group(T, h, old, G, e0, end, scaled, inv, inj, pb, k0, k1);
 }
 
 // ---------------------------------------------------------------------------
@@ -697,10 +799,6 @@ template <typename V>
 __device__ __forceinline__ V in_vgpr(V x) {
   asm("" : "+v"(x));
   return x;
-}
-
-__device__ __forceinline__ uint32_t lane_id() {
-  return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
 }
 
 // Position of this lane's entry among the lanes of `mask`, offset by base.
@@ -1995,23 +2093,40 @@ static int launch_step(StepSrc src, int32_t n_tensors, int32_t n_chunks, float *
   };
   if (int r = mark(0)) return r;
   const bool exact = (flags & LUMA_FLAG_EXACT_ONLY) != 0;
-  if (exact)
-    hipLaunchKernelGGL(pass1_exact_kernel, dim3(n_chunks), dim3(kThreads), 0, s, src, partials);
-  else
-    hipLaunchKernelGGL(pass1_fast_kernel, dim3(n_chunks), dim3(kThreads), 0, s, src, partials);
-  if (int r = check_launch("luma_step: pass 1 launch")) return r;
+  // chunks [0, small_from): a workgroup each; [small_from, n_chunks): small
+  // tensors, a wavefront each
+  const int32_t n_big = src.small_from;
+  const int32_t small_blocks = (n_chunks - n_big + kThreads / 64 - 1) / (kThreads / 64);
+  if (n_big > 0) {
+    if (exact)
+      hipLaunchKernelGGL(pass1_exact_kernel, dim3(n_big), dim3(kThreads), 0, s, src, partials);
+    else
+      hipLaunchKernelGGL(pass1_fast_kernel, dim3(n_big), dim3(kThreads), 0, s, src, partials);
+    if (int r = check_launch("luma_step: pass 1 launch")) return r;
+  }
+  if (small_blocks > 0) {
+    hipLaunchKernelGGL(pass1_small_kernel, dim3(small_blocks), dim3(kThreads), 0, s, src, partials);
+    if (int r = check_launch("luma_step: pass 1 (small tensors) launch")) return r;
+  }
   if (int r = mark(1)) return r;
   hipLaunchKernelGGL(finalize_kernel, dim3(n_tensors), dim3(64), 0, s, src,
                      (const float *)partials);
   if (int r = check_launch("luma_step: finalize launch")) return r;
   if (int r = mark(2)) return r;
-  if (exact)
-    hipLaunchKernelGGL(pass2_exact_kernel, dim3(n_chunks), dim3(kThreads), 0, s, src, base_seed,
-                       (int)noise_mode);
-  else
-    hipLaunchKernelGGL(pass2_fast_kernel, dim3(n_chunks), dim3(kThreads), 0, s, src, base_seed,
-                       (int)noise_mode);
-  if (int r = check_launch("luma_step: pass 2 launch")) return r;
+  if (n_big > 0) {
+    if (exact)
+      hipLaunchKernelGGL(pass2_exact_kernel, dim3(n_big), dim3(kThreads), 0, s, src, base_seed,
+                         (int)noise_mode);
+    else
+      hipLaunchKernelGGL(pass2_fast_kernel, dim3(n_big), dim3(kThreads), 0, s, src, base_seed,
+                         (int)noise_mode);
+    if (int r = check_launch("luma_step: pass 2 launch")) return r;
+  }
+  if (small_blocks > 0) {
+    hipLaunchKernelGGL(pass2_small_kernel, dim3(small_blocks), dim3(kThreads), 0, s, src,
+                       base_seed, (int)noise_mode);
+    if (int r = check_launch("luma_step: pass 2 (small tensors) launch")) return r;
+  }
   return mark(3);
 }
 
@@ -2029,6 +2144,10 @@ static int step_impl(const LumaStepArgs *a, void *stream, void *const *events) {
   src.groups = a->groups;
   src.scaling = a->scaling;
   src.chunk_shift = __builtin_ctz((unsigned)c);
+  if (a->small_chunks < 0 || a->small_chunks > a->n_chunks)
+    return fail("luma_step: small_chunks must be in [0, n_chunks]");
+  src.small_from = a->n_chunks - a->small_chunks;
+  src.n_chunks = a->n_chunks;
   return launch_step(src, a->n_tensors, a->n_chunks, a->partials, a->base_seed, a->noise_mode,
                      a->flags, static_cast<hipStream_t>(stream), events);
 }
@@ -2099,6 +2218,8 @@ int luma_step_tensor(const LumaTensor *tensor, const LumaGroup *group, float *pa
   src.one.first_chunk = 0;
   src.group = *group;
   src.chunk_shift = shift;
+  src.small_from = (int32_t)nch;   // one tensor: no small-tensor chunks
+  src.n_chunks = (int32_t)nch;
   if (scaling) src.scaling = *scaling;
   return launch_step(src, 1, (int32_t)nch, partials, base_seed, noise_mode, flags,
                      static_cast<hipStream_t>(stream), nullptr);

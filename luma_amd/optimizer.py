@@ -131,9 +131,12 @@ class _Engine:
         self.device = device
         self._tensor_key = None      # bytes of the uploaded tensor table
         self._tensor_src = None      # (table array, chunk setting) last uploaded or matched
-        self._numel_key = None       # bytes of its numel column and chunk length (chunk table)
+        self._numel_key = None       # bytes of its numel column and chunk layout (chunk table)
+        self._first = None           # first_chunk column of that layout
         self._chunk = L.CHUNK_ELEMS  # chunk length of the uploaded chunk table
         self.chunk_elems = 0         # fixed chunk length (a power of two), 0: chunk_for's choice
+        self.small_tensors = True    # step tensors of <= SMALL_TENSOR elements a wavefront each
+        self._small_chunks = 0       # trailing chunk records of such tensors (uploaded table)
         self._d_tensors = None
         self._d_chunks = None
         self._n_chunks = 0
@@ -219,11 +222,12 @@ class _Engine:
         launch, unchanged since: the comparison of its contents is skipped."""
         capturing = torch.cuda.is_current_stream_capturing()
         n = len(tt)
+        setting = (self.chunk_elems, self._small_limit())
         if not (same_table and self._tensor_src is not None and self._tensor_src[0] is tt
-                and self._tensor_src[1] == self.chunk_elems):
+                and self._tensor_src[1] == setting):
             self._tensor_src = None     # stays unset if the upload fails
             self._match_table(tt, capturing)
-            self._tensor_src = (tt, self.chunk_elems)
+            self._tensor_src = (tt, setting)
         n_chunks = self._n_chunks
         gkey = groups.tobytes()
         if gkey != self._group_key:
@@ -245,7 +249,7 @@ class _Engine:
             chunks=self._d_chunks.data_ptr(), groups=self._d_groups.data_ptr(),
             partials=self._partials.data_ptr(),
             base_seed=base_seed & _MASK64, noise_mode=noise_mode, flags=flags,
-            chunk_elems=self._chunk, reserved=0,
+            chunk_elems=self._chunk, small_chunks=self._small_chunks,
             scaling=L.Scaling(scaling[0] or None, scaling[1] or None))
         if self.profile_events is None:
             L.check(self.lib.luma_step(ctypes.byref(args), self._stream()), "luma_step")
@@ -254,32 +258,62 @@ class _Engine:
             L.check(self.lib.luma_step_profiled(ctypes.byref(args), self._stream(), evs),
                     "luma_step_profiled")
 
+    def _small_limit(self) -> int:
+        """Largest tensor stepped a wavefront each (0: none)."""
+        return int(L.SMALL_TENSOR) if self.small_tensors else 0
+
+    def chunk_layout(self, numels: np.ndarray, c: int):
+        """Chunk table layout of tensors of these sizes at chunk length c: the
+        first chunk of every tensor, the chunk records (tensor, index) and the
+        number of trailing records that belong to small tensors.  Tensors of at
+        most SMALL_TENSOR elements come last, stepped a wavefront per chunk
+        (luma.h, LumaStepArgs.small_chunks); the others keep their order."""
+        n = len(numels)
+        nch = (numels + c - 1) // c
+        if self.small_tensors:
+            small = numels <= L.SMALL_TENSOR
+            order = np.concatenate([np.nonzero(~small)[0], np.nonzero(small)[0]])
+            n_small = int(nch[small].sum())
+        else:
+            order = np.arange(n)
+            n_small = 0
+        nch_o = nch[order]
+        first_o = np.zeros(n, dtype=np.int64)
+        np.cumsum(nch_o[:-1], out=first_o[1:])
+        first = np.empty(n, dtype=np.int64)
+        first[order] = first_o
+        n_chunks = int(nch.sum())
+        ch = np.empty(n_chunks, dtype=L.CHUNK_DTYPE)
+        ch["tensor"] = np.repeat(order.astype(np.int32), nch_o)
+        ch["index"] = np.arange(n_chunks, dtype=np.int64) - np.repeat(first_o, nch_o)
+        return first, ch, n_small
+
     def _match_table(self, tt: np.ndarray, capturing: bool):
         """Upload tt (and its chunk table) unless the device holds it already."""
-        n = len(tt)
-        # first_chunk follows the chunk length of this launch (a cached table
-        # may have been built for another)
+        # first_chunk follows the chunk length and layout of this launch (a
+        # cached table may have been built for another)
         numels = tt["numel"]
         c = self.chunk_for(numels)
-        nch = (numels + c - 1) // c
-        first = np.zeros(n, dtype=np.int64)
-        np.cumsum(nch[:-1], out=first[1:])
-        tt["first_chunk"] = first
-        key = tt.tobytes()
+        nkey = (numels.tobytes() + c.to_bytes(4, "little")
+                + self._small_limit().to_bytes(8, "little"))
+        if nkey != self._numel_key:
+            if capturing:
+                raise self._capture_error("the parameter or gradient set")
+            first, ch, n_small = self.chunk_layout(numels, c)
+            tt["first_chunk"] = first
+            key = tt.tobytes()
+            self._d_chunks = self._upload(ch)
+            self._n_chunks = len(ch)
+            self._small_chunks = n_small
+            self._chunk = c
+            self._numel_key = nkey
+            self._first = first
+        else:
+            tt["first_chunk"] = self._first
+            key = tt.tobytes()
         if key != self._tensor_key:
             if capturing:
                 raise self._capture_error("the parameter or gradient set")
-            nkey = numels.tobytes() + c.to_bytes(4, "little")
-            if nkey != self._numel_key:
-                n_chunks = int(nch.sum())
-                ch = np.empty(n_chunks, dtype=L.CHUNK_DTYPE)
-                ch["tensor"] = np.repeat(np.arange(n, dtype=np.int32), nch)
-                ch["index"] = (np.arange(n_chunks, dtype=np.int64)
-                               - np.repeat(tt["first_chunk"].astype(np.int64), nch))
-                self._d_chunks = self._upload(ch)
-                self._n_chunks = n_chunks
-                self._chunk = c
-                self._numel_key = nkey
             self._d_tensors = self._upload(tt)
             self._tensor_key = key
 

@@ -1,0 +1,91 @@
+"""Small tensors stepped one wavefront each (LumaStepArgs.small_chunks).
+
+Tensors of at most LUMA_SMALL_TENSOR elements take the last chunk records
+and the wavefront kernels (exact path).  Their results must be the oracle's,
+as the workgroup kernels' are, whichever route a tensor takes from step to
+step; a large tensor routed to the wavefront kernels is stepped correctly
+too, and the code summaries of such a step are not used by the next one.
+"""
+
+import pytest
+import torch
+
+from luma_amd import _lib as L
+
+from config_util import SampledPair, normal_grad
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda")
+# around the limit, tiny, and a few tensors that take whole workgroups
+SIZES = [1, 2, 7, 64, 100, 511, 512, 513, 1000, 2047, 2048, 4096, 5000, 70000, 300, 8]
+
+
+def _params(seed=11):
+    gen = torch.Generator(device=DEV).manual_seed(seed)
+    return [(torch.randn(n, device=DEV, generator=gen) * 0.02) for n in SIZES]
+
+
+def _step(pair, t, dtype=torch.float32):
+    gen = torch.Generator(device=DEV).manual_seed(500 + t)
+    gd = [normal_grad(p.shape, 1e-3, gen, DEV, dtype, outliers=1e-2, zeros=0.02)
+          for p in pair.params]
+    pair.step(gd, {i: g.cpu() for i, g in enumerate(gd)})
+    return pair.check()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_small_tensors_match_oracle(dtype):
+    pair = SampledPair(_params(), range(len(SIZES)))
+    for t in range(1, 5):
+        _step(pair, t, dtype)
+        eng = pair.opt._engine
+        assert eng._small_chunks == sum(1 for n in SIZES if n <= L.SMALL_TENSOR)
+
+
+def test_routes_change_between_steps(monkeypatch):
+    """Step 2 routes every tensor (up to 70000 elements) to the wavefront
+    kernels, step 3 none, step 4 the default: every step matches the oracle,
+    so the summaries of step 2's large tensors (not written) are not used by
+    step 3's pass 1."""
+    pair = SampledPair(_params(12), range(len(SIZES)))
+    _step(pair, 1)
+    monkeypatch.setattr(L, "SMALL_TENSOR", 1 << 20)
+    _step(pair, 2)
+    assert pair.opt._engine._small_chunks == pair.opt._engine._n_chunks
+    monkeypatch.setattr(L, "SMALL_TENSOR", 512)
+    pair.opt._engine.small_tensors = False
+    _step(pair, 3)
+    assert pair.opt._engine._small_chunks == 0
+    pair.opt._engine.small_tensors = True
+    _step(pair, 4)
+    assert pair.opt._engine._small_chunks > 0
+
+
+def test_small_route_matches_workgroup_route():
+    """With Philox draws: the same codes and scales through either route,
+    parameters within 1e-6 of their scale (the workgroup kernels' update is
+    the fast path's, within 1e-6 of the exact one)."""
+    from luma_amd import LUMA
+    gen = torch.Generator(device=DEV).manual_seed(3)
+    sizes = [1, 5, 64, 200, 512, 333] * 20
+    a = [(torch.randn(n, device=DEV, generator=gen) * 0.02).requires_grad_(True) for n in sizes]
+    b = [p.detach().clone().requires_grad_(True) for p in a]
+    oa, ob = LUMA(a, lr=1e-3), LUMA(b, lr=1e-3)
+    ob._base_seed = oa._base_seed
+    ob._get_engine(b[0].device).small_tensors = False
+    for t in range(4):
+        for p, q in zip(a, b):
+            g = torch.randn(p.shape, device=DEV, generator=gen) * 1e-3
+            p.grad, q.grad = g, g.clone()
+        oa.step()
+        ob.step()
+    torch.cuda.synchronize()
+    assert oa._engine._small_chunks == len(sizes) and ob._engine._small_chunks == 0
+    sa, sb = oa.state_dict()["state"], ob.state_dict()["state"]
+    for i, (p, q) in enumerate(zip(a, b)):
+        assert torch.equal(sa[i]["Q_m"], sb[i]["Q_m"]), i
+        assert torch.equal(sa[i]["Q_w"], sb[i]["Q_w"]), i
+        assert sa[i]["S_m"] == sb[i]["S_m"] and sa[i]["S_v"] == sb[i]["S_v"], i
+        d = float((p.detach() - q.detach()).abs().max())
+        assert d <= 1e-6 * float(q.detach().abs().max()) + 1e-8, (i, d)

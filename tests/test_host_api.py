@@ -191,3 +191,26 @@ def test_state_arena_layout():
         qw.fill_(-(i + 1))
     for i, (qm, qw) in enumerate(views):
         assert (qm == i + 1).all() and (qw == -(i + 1)).all()
+
+
+def test_chunk_layout_small_tensors_last():
+    """Tensors of at most SMALL_TENSOR elements take the last chunk records
+    (one each); the others keep their order; first_chunk points at each
+    tensor's records."""
+    import types
+    import numpy as np
+    from luma_amd.optimizer import _Engine
+    numels = np.array([5000, 3, 512, 513, 40000, 1, 20000], dtype=np.int64)
+    eng = types.SimpleNamespace(small_tensors=True)
+    first, ch, n_small = _Engine.chunk_layout(eng, numels, 16384)
+    assert n_small == 3
+    assert ch["tensor"].tolist() == [0, 3, 4, 4, 4, 6, 6, 1, 2, 5]
+    assert ch["index"].tolist() == [0, 0, 0, 1, 2, 0, 1, 0, 0, 0]
+    assert first.tolist() == [0, 7, 8, 1, 2, 9, 5]
+    for t in range(len(numels)):
+        assert ch["tensor"][first[t]] == t and ch["index"][first[t]] == 0
+    eng.small_tensors = False
+    first, ch, n_small = _Engine.chunk_layout(eng, numels, 16384)
+    assert n_small == 0
+    assert ch["tensor"].tolist() == [0, 1, 2, 3, 4, 4, 4, 5, 6, 6]
+    assert first.tolist() == [0, 1, 2, 3, 4, 7, 8]
