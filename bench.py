@@ -226,6 +226,30 @@ def copy_calibration(reps):
     print(json.dumps({"copy_calibration_bytes_each_way": COPY_ELEMS * 4, "launches": reps}))
 
 
+def ceilings(reps=5):
+    """Achievable HBM rates of plain torch kernels on this GPU, next to which
+    the step's passes are read: a copy (y = x * 1: reads and writes), and a
+    read-only reduction (max), each over 2^32 float32 (16 GiB read)."""
+    n = 1 << 32
+    x = torch.ones(n, device="cuda")
+    out = {}
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    half = x[: n // 2]
+    y = torch.empty_like(half)
+    for name, fn, nbytes in (("copy", lambda: torch.mul(half, 1.0, out=y), n * 4),
+                             ("read_max", lambda: torch.amax(x), n * 4)):
+        fn()
+        torch.cuda.synchronize()
+        ev[0].record()
+        for _ in range(reps):
+            fn()
+        ev[1].record()
+        torch.cuda.synchronize()
+        ms = ev[0].elapsed_time(ev[1]) / reps
+        out[name] = {"ms": round(ms, 3), "bytes": nbytes, "GB_s": round(nbytes / ms / 1e6, 1)}
+    print(json.dumps({"hbm_ceilings": out, "peak_GB_s": HBM_PEAK / 1e9}))
+
+
 def _pmc_per_dispatch(path, kernel_prefix, counter):
     import csv
     vals = {}
@@ -332,6 +356,10 @@ def stats_report(config, trace_csv, bench_json, out):
                      f"{min(d):.3f} | {max(d):.3f} | {100 * sum(d) / total:.2f} | "
                      f"{'' if bev is None else f'{bev:.3f}'} |")
     lines += ["",
+              "The bench's HIP-event intervals bracket each pass: pass 1's includes "
+              "`luma::pass1_small_kernel`, pass 2's `luma::pass2_small_kernel` (tensors of at most "
+              "512 elements, one wavefront each) when the set has any.",
+              "",
               f"Step time in the same run (bench wall clock): {bench['ms_per_step']:.3f} ms; "
               f"{bench['value']} Gparams/s.",
               "Kernels not listed are torch's synthetic-data set-up outside the timed region."]
@@ -405,6 +433,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="llama3_8b", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--ceilings", action="store_true",
+                    help="time torch's copy and max over 16 GiB (achievable HBM rates)")
     ap.add_argument("--copy-calibration", type=int, metavar="REPS",
                     help="only run the copy kernel used to scale the HBM counters")
     ap.add_argument("--traffic-report", nargs=7,
@@ -427,6 +457,9 @@ def main():
         return
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+    if args.ceilings:
+        ceilings()
         return
     if args.gpus != 1:
         print(f"bench.py: measures one GPU only (--gpus {args.gpus} requested); "
