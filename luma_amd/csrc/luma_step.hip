@@ -687,6 +687,46 @@ __device__ __noinline__ float2 exact_mv(int qm, int qw, float g, const LUMA_GLOB
   return make_float2(mn, vn);
 }
 
+// The exact |m'| and v' of each tensor's two seeds (the elements that held
+// its maxima at the previous step), for pass 1's initial thresholds: one
+// wavefront per tensor (lane 0 the momentum seed, lane 1 the preconditioner
+// seed), instead of every wavefront of every chunk evaluating them.  Tensors
+// without state and small-route tensors (exact pass 1) need none.
+__global__ __launch_bounds__(kThreads) void seed_kernel(StepSrc src, int32_t n_tensors) {
+  if (skip_step(src)) return;
+  const int64_t ti = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (ti >= n_tensors) return;
+  Tensor T;
+  LumaGroup grp;
+  if (src.tensors) {
+    T = src.tensors[ti];
+    grp = src.groups[T.group];
+  } else {
+    T = src.one;
+    grp = src.group;
+  }
+  if (T.first_chunk >= src.small_from) return;
+  LUMA_GLOBAL Slot &S = *T.slot;
+  const int64_t prev = S.step;
+  if (prev < 1) return;
+  const Hyper h = group_hyper(grp);
+  const LUMA_GLOBAL Grid *old = &S.grid[prev & 1];
+  const uint32_t lane = lane_id();
+  const int64_t si = lane == 0 ? S.seed_m : S.seed_v;
+  float2 e = make_float2(0.0f, 0.0f);
+  if (lane < 2 && si >= 0 && si < T.numel) {
+    float g = load_grad(T.grad, si, T.grad_dtype);
+    if (src.scaling.grad_scale != nullptr) g = unscale_rt(g, inv_scale(src), T.grad_dtype);
+    e = exact_mv(T.q_m[si], (int)(uint16_t)T.q_w[si], g, old, h);
+  }
+  const float xm = __shfl(e.x, 0, 64), xv = __shfl(e.y, 1, 64);
+  if (lane == 0) {
+    S.seed_xm = fabsf(xm);
+    S.seed_xv = xv;
+    S.seed_t = prev + 1;
+  }
+}
+
 // New code of one element before its draw is final (exact path): the
 // 16-bit code when the uniform u >= p (lo) and when u < p (hi), and the
 // argument a of p = exact_sr_prob(a, z).  The caller knows u to an interval
@@ -1101,21 +1141,18 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     }
   };
   // Seeds: the elements that held the tensor's maxima at the previous step
-  // (recorded by its finalize).  Their exact m', v' now are lower bounds of
-  // this step's maxima, whichever elements hold those, so they start the
-  // thresholds high: blocks below them are skipped from the first iteration.
-  // Lane 0 evaluates the momentum seed, lane 1 the preconditioner seed.
+  // (recorded by its finalize).  Their exact m', v' now (seed_kernel, once
+  // per tensor before this pass) are lower bounds of this step's maxima,
+  // whichever elements hold those, so they start the thresholds high: blocks
+  // below them are skipped from the first iteration.
   if (old) {
     const LUMA_GLOBAL Slot &S = *T.slot;
-    const int64_t sm = S.seed_m, sv = S.seed_v;
-    const int64_t si = lane == 0 ? sm : sv;
-    float2 e = make_float2(0.0f, 0.0f);
-    if (lane < 2 && si >= 0 && si < T.numel) e = exact_at(si);
-    const float lbm = __shfl(e.x, 0, 64), lbv = __shfl(e.y, 1, 64);
-    T0m = exact_threshold(fabsf(lbm), B.abs_m, hi_m);
-    T0v = exact_threshold(lbv, B.abs_v, hi_v);
-    Tm = T0m;
-    Tv = T0v;
+    if (S.seed_t == S.step + 1) {
+      T0m = exact_threshold(S.seed_xm, B.abs_m, hi_m);
+      T0v = exact_threshold(S.seed_xv, B.abs_v, hi_v);
+      Tm = T0m;
+      Tv = T0v;
+    }
   }
   // Every lane of a wave runs the same iterations (lanes past the end carry
   // n = 0), so the ballots and the queue length stay uniform across the wave;
@@ -1891,6 +1928,7 @@ __device__ void write_slot(Slot &s, int64_t t, double s_m, double s_v, double ep
   s.summ_step = 0;   // codes written by other means: no summaries for them
   s.summ_shift = 0;
   s.seed_m = s.seed_v = -1;
+  s.seed_t = 0;
 }
 
 __global__ void set_scales_kernel(const LumaScaleInit *__restrict__ items, int n) {
@@ -2098,10 +2136,14 @@ static int launch_step(StepSrc src, int32_t n_tensors, int32_t n_chunks, float *
   const int32_t n_big = src.small_from;
   const int32_t small_blocks = (n_chunks - n_big + kThreads / 64 - 1) / (kThreads / 64);
   if (n_big > 0) {
-    if (exact)
+    if (exact) {
       hipLaunchKernelGGL(pass1_exact_kernel, dim3(n_big), dim3(kThreads), 0, s, src, partials);
-    else
+    } else {
+      hipLaunchKernelGGL(seed_kernel, dim3((n_tensors + kThreads / 64 - 1) / (kThreads / 64)),
+                         dim3(kThreads), 0, s, src, n_tensors);
+      if (int r = check_launch("luma_step: seed launch")) return r;
       hipLaunchKernelGGL(pass1_fast_kernel, dim3(n_big), dim3(kThreads), 0, s, src, partials);
+    }
     if (int r = check_launch("luma_step: pass 1 launch")) return r;
   }
   if (small_blocks > 0) {
