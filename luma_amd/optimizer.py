@@ -368,7 +368,7 @@ class _Plan:
     """
 
     __slots__ = ("all_params", "has_grad", "work_idx", "layout_at", "layout", "gdtypes",
-                 "device_index", "states", "tt", "host")
+                 "device_index", "states", "tt", "host", "chunk_setting")
 
     _FIELDS = (L.TENSOR_DTYPE.itemsize, L.TENSOR_DTYPE.fields["grad"][1],
                L.TENSOR_DTYPE.fields["param"][1])
@@ -393,6 +393,9 @@ class _Plan:
         self.states = states
         self.tt = tt
         self.host = host
+        # the engine's fixed chunk length when planned: the code summaries in
+        # tt were sized for the chunk length it gave
+        self.chunk_setting = None
 
     @staticmethod
     def usable(work, rows) -> bool:
@@ -702,7 +705,8 @@ class LUMA(Optimizer):
                 loss = closure()
 
         plan = self._plan
-        if plan is not None and self._noise is None:
+        if (plan is not None and self._noise is None
+                and plan.chunk_setting == self._engine.chunk_elems):
             r = plan.refresh(self.param_groups)
             if r:
                 self._engine.launch(plan.tt, self._group_table(), self._base_seed,
@@ -804,5 +808,6 @@ class LUMA(Optimizer):
             state["step"] += 1
         if noise_mode == L.NOISE_PHILOX and _Plan.usable(work, rows):
             self._plan = _Plan(self.param_groups, work, rows, states, tt, engine.host)
+            self._plan.chunk_setting = engine.chunk_elems
         self._noise = None
         return loss

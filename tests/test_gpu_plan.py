@@ -137,3 +137,19 @@ def test_plan_step_counts_match_device_counts():
     sd = oa.state_dict()["state"]
     assert [sd[i]["step"] for i in range(len(a))] == [5] * len(a)
     assert [oa.state[p]["step"] for p in a] == [5] * len(a)
+
+
+def test_plan_dropped_when_the_chunk_length_changes():
+    """A plan's code summaries were sized for its chunk length: a new fixed
+    chunk length rebuilds the table (and the summaries) instead."""
+    a, b, oa, ob, gen = _pair()
+    for p in a:
+        p.grad = torch.randn(p.shape, device="cuda", generator=gen) * 1e-3
+    oa.step()
+    plan = oa._plan
+    assert plan is not None and plan.chunk_setting == 0
+    oa._engine.chunk_elems = 2048
+    oa.step()
+    assert oa._plan is not plan and oa._plan.chunk_setting == 2048
+    assert oa._engine._chunk == 2048
+    torch.cuda.synchronize()
