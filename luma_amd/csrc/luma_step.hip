@@ -1174,23 +1174,19 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     const FastEma d = fast_ema<SMALL, false>((int)(sw & 0xFFFFu), (int)(kCodeFloat | (sw >> 16)),
                                              0.0f, K.dm, K.ndw, K.nbias, K.iwmin, K.eps, K.b1,
                                              K.omb1, K.b2, K.omb2, K.sign);
-    Raw8 raw;   // gradients of the lane's next group, loaded one iteration ahead
-    load_grads<GD>(T, beg + (int64_t)threadIdx.x * kVec, raw);
-    for (; it < n_whole; ++it) {
-      const int64_t e0 = beg + ((int64_t)it * kThreads + threadIdx.x) * kVec;
-      const int nx = it + 1 < n_whole ? it + 1 : it;
-      const Raw8 cur = raw;
-      load_grads<GD>(T, beg + ((int64_t)nx * kThreads + threadIdx.x) * kVec, raw);
-      // The bound at the thread's code extremes and its largest |g|: the
-      // operations of p1_reach.
+    // One iteration on the gradients `cur` of group j: the bound at the
+    // thread's code extremes and its largest |g| (the operations of
+    // p1_reach); only when it reaches a threshold in some lane are the
+    // wave's codes read and decoded.
+    auto visit = [&](const Raw8 &cur, int j) {
+      const int64_t e0 = beg + ((int64_t)j * kThreads + threadIdx.x) * kVec;
       {
         const float g = raw_gmax<GD, SCALED>(cur, K.inv);
         const float mn = fmaf(K.b1, d.am, K.omb1 * g);
         const float vn = fmaf(K.b2, d.v, K.omb2 * (g * g));
         const uint32_t um = __float_as_uint(mn * K.up_m) & 0x7FFFFFFFu;
         const uint32_t uv = __float_as_uint(fmaf(vn, K.up_v, K.abs_v)) & 0x7FFFFFFFu;
-        if (!__ballot(um >= Tm || uv >= Tv))
-          continue;   // no element of the wave's groups can be a candidate: codes not read
+        if (!__ballot(um >= Tm || uv >= Tv)) return;   // no candidate: codes not read
       }
       Group8 G;
       unpack_grads<GD>(cur, G);
@@ -1208,7 +1204,24 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
       uint32_t am[kVec], av[kVec];
       p1_compute<SMALL, true>(G, K, kVec, Tm, Tv, am, av);
       take(e0, kVec, am, av);
+    };
+    // Two gradient buffers, each loaded one iteration before its use, in a
+    // loop unrolled by two: copying a buffer whose load is in flight (a
+    // single buffer carried across iterations) would make every iteration
+    // wait for the load just issued.
+    auto group_at = [&](int j) {
+      return beg + ((int64_t)(j < n_whole ? j : n_whole - 1) * kThreads + threadIdx.x) * kVec;
+    };
+    Raw8 ra, rb;
+    load_grads<GD>(T, group_at(0), ra);
+    for (; it < n_whole; it += 2) {
+      load_grads<GD>(T, group_at(it + 1), rb);
+      visit(ra, it);
+      if (it + 1 >= n_whole) break;
+      load_grads<GD>(T, group_at(it + 2), ra);
+      visit(rb, it + 1);
     }
+    it = n_whole;
   } else if (n_whole > 0) {
     Raw8 raw;
     load_raw<GD>(T, beg + (int64_t)threadIdx.x * kVec, raw);
