@@ -1365,6 +1365,25 @@ __device__ __forceinline__ T sel8(const T (&a)[kVec], uint32_t k) {
   return b2 ? y47 : y03;
 }
 
+// The packed 32-bit words of a group of 8 elements, two 16-bit values per
+// word: word k >> 1 holds element k in its low (k even) or high half.
+struct Words4 {
+  uint32_t qm[4];   // old momentum codes
+  uint32_t qw[4];   // old preconditioner codes
+  uint32_t g[4];    // 16-bit gradients after unscaling (bfloat16 only)
+};
+
+// a[k >> 1] for a per-lane k in 0..7 (two selects per level).
+__device__ __forceinline__ uint32_t word_of(const uint32_t (&a)[4], uint32_t k) {
+  const bool b1 = (k & 2u) != 0, b2 = (k & 4u) != 0;
+  const uint32_t x01 = b1 ? a[1] : a[0], x23 = b1 ? a[3] : a[2];
+  return b2 ? x23 : x01;
+}
+
+__device__ __forceinline__ uint32_t pack_lo16(uint32_t hi, uint32_t lo) {
+  return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
+
 // Certified LogSR decision (see luma_fast.h): with z = y + 1 - c, c the
 // middle of the uniform's interval, the code is floor(z); it is certain
 // when [z - e, z + e] holds no integer, e bounding |z - z_exact| plus the
@@ -1491,12 +1510,42 @@ __device__ __forceinline__ void acc_codes(CodeAcc &acc, vu4 a, vu4 b) {
 
 // acc: folds in the codes the fast path stores for the lane's valid
 // elements (the code summaries widen them by the decision margin).
+// W: the words of the old codes and (bfloat16) gradients, for the queues.
 template <int GD, bool INJ, bool SMALL, bool SCALED, bool FULL, bool STAGE>
 __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, int64_t e0, int n,
-                                            uint32_t k0, uint32_t k1, Group8 &Q, U4 &coarse,
-                                            uint4 *stage, CodeAcc &acc) {
-  load_group<GD, true>(T, e0, n, FULL, Q);
+                                            uint32_t k0, uint32_t k1, Group8 &Q, Words4 &W,
+                                            U4 &coarse, uint4 *stage, CodeAcc &acc) {
+  if (FULL) {
+    Raw8 R;
+    R.qm = *(const LUMA_GLOBAL vu4 *)(T.q_m + e0);
+    R.qw = load_stream((const LUMA_GLOBAL vu4 *)(T.q_w + e0));
+    if (GD == LUMA_GRAD_F32) {
+      R.g0 = load_stream((const LUMA_GLOBAL vu4 *)((const LUMA_GLOBAL float *)T.grad + e0));
+      R.g1 = load_stream((const LUMA_GLOBAL vu4 *)((const LUMA_GLOBAL float *)T.grad + e0 + 4));
+    } else {
+      R.g0 = load_stream((const LUMA_GLOBAL vu4 *)((const LUMA_GLOBAL uint16_t *)T.grad + e0));
+    }
+    unpack_raw<GD>(R, Q);
+    W.qm[0] = R.qm.x; W.qm[1] = R.qm.y; W.qm[2] = R.qm.z; W.qm[3] = R.qm.w;
+    W.qw[0] = R.qw.x; W.qw[1] = R.qw.y; W.qw[2] = R.qw.z; W.qw[3] = R.qw.w;
+    W.g[0] = R.g0.x; W.g[1] = R.g0.y; W.g[2] = R.g0.z; W.g[3] = R.g0.w;
+  } else {
+    load_group<GD, true>(T, e0, n, false, Q);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      W.qm[i] = pack_lo16((uint32_t)Q.qm[2 * i + 1], (uint32_t)Q.qm[2 * i]);
+      W.qw[i] = pack_lo16((uint32_t)Q.qw[2 * i + 1], (uint32_t)Q.qw[2 * i]);
+    }
+  }
   unscale_group<GD, SCALED>(Q, C.inv);
+  // bfloat16 words of the unscaled gradients: the loaded words unless scaled
+  // (an unscaled bfloat16 gradient is a float32 with its low half zero)
+  if (GD == LUMA_GRAD_BF16 && (SCALED || !FULL)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      W.g[i] = __builtin_amdgcn_perm(__float_as_uint(Q.g[2 * i + 1]), __float_as_uint(Q.g[2 * i]),
+                                     0x07060302u);
+  }
   float p[kVec];
   if (FULL) {
     const vf4 p0 = load_stream((const LUMA_GLOBAL vf4 *)(T.param + e0));
@@ -1676,11 +1725,15 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   uint4 *stage = queue_w + kQueueCapW;
   uint32_t qlen_m = 0, qlen_w = 0;   // pending entries
   uint32_t head_m = 0, head_w = 0;   // ring position of the oldest
-  // Queue entry: x = chunk offset, y = the uniform's top 8 bits (Philox; its
-  // low 16 bits come from the fine block), z = the gradient as float32 bits
-  // (no second read of HBM), w = the old code's 16 bits.  The fast codes were
-  // already stored (or staged); the exact ones overwrite them (same
-  // wavefront, so the stores stay in program order).
+  // Queue entry of element k of a group: x = chunk offset (k = x & 7),
+  // y = the coarse Philox word holding the element's top uniform bytes (its
+  // low 16 bits come from the fine block), z = the gradient (bfloat16: the
+  // word of two unscaled gradients holding it; otherwise its float32 bits;
+  // no second read of HBM), w = the word of two old codes holding its code.
+  // The entry keeps whole words so that building it costs two selects per
+  // field; the drain, 64 entries at a time, takes the element's half.  The
+  // fast codes were already stored (or staged); the exact ones overwrite
+  // them (same wavefront, so the stores stay in program order).
   // The code of a queued element from its pair: lo = hi when the uniform's
   // interval decided it; else (Philox) the fine block gives u's low 16 bits.
   const float zm_new = nw->zm, zw_new = nw->zw;
@@ -1704,19 +1757,28 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   // 2048 elements per iteration) and to lane (o >> 3) & 63 of this wave.
   static_assert(kThreads * kVec == 2048, "iteration of a chunk offset");
   int staged_lo = 0, staged_hi = 0;
+  // an entry's element: its half of the words (sh = 16 for odd k)
+  auto ent_grad = [&](const uint4 &ent, uint32_t sh) -> float {
+    return GD == LUMA_GRAD_BF16 ? __uint_as_float((ent.z >> sh) << 16) : __uint_as_float(ent.z);
+  };
   auto run_m = [&](uint4 ent) {
     const int64_t i = beg + ent.x;
-    const CodePair c = unpack_pair(exact_pair_m((int)(int16_t)ent.w, __uint_as_float(ent.z), old,
-                                                nw, h, u_lo(ent.y, T.u_m, i),
-                                                u_hi(ent.y, T.u_m, i)));
-    T.q_m[i] = (int16_t)draw(c, zm_new, i, ent.y, 0);
+    const uint32_t sh = (ent.x & 1u) << 4;
+    const uint32_t top = INJ ? 0u : (ent.y >> sh) & 0xFFu;
+    const CodePair c = unpack_pair(exact_pair_m((int)(int16_t)(ent.w >> sh), ent_grad(ent, sh),
+                                                old, nw, h, u_lo(top, T.u_m, i),
+                                                u_hi(top, T.u_m, i)));
+    T.q_m[i] = (int16_t)draw(c, zm_new, i, top, 0);
   };
   auto run_w = [&](uint4 ent) {
     const uint32_t o = ent.x;
     const int64_t i = beg + o;
-    const CodePair c = unpack_pair(exact_pair_w((int)ent.w, __uint_as_float(ent.z), old, nw, h,
-                                                u_lo(ent.y, T.u_w, i), u_hi(ent.y, T.u_w, i)));
-    const uint16_t code = (uint16_t)draw(c, zw_new, i, ent.y, 1);
+    const uint32_t sh = (o & 1u) << 4;
+    const uint32_t top = INJ ? 0u : (ent.y >> (sh + 8u)) & 0xFFu;
+    const CodePair c = unpack_pair(exact_pair_w((int)((ent.w >> sh) & 0xFFFFu), ent_grad(ent, sh),
+                                                old, nw, h, u_lo(top, T.u_w, i),
+                                                u_hi(top, T.u_w, i)));
+    const uint16_t code = (uint16_t)draw(c, zw_new, i, top, 1);
     const int it_e = (int)(o >> 11);
     if (it_e >= staged_lo && it_e < staged_hi) {
       uint16_t *slot = (uint16_t *)&stage[(it_e % kStage) * 64 + ((o >> 3) & 63u)];
@@ -1727,7 +1789,8 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   };
   // Queue the codes of one iteration that the fast path could not certify,
   // and run full batches of 64, oldest first.
-  auto take = [&](int64_t e0, uint32_t flags, const Group8 &Q, const U4 &coarse) {
+  auto take = [&](int64_t e0, uint32_t flags, const Group8 &Q, const Words4 &W,
+                  const U4 &coarse) {
     if (!__ballot(flags != 0)) return;
     const uint32_t off0 = (uint32_t)(e0 - beg);
     // queue positions: a wave prefix sum of (momentum count | preconditioner
@@ -1738,39 +1801,38 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
     const uint32_t excl = incl - cnt;
     const uint32_t tot_m = tot & 0xFFFFu, tot_w = tot >> 16;
-    // queue entry of code k (element off0 + k): its top uniform byte is byte
-    // 2k (momentum) or 2k + 1 (preconditioner) of the coarse block, in word k/2
-    auto entry = [&](uint32_t k, int code, uint32_t byte_shift) {
-      const uint32_t w01 = (k & 2u) ? coarse.y : coarse.x, w23 = (k & 2u) ? coarse.w : coarse.z;
-      const uint32_t wd = (k & 4u) ? w23 : w01;
-      const uint32_t byte = INJ ? 0u : (wd >> (16u * (k & 1u) + byte_shift)) & 0xFFu;
-      return make_uint4(off0 + k, byte, __float_as_uint(sel8(Q.g, k)), (uint32_t)code & 0xFFFFu);
+    // queue entry of element off0 + k: its top uniform bytes are bytes 2k
+    // (momentum) and 2k + 1 (preconditioner) of the coarse block, in word k/2
+    const uint32_t cw[4] = {coarse.x, coarse.y, coarse.z, coarse.w};
+    auto entry = [&](uint32_t k, const uint32_t (&codes)[4]) {
+      const uint32_t g = GD == LUMA_GRAD_BF16 ? word_of(W.g, k) : __float_as_uint(sel8(Q.g, k));
+      return make_uint4(off0 + k, INJ ? 0u : word_of(cw, k), g, word_of(codes, k));
     };
     if (qlen_m + tot_m <= (uint32_t)kQueueCapM) {
       uint32_t pos = head_m + qlen_m + (excl & 0xFFFFu);
       for (uint32_t f = fm; f != 0u; f &= f - 1u) {
         const uint32_t k = (uint32_t)__builtin_ctz(f);
-        queue_m[pos++ & (kQueueCapM - 1)] = entry(k, sel8(Q.qm, k), 0u);
+        queue_m[pos++ & (kQueueCapM - 1)] = entry(k, W.qm);
       }
       qlen_m += tot_m;
     } else {
       // more than the queue holds (only when most codes are uncertain): in place
       for (uint32_t f = fm; f != 0u; f &= f - 1u) {
         const uint32_t k = (uint32_t)__builtin_ctz(f);
-        run_m(entry(k, sel8(Q.qm, k), 0u));
+        run_m(entry(k, W.qm));
       }
     }
     if (qlen_w + tot_w <= (uint32_t)kQueueCapW) {
       uint32_t pos = head_w + qlen_w + (excl >> 16);
       for (uint32_t f = fw; f != 0u; f &= f - 1u) {
         const uint32_t k = (uint32_t)__builtin_ctz(f);
-        queue_w[pos++ & (kQueueCapW - 1)] = entry(k, sel8(Q.qw, k), 8u);
+        queue_w[pos++ & (kQueueCapW - 1)] = entry(k, W.qw);
       }
       qlen_w += tot_w;
     } else {
       for (uint32_t f = fw; f != 0u; f &= f - 1u) {
         const uint32_t k = (uint32_t)__builtin_ctz(f);
-        run_w(entry(k, sel8(Q.qw, k), 8u));
+        run_w(entry(k, W.qw));
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -1821,11 +1883,12 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   for (; it < n_whole; ++it) {
     const int64_t e0 = beg + ((int64_t)it * kThreads + threadIdx.x) * kVec;
     Group8 Q;
+    Words4 W;
     U4 coarse{};
     const uint32_t flags = p2_iter<GD, INJ, SMALL, SCALED, true, true>(
-        T, C, e0, kVec, k0, k1, Q, coarse, &stage[(it % kStage) * 64 + lane], acc);
+        T, C, e0, kVec, k0, k1, Q, W, coarse, &stage[(it % kStage) * 64 + lane], acc);
     staged_hi = it + 1;
-    take(e0, flags, Q, coarse);
+    take(e0, flags, Q, W, coarse);
     const int wb = it + 1 - kStage;   // the slot iteration it + 1 will use
     if (wb >= 0) {
       while (qlen_w > 0 && oldest_w() <= wb) batch_w();
@@ -1844,14 +1907,15 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     const int64_t rem = end - e0;
     const int n = rem <= 0 ? 0 : (rem < kVec ? (int)rem : kVec);
     Group8 Q;
+    Words4 W;
     U4 coarse{};
     const uint32_t flags =
         (vec_ok && n == kVec)
-            ? p2_iter<GD, INJ, SMALL, SCALED, true, false>(T, C, e0, n, k0, k1, Q, coarse, nullptr,
-                                                           acc)
-            : p2_iter<GD, INJ, SMALL, SCALED, false, false>(T, C, e0, n, k0, k1, Q, coarse,
+            ? p2_iter<GD, INJ, SMALL, SCALED, true, false>(T, C, e0, n, k0, k1, Q, W, coarse,
+                                                           nullptr, acc)
+            : p2_iter<GD, INJ, SMALL, SCALED, false, false>(T, C, e0, n, k0, k1, Q, W, coarse,
                                                             nullptr, acc);
-    take(e0, flags, Q, coarse);
+    take(e0, flags, Q, W, coarse);
   }
   // The thread's summary word: its largest |Q_m| + margin, its smallest
   // Q_w - margin (clamped to the code ranges).
