@@ -770,6 +770,7 @@ __device__ __forceinline__ uint64_t sr_resolve(int lo, int hi, float a, float z,
 // u < exact_sr_prob(a, z) for a u known exactly; the double expm1 runs only
 // when u falls inside sr_prob_bracket's bracket.  A call, so that the
 // streaming loops keep their registers.
+template <int KTAG>
 __device__ __noinline__ bool sr_below(float a, float z, float u) {
   float pl, ph;
   if (!sr_prob_bracket(a, z, pl, ph)) return u < exact_sr_prob(a, z);
@@ -779,6 +780,7 @@ __device__ __noinline__ bool sr_below(float a, float z, float u) {
 }
 
 // Momentum: the same float32 sequence as exact_mv's m' then exact_quant_m.
+template <int KTAG>
 __device__ __noinline__ uint64_t exact_pair_m(int qm, float g, const LUMA_GLOBAL Grid *old,
                                               const LUMA_GLOBAL Grid *nw, Hyper h, float ulo,
                                               float uhi) {
@@ -792,6 +794,7 @@ __device__ __noinline__ uint64_t exact_pair_m(int qm, float g, const LUMA_GLOBAL
 }
 
 // Preconditioner: exact_mv's v' then exact_quant_w.
+template <int KTAG>
 __device__ __noinline__ uint64_t exact_pair_w(int qw, float g, const LUMA_GLOBAL Grid *old,
                                               const LUMA_GLOBAL Grid *nw, Hyper h, float ulo,
                                               float uhi) {
@@ -1354,15 +1357,28 @@ __device__ __forceinline__ uint32_t wave_scan_incl(uint32_t x) {
   return x;
 }
 
-// a[k] for a per-lane index k in 0..7, as a select tree (no indexed
-// register access).
-template <typename T>
-__device__ __forceinline__ T sel8(const T (&a)[kVec], uint32_t k) {
-  const bool b0 = (k & 1u) != 0, b1 = (k & 2u) != 0, b2 = (k & 4u) != 0;
-  const T x01 = b0 ? a[1] : a[0], x23 = b0 ? a[3] : a[2];
-  const T x45 = b0 ? a[5] : a[4], x67 = b0 ? a[7] : a[6];
-  const T y03 = b1 ? x23 : x01, y47 = b1 ? x67 : x45;
-  return b2 ? y47 : y03;
+// Per-lane selects by the bits of an index.  v_cndmask_b32 issues at about
+// a fifth of the rate of plain VALU on gfx950 (0.21 vs 0.96-1.3 wave
+// instructions per clock per CU), so a select is a v_bfi_b32 with an
+// all-ones / all-zeros mask: bit b of k sign-extended by v_bfe_i32.  The
+// empty asm keeps the compiler from turning the mask back into a compare
+// and v_cndmask.
+__device__ __forceinline__ uint32_t bit_mask(uint32_t k, int b) {
+  uint32_t m = (uint32_t)__builtin_amdgcn_sbfe((int)k, b, 1);
+  asm("" : "+v"(m));
+  return m;
+}
+
+__device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) {
+  return (a & m) | (b & ~m);   // m ? a : b, bitwise
+}
+
+// a[k] for a per-lane index k in 0..7 (no indexed register access).
+__device__ __forceinline__ uint32_t sel8(const uint32_t (&a)[kVec], uint32_t k) {
+  const uint32_t m0 = bit_mask(k, 0), m1 = bit_mask(k, 1), m2 = bit_mask(k, 2);
+  const uint32_t x01 = bfi(m0, a[1], a[0]), x23 = bfi(m0, a[3], a[2]);
+  const uint32_t x45 = bfi(m0, a[5], a[4]), x67 = bfi(m0, a[7], a[6]);
+  return bfi(m2, bfi(m1, x67, x45), bfi(m1, x23, x01));
 }
 
 // The packed 32-bit words of a group of 8 elements, two 16-bit values per
@@ -1373,11 +1389,9 @@ struct Words4 {
   uint32_t g[4];    // 16-bit gradients after unscaling (bfloat16 only)
 };
 
-// a[k >> 1] for a per-lane k in 0..7 (two selects per level).
-__device__ __forceinline__ uint32_t word_of(const uint32_t (&a)[4], uint32_t k) {
-  const bool b1 = (k & 2u) != 0, b2 = (k & 4u) != 0;
-  const uint32_t x01 = b1 ? a[1] : a[0], x23 = b1 ? a[3] : a[2];
-  return b2 ? x23 : x01;
+// a[k >> 1] for a per-lane k in 0..7; m1, m2: bit_mask(k, 1), bit_mask(k, 2).
+__device__ __forceinline__ uint32_t word_of(const uint32_t (&a)[4], uint32_t m1, uint32_t m2) {
+  return bfi(m2, bfi(m1, a[3], a[2]), bfi(m1, a[1], a[0]));
 }
 
 __device__ __forceinline__ uint32_t pack_lo16(uint32_t hi, uint32_t lo) {
@@ -1422,16 +1436,16 @@ struct P2Const {
   uint32_t sign;            // 0x80000000
 };
 
-// Moves every constant of the loop into VGPRs (see in_vgpr).
+// Moves the constants of the loop's dual-issued instructions into VGPRs (see
+// in_vgpr).  Those read only by single-issued or half-rate instructions
+// (v_med3, v_and_or, v_mad_u64_u32: the clamp bounds, the sign mask, the
+// Philox multipliers) and the Philox key, whose ten round keys would hold ten
+// VGPR pairs, stay in SGPRs: the VGPRs go to the next iteration's loads.
 __device__ __forceinline__ void launder(P2Const &C) {
   C.D.dm = in_vgpr(C.D.dm);
   C.D.dw = in_vgpr(C.D.dw);
   C.D.iwmin = in_vgpr(C.D.iwmin);
   C.D.eps = in_vgpr(C.D.eps);
-  C.pk0 = in_vgpr(C.pk0);
-  C.pk1 = in_vgpr(C.pk1);
-  C.pm0 = in_vgpr(C.pm0);
-  C.pm1 = in_vgpr(C.pm1);
   C.b1 = in_vgpr(C.b1);
   C.omb1 = in_vgpr(C.omb1);
   C.b2 = in_vgpr(C.b2);
@@ -1447,14 +1461,12 @@ __device__ __forceinline__ void launder(P2Const &C) {
   C.cl = in_vgpr(C.cl);
   C.wmin_n = in_vgpr(C.wmin_n);
   C.we = in_vgpr(C.we);
-  C.xmin = in_vgpr(C.xmin);
   C.zoff = in_vgpr(C.zoff);
   C.k1 = in_vgpr(C.k1);
   C.k2 = in_vgpr(C.k2);
   C.k3 = in_vgpr(C.k3);
   C.k7 = in_vgpr(C.k7);
   C.k8 = in_vgpr(C.k8);
-  C.kmax_m = in_vgpr(C.kmax_m);
   C.ndw = in_vgpr(C.ndw);
   C.nbias = in_vgpr(C.nbias);
   C.nk1 = in_vgpr(C.nk1);
@@ -1462,9 +1474,7 @@ __device__ __forceinline__ void launder(P2Const &C) {
   C.hk3 = in_vgpr(C.hk3);
   C.nk7 = in_vgpr(C.nk7);
   C.hk8 = in_vgpr(C.hk8);
-  C.kmax_w = in_vgpr(C.kmax_w);
   C.inv = in_vgpr(C.inv);
-  C.sign = in_vgpr(C.sign);
 }
 
 // One iteration of 8 consecutive elements.  FULL: all 8 valid and 16-byte
@@ -1510,21 +1520,36 @@ __device__ __forceinline__ void acc_codes(CodeAcc &acc, vu4 a, vu4 b) {
 
 // acc: folds in the codes the fast path stores for the lane's valid
 // elements (the code summaries widen them by the decision margin).
+// The 16-byte vectors one whole group reads: old codes, gradients (g1:
+// float32 only) and parameters.
+struct P2Raw {
+  Raw8 r;
+  vf4 p0, p1;
+};
+
+template <int GD>
+__device__ __forceinline__ void load_p2raw(const Tensor &T, int64_t e0, P2Raw &R) {
+  R.r.qm = *(const LUMA_GLOBAL vu4 *)(T.q_m + e0);
+  R.r.qw = load_stream((const LUMA_GLOBAL vu4 *)(T.q_w + e0));
+  if (GD == LUMA_GRAD_F32) {
+    R.r.g0 = load_stream((const LUMA_GLOBAL vu4 *)((const LUMA_GLOBAL float *)T.grad + e0));
+    R.r.g1 = load_stream((const LUMA_GLOBAL vu4 *)((const LUMA_GLOBAL float *)T.grad + e0 + 4));
+  } else {
+    R.r.g0 = load_stream((const LUMA_GLOBAL vu4 *)((const LUMA_GLOBAL uint16_t *)T.grad + e0));
+  }
+  R.p0 = load_stream((const LUMA_GLOBAL vf4 *)(T.param + e0));
+  R.p1 = load_stream((const LUMA_GLOBAL vf4 *)(T.param + e0 + 4));
+}
+
 // W: the words of the old codes and (bfloat16) gradients, for the queues.
+// FULL: the group's vectors are in RW (load_p2raw); otherwise it loads its
+// n valid elements itself.
 template <int GD, bool INJ, bool SMALL, bool SCALED, bool FULL, bool STAGE>
 __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, int64_t e0, int n,
-                                            uint32_t k0, uint32_t k1, Group8 &Q, Words4 &W,
-                                            U4 &coarse, uint4 *stage, CodeAcc &acc) {
+                                            const P2Raw &RW, uint32_t k0, uint32_t k1, Group8 &Q,
+                                            Words4 &W, U4 &coarse, uint4 *stage, CodeAcc &acc) {
   if (FULL) {
-    Raw8 R;
-    R.qm = *(const LUMA_GLOBAL vu4 *)(T.q_m + e0);
-    R.qw = load_stream((const LUMA_GLOBAL vu4 *)(T.q_w + e0));
-    if (GD == LUMA_GRAD_F32) {
-      R.g0 = load_stream((const LUMA_GLOBAL vu4 *)((const LUMA_GLOBAL float *)T.grad + e0));
-      R.g1 = load_stream((const LUMA_GLOBAL vu4 *)((const LUMA_GLOBAL float *)T.grad + e0 + 4));
-    } else {
-      R.g0 = load_stream((const LUMA_GLOBAL vu4 *)((const LUMA_GLOBAL uint16_t *)T.grad + e0));
-    }
+    const Raw8 &R = RW.r;
     unpack_raw<GD>(R, Q);
     W.qm[0] = R.qm.x; W.qm[1] = R.qm.y; W.qm[2] = R.qm.z; W.qm[3] = R.qm.w;
     W.qw[0] = R.qw.x; W.qw[1] = R.qw.y; W.qw[2] = R.qw.z; W.qw[3] = R.qw.w;
@@ -1548,10 +1573,8 @@ __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, i
   }
   float p[kVec];
   if (FULL) {
-    const vf4 p0 = load_stream((const LUMA_GLOBAL vf4 *)(T.param + e0));
-    const vf4 p1 = load_stream((const LUMA_GLOBAL vf4 *)(T.param + e0 + 4));
-    p[0] = p0.x; p[1] = p0.y; p[2] = p0.z; p[3] = p0.w;
-    p[4] = p1.x; p[5] = p1.y; p[6] = p1.z; p[7] = p1.w;
+    p[0] = RW.p0.x; p[1] = RW.p0.y; p[2] = RW.p0.z; p[3] = RW.p0.w;
+    p[4] = RW.p1.x; p[5] = RW.p1.y; p[6] = RW.p1.z; p[7] = RW.p1.w;
   } else {
 #pragma unroll
     for (int j = 0; j < kVec; ++j) p[j] = j < n ? T.param[e0 + j] : 0.0f;
@@ -1657,7 +1680,7 @@ __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, i
   return flags;
 }
 
-template <int GD, bool INJ, bool SMALL, bool SCALED>
+template <int GD, bool INJ, bool SMALL, bool SCALED, int KTAG>
 __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOBAL Grid *old,
                                 const LUMA_GLOBAL Grid *nw, float inv, int64_t ci, int64_t beg,
                                 int64_t end, uint32_t k0, uint32_t k1, uint4 *queue) {
@@ -1741,7 +1764,7 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     if (c.lo == c.hi) return c.lo;
     const U4 fine = philox_fine_block((uint64_t)i, pb, k0, k1);
     const float u = (float)((top << 16) | u4_half(fine, 2 * (int)(i & 3) + which)) * 0x1p-24f;
-    return sr_below(c.a, z, u) ? c.hi : c.lo;
+    return sr_below<KTAG>(c.a, z, u) ? c.hi : c.lo;
   };
   // The interval of an entry's uniform: the injected u itself, or (Philox)
   // the interval of its top byte.
@@ -1765,7 +1788,7 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     const int64_t i = beg + ent.x;
     const uint32_t sh = (ent.x & 1u) << 4;
     const uint32_t top = INJ ? 0u : (ent.y >> sh) & 0xFFu;
-    const CodePair c = unpack_pair(exact_pair_m((int)(int16_t)(ent.w >> sh), ent_grad(ent, sh),
+    const CodePair c = unpack_pair(exact_pair_m<KTAG>((int)(int16_t)(ent.w >> sh), ent_grad(ent, sh),
                                                 old, nw, h, u_lo(top, T.u_m, i),
                                                 u_hi(top, T.u_m, i)));
     T.q_m[i] = (int16_t)draw(c, zm_new, i, top, 0);
@@ -1775,7 +1798,7 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     const int64_t i = beg + o;
     const uint32_t sh = (o & 1u) << 4;
     const uint32_t top = INJ ? 0u : (ent.y >> (sh + 8u)) & 0xFFu;
-    const CodePair c = unpack_pair(exact_pair_w((int)((ent.w >> sh) & 0xFFFFu), ent_grad(ent, sh),
+    const CodePair c = unpack_pair(exact_pair_w<KTAG>((int)((ent.w >> sh) & 0xFFFFu), ent_grad(ent, sh),
                                                 old, nw, h, u_lo(top, T.u_w, i),
                                                 u_hi(top, T.u_w, i)));
     const uint16_t code = (uint16_t)draw(c, zw_new, i, top, 1);
@@ -1805,8 +1828,17 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     // (momentum) and 2k + 1 (preconditioner) of the coarse block, in word k/2
     const uint32_t cw[4] = {coarse.x, coarse.y, coarse.z, coarse.w};
     auto entry = [&](uint32_t k, const uint32_t (&codes)[4]) {
-      const uint32_t g = GD == LUMA_GRAD_BF16 ? word_of(W.g, k) : __float_as_uint(sel8(Q.g, k));
-      return make_uint4(off0 + k, INJ ? 0u : word_of(cw, k), g, word_of(codes, k));
+      const uint32_t m1 = bit_mask(k, 1), m2 = bit_mask(k, 2);
+      uint32_t g;
+      if (GD == LUMA_GRAD_BF16) {
+        g = word_of(W.g, m1, m2);
+      } else {
+        uint32_t gb[kVec];
+#pragma unroll
+        for (int j = 0; j < kVec; ++j) gb[j] = __float_as_uint(Q.g[j]);
+        g = sel8(gb, k);
+      }
+      return make_uint4(off0 + k, INJ ? 0u : word_of(cw, m1, m2), g, word_of(codes, m1, m2));
     };
     if (qlen_m + tot_m <= (uint32_t)kQueueCapM) {
       uint32_t pos = head_m + qlen_m + (excl & 0xFFFFu);
@@ -1879,22 +1911,41 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   // preconditioner codes; before a slot is reused, the iteration it holds has
   // its queued entries run and is written back.
   const int n_whole = vec_ok ? (int)((end - beg) / kStride) : 0;
-  int it = 0;
-  for (; it < n_whole; ++it) {
-    const int64_t e0 = beg + ((int64_t)it * kThreads + threadIdx.x) * kVec;
+  // Each iteration's vectors are loaded one iteration ahead, into two
+  // buffers in a loop unrolled by two (copying a buffer whose loads are in
+  // flight would make the copy wait for them); past the last whole group the
+  // loads repeat the last group, and are not used.
+  auto group_at = [&](int j) {
+    return beg + ((int64_t)(j < n_whole ? j : n_whole - 1) * kThreads + threadIdx.x) * kVec;
+  };
+  auto whole_iter = [&](const P2Raw &R, int j) {
+    const int64_t e0 = group_at(j);
     Group8 Q;
     Words4 W;
     U4 coarse{};
     const uint32_t flags = p2_iter<GD, INJ, SMALL, SCALED, true, true>(
-        T, C, e0, kVec, k0, k1, Q, W, coarse, &stage[(it % kStage) * 64 + lane], acc);
-    staged_hi = it + 1;
+        T, C, e0, kVec, R, k0, k1, Q, W, coarse, &stage[(j % kStage) * 64 + lane], acc);
+    staged_hi = j + 1;
     take(e0, flags, Q, W, coarse);
-    const int wb = it + 1 - kStage;   // the slot iteration it + 1 will use
+    const int wb = j + 1 - kStage;   // the slot iteration j + 1 will use
     if (wb >= 0) {
       while (qlen_w > 0 && oldest_w() <= wb) batch_w();
       write_back(wb);
       staged_lo = wb + 1;
     }
+  };
+  int it = 0;
+  if (n_whole > 0) {
+    P2Raw ra, rb;
+    load_p2raw<GD>(T, group_at(0), ra);
+    for (; it < n_whole; it += 2) {
+      load_p2raw<GD>(T, group_at(it + 1), rb);
+      whole_iter(ra, it);
+      if (it + 1 >= n_whole) break;
+      load_p2raw<GD>(T, group_at(it + 2), ra);
+      whole_iter(rb, it + 1);
+    }
+    it = n_whole;
   }
   // drain the staged iterations
   while (qlen_w > 0) batch_w();
@@ -1909,12 +1960,14 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     Group8 Q;
     Words4 W;
     U4 coarse{};
+    P2Raw R;
+    const bool whole = vec_ok && n == kVec;
+    if (whole) load_p2raw<GD>(T, e0, R);
     const uint32_t flags =
-        (vec_ok && n == kVec)
-            ? p2_iter<GD, INJ, SMALL, SCALED, true, false>(T, C, e0, n, k0, k1, Q, W, coarse,
-                                                           nullptr, acc)
-            : p2_iter<GD, INJ, SMALL, SCALED, false, false>(T, C, e0, n, k0, k1, Q, W, coarse,
-                                                            nullptr, acc);
+        whole ? p2_iter<GD, INJ, SMALL, SCALED, true, false>(T, C, e0, n, R, k0, k1, Q, W, coarse,
+                                                             nullptr, acc)
+              : p2_iter<GD, INJ, SMALL, SCALED, false, false>(T, C, e0, n, R, k0, k1, Q, W,
+                                                              coarse, nullptr, acc);
     take(e0, flags, Q, W, coarse);
   }
   // The thread's summary word: its largest |Q_m| + margin, its smallest
@@ -1931,35 +1984,43 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   if (lane < qlen_w) run_w(queue_w[(head_w + lane) & (kQueueCapW - 1)]);
 }
 
-template <int GD, bool SCALED>
+template <int GD, bool SCALED, bool INJ_OK>
 __device__ __forceinline__ void pass2_dispatch_s(const Tensor &T, const Hyper &h,
                                                  const LUMA_GLOBAL Grid *old,
                                                  const LUMA_GLOBAL Grid *nw, float inv, int64_t ci,
                                                  int64_t beg, int64_t end, uint32_t k0,
                                                  uint32_t k1, bool inj, bool small, uint4 *q) {
-  if (inj) {
+  if (INJ_OK && inj) {
     if (small)
-      pass2_fast_body<GD, true, true, SCALED>(T, h, old, nw, inv, ci, beg, end, k0, k1, q);
+      pass2_fast_body<GD, true, true, SCALED, INJ_OK>(T, h, old, nw, inv, ci, beg, end, k0, k1, q);
     else
-      pass2_fast_body<GD, true, false, SCALED>(T, h, old, nw, inv, ci, beg, end, k0, k1, q);
+      pass2_fast_body<GD, true, false, SCALED, INJ_OK>(T, h, old, nw, inv, ci, beg, end, k0, k1, q);
   } else {
     if (small)
-      pass2_fast_body<GD, false, true, SCALED>(T, h, old, nw, inv, ci, beg, end, k0, k1, q);
+      pass2_fast_body<GD, false, true, SCALED, INJ_OK>(T, h, old, nw, inv, ci, beg, end, k0, k1, q);
     else
-      pass2_fast_body<GD, false, false, SCALED>(T, h, old, nw, inv, ci, beg, end, k0, k1, q);
+      pass2_fast_body<GD, false, false, SCALED, INJ_OK>(T, h, old, nw, inv, ci, beg, end, k0, k1, q);
   }
 }
 
-template <int GD>
+template <int GD, bool INJ_OK>
 __device__ __forceinline__ void pass2_dispatch(const Tensor &T, const Hyper &h,
                                                const LUMA_GLOBAL Grid *old,
                                                const LUMA_GLOBAL Grid *nw, float inv, bool scaled,
                                                int64_t ci, int64_t beg, int64_t end, uint32_t k0,
                                                uint32_t k1, bool inj, bool small, uint4 *q) {
-  if (scaled) pass2_dispatch_s<GD, true>(T, h, old, nw, inv, ci, beg, end, k0, k1, inj, small, q);
-  else pass2_dispatch_s<GD, false>(T, h, old, nw, inv, ci, beg, end, k0, k1, inj, small, q);
+  if (scaled)
+    pass2_dispatch_s<GD, true, INJ_OK>(T, h, old, nw, inv, ci, beg, end, k0, k1, inj, small, q);
+  else
+    pass2_dispatch_s<GD, false, INJ_OK>(T, h, old, nw, inv, ci, beg, end, k0, k1, inj, small, q);
 }
 
+// INJ_OK: a launch with injected uniforms.  Philox launches use the kernel
+// without the injected-uniform paths: compiled together with them, the
+// kernel's register allocation (the largest over every path it holds) goes
+// from 167 VGPRs to 248 and spills, which would halve the occupancy of the
+// Philox paths.
+template <bool INJ_OK>
 __global__ __launch_bounds__(kThreads) void pass2_fast_kernel(StepSrc src, uint64_t base_seed,
                                                               int noise_mode) {
   if (skip_step(src)) return;
@@ -1983,11 +2044,14 @@ __global__ __launch_bounds__(kThreads) void pass2_fast_kernel(StepSrc src, uint6
   __shared__ uint4 qbuf[kThreads / 64][kQueueCapM + kQueueCapW + kStage * 64];
   uint4 *q = qbuf[threadIdx.x >> 6];
   if (T.grad_dtype == LUMA_GRAD_BF16)
-    pass2_dispatch<LUMA_GRAD_BF16>(T, h, old, nw, inv, scaled, ci, beg, end, k0, k1, inj, small, q);
+    pass2_dispatch<LUMA_GRAD_BF16, INJ_OK>(T, h, old, nw, inv, scaled, ci, beg, end, k0, k1, inj,
+                                           small, q);
   else if (T.grad_dtype == LUMA_GRAD_F16)
-    pass2_dispatch<LUMA_GRAD_F16>(T, h, old, nw, inv, scaled, ci, beg, end, k0, k1, inj, small, q);
+    pass2_dispatch<LUMA_GRAD_F16, INJ_OK>(T, h, old, nw, inv, scaled, ci, beg, end, k0, k1, inj,
+                                          small, q);
   else
-    pass2_dispatch<LUMA_GRAD_F32>(T, h, old, nw, inv, scaled, ci, beg, end, k0, k1, inj, small, q);
+    pass2_dispatch<LUMA_GRAD_F32, INJ_OK>(T, h, old, nw, inv, scaled, ci, beg, end, k0, k1, inj,
+                                          small, q);
 }
 
 // ---------------------------------------------------------------------------
@@ -2236,9 +2300,12 @@ static int launch_step(StepSrc src, int32_t n_tensors, int32_t n_chunks, float *
     if (exact)
       hipLaunchKernelGGL(pass2_exact_kernel, dim3(n_big), dim3(kThreads), 0, s, src, base_seed,
                          (int)noise_mode);
+    else if (noise_mode == LUMA_NOISE_INJECTED)
+      hipLaunchKernelGGL(pass2_fast_kernel<true>, dim3(n_big), dim3(kThreads), 0, s, src,
+                         base_seed, (int)noise_mode);
     else
-      hipLaunchKernelGGL(pass2_fast_kernel, dim3(n_big), dim3(kThreads), 0, s, src, base_seed,
-                         (int)noise_mode);
+      hipLaunchKernelGGL(pass2_fast_kernel<false>, dim3(n_big), dim3(kThreads), 0, s, src,
+                         base_seed, (int)noise_mode);
     if (int r = check_launch("luma_step: pass 2 launch")) return r;
   }
   if (small_blocks > 0) {
