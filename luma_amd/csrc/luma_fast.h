@@ -136,6 +136,50 @@ __device__ __forceinline__ float fast_log1p_relerr(float a_top) {
   return a_top <= kSmall ? 3.0f * kU : 10.0f * kU;
 }
 
+// Momentum regimes of a tensor's fast path, from its largest decode argument
+// x_top = 32767 dm (old grid) and its largest |m'|, S_m (new scale):
+//   kRegSmall    x_top <= 1/8 and S_m <= 1/8: the minimax polynomials;
+//   kRegMedium   x_top < 1/2 and S_m <= 1/2: the general functions' first
+//                branches alone (the Taylor expm1 and the atanh series), the
+//                ones the general functions pick for every argument below
+//                1/2 -- the same values without the second branch, its
+//                transcendentals and the per-element select;
+//   kRegGeneral  both branches and a select per element.
+// The error bounds are the general ones (fast_*_relerr of x_top and S_m).
+// The atanh series stays within them for arguments somewhat above 1/2
+// (its truncation at s <= 0.2: below 0.02u), which covers a fast |m'| a few
+// ulp above S_m.
+constexpr int kRegSmall = 0, kRegMedium = 1, kRegGeneral = 2;
+constexpr float kMedium = 0.5f;
+
+template <int REG>
+__device__ __forceinline__ float fast_expm1(float x) {
+  if (REG == kRegSmall) return fast_expm1_small(x);
+  if (REG == kRegGeneral) return fast_expm1_general(x);
+  float p = fmaf(x, 1.0f / 40320.0f, 1.0f / 5040.0f);
+  p = fmaf(x, p, 1.0f / 720.0f);
+  p = fmaf(x, p, 1.0f / 120.0f);
+  p = fmaf(x, p, 1.0f / 24.0f);
+  p = fmaf(x, p, 1.0f / 6.0f);
+  p = fmaf(x, p, 0.5f);
+  p = fmaf(x, p, 1.0f);
+  return x * p;
+}
+
+template <int REG>
+__device__ __forceinline__ float fast_log1p(float a) {
+  if (REG == kRegSmall) return fast_log1p_small(a);
+  if (REG == kRegGeneral) return fast_log1p_general(a);
+  const float s = a * __builtin_amdgcn_rcpf(2.0f + a);
+  const float s2 = s * s;
+  float c = fmaf(s2, 2.0f / 11.0f, 2.0f / 9.0f);
+  c = fmaf(s2, c, 2.0f / 7.0f);
+  c = fmaf(s2, c, 2.0f / 5.0f);
+  c = fmaf(s2, c, 2.0f / 3.0f);
+  c = fmaf(s2, c, 2.0f);
+  return s * c;
+}
+
 // Fast decode + EMA of one element (functional.py:113-126, 269-275).
 // m-decode argument x = |q| * dm is formed exactly as on the exact path.
 struct FastEma {
@@ -154,14 +198,14 @@ struct FastEma {
 // PRECISE_V: form e^-x with the two-word argument reduction (pass 2, whose
 // parameter update and code bounds use v'); pass 1 only needs the cheaper
 // single exp2, whose error its max-tracking bound covers (x * u term).
-template <bool SMALL_M, bool PRECISE_V>
+template <int REG_M, bool PRECISE_V>
 __device__ __forceinline__ FastEma fast_ema(int qm, int qw, float g, float dm, float ndw,
                                             float nbias, float iwmin, float eps, float b1, float omb1,
                                             float b2, float omb2, uint32_t sign) {
   FastEma r;
   const float qf = (float)qm;
   const float x = fabsf(qf) * dm;
-  const float e = SMALL_M ? fast_expm1_small(x) : fast_expm1_general(x);
+  const float e = fast_expm1<REG_M>(x);
   const float m = __uint_as_float(__float_as_uint(e) | (__float_as_uint(qf) & sign));
   r.am = e;
   const float nx = fmaf(__int_as_float(qw), ndw, nbias);

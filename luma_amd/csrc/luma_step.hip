@@ -918,7 +918,7 @@ __device__ __forceinline__ void unscale_group(Group8 &G, float inv) {
 template <bool SMALL>
 __device__ __forceinline__ bool p1_reach(int qa, int qw_lo, uint32_t gb, const P1Const &K,
                                          uint32_t Tm, uint32_t Tv) {
-  const FastEma fb = fast_ema<SMALL, false>(qa, qw_lo, __uint_as_float(gb), K.dm, K.ndw, K.nbias,
+  const FastEma fb = fast_ema<SMALL ? kRegSmall : kRegGeneral, false>(qa, qw_lo, __uint_as_float(gb), K.dm, K.ndw, K.nbias,
                                             K.iwmin, K.eps, K.b1, K.omb1, K.b2, K.omb2, K.sign);
   const uint32_t um = __float_as_uint(fb.mn * K.up_m) & 0x7FFFFFFFu;
   const uint32_t uv = __float_as_uint(fmaf(fb.vn, K.up_v, K.abs_v)) & 0x7FFFFFFFu;
@@ -989,7 +989,7 @@ __device__ __forceinline__ void p1_compute(const Group8 &G, const P1Const &K, in
   }
 #pragma unroll
   for (int j = 0; j < kVec; ++j) {
-    const FastEma f = fast_ema<SMALL, false>(G.qm[j], G.qw[j], G.g[j], K.dm, K.ndw, K.nbias, K.iwmin,
+    const FastEma f = fast_ema<SMALL ? kRegSmall : kRegGeneral, false>(G.qm[j], G.qw[j], G.g[j], K.dm, K.ndw, K.nbias, K.iwmin,
                                              K.eps, K.b1, K.omb1, K.b2, K.omb2, K.sign);
     am[j] = __float_as_uint(f.mn) & 0x7FFFFFFFu;
     av[j] = __float_as_uint(f.vn) & 0x7FFFFFFFu;
@@ -1174,7 +1174,7 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     // bound; each iteration then bounds with the lane's largest |g| alone.
     static_assert(LUMA_SUMMARY_WORDS == kThreads, "one summary word per thread of a chunk");
     const uint32_t sw = T.summary[ci * LUMA_SUMMARY_WORDS + threadIdx.x];
-    const FastEma d = fast_ema<SMALL, false>((int)(sw & 0xFFFFu), (int)(kCodeFloat | (sw >> 16)),
+    const FastEma d = fast_ema<SMALL ? kRegSmall : kRegGeneral, false>((int)(sw & 0xFFFFu), (int)(kCodeFloat | (sw >> 16)),
                                              0.0f, K.dm, K.ndw, K.nbias, K.iwmin, K.eps, K.b1,
                                              K.omb1, K.b2, K.omb2, K.sign);
     // One iteration on the gradients `cur` of group j: the bound at the
@@ -1544,7 +1544,7 @@ __device__ __forceinline__ void load_p2raw(const Tensor &T, int64_t e0, P2Raw &R
 // W: the words of the old codes and (bfloat16) gradients, for the queues.
 // FULL: the group's vectors are in RW (load_p2raw); otherwise it loads its
 // n valid elements itself.
-template <int GD, bool INJ, bool SMALL, bool SCALED, bool FULL, bool STAGE>
+template <int GD, bool INJ, int REG, bool SCALED, bool FULL, bool STAGE>
 __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, int64_t e0, int n,
                                             const P2Raw &RW, uint32_t k0, uint32_t k1, Group8 &Q,
                                             Words4 &W, U4 &coarse, uint4 *stage, CodeAcc &acc) {
@@ -1601,7 +1601,7 @@ __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, i
   uint32_t flags = 0;
 #pragma unroll
   for (int j = 0; j < kVec; ++j) {
-    const FastEma f = fast_ema<SMALL, true>(Q.qm[j], Q.qw[j], Q.g[j], C.D.dm, C.ndw, C.nbias, C.D.iwmin,
+    const FastEma f = fast_ema<REG, true>(Q.qm[j], Q.qw[j], Q.g[j], C.D.dm, C.ndw, C.nbias, C.D.iwmin,
                                             C.D.eps, C.b1, C.omb1, C.b2, C.omb2, C.sign);
     const float s = __builtin_amdgcn_sqrtf(f.vn);
     // AdamW update (functional.py:278-279), within 1e-6 of the exact path:
@@ -1611,7 +1611,7 @@ __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, i
     // momentum code: z = log1p(|m'|)/dm + offset.  |m'| <= S_m' exactly, so
     // the exact path's clamp is inactive; the code's sign is m''s.
     const float am = in_vgpr(fabsf(f.mn));   // one v_and, not an |.| modifier per fma
-    const float L = SMALL ? fast_log1p_small(am) : fast_log1p_general(am);
+    const float L = fast_log1p<REG>(am);
     const float zm = fmaf(L, C.idm, zmu_m[j]);
     const float hm = fmaf(f.am, C.nk1, fmaf(zm, C.nk2, C.hk3));    // 0.5 - e
     // floor(z) as z - fract(z) (exact for |z| < 2^23; v_fract is needed for
@@ -1680,7 +1680,7 @@ __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, i
   return flags;
 }
 
-template <int GD, bool INJ, bool SMALL, bool SCALED, int KTAG>
+template <int GD, bool INJ, int REG, bool SCALED, int KTAG>
 __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOBAL Grid *old,
                                 const LUMA_GLOBAL Grid *nw, float inv, int64_t ci, int64_t beg,
                                 int64_t end, uint32_t k0, uint32_t k1, uint4 *queue) {
@@ -1923,7 +1923,7 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     Group8 Q;
     Words4 W;
     U4 coarse{};
-    const uint32_t flags = p2_iter<GD, INJ, SMALL, SCALED, true, true>(
+    const uint32_t flags = p2_iter<GD, INJ, REG, SCALED, true, true>(
         T, C, e0, kVec, R, k0, k1, Q, W, coarse, &stage[(j % kStage) * 64 + lane], acc);
     staged_hi = j + 1;
     take(e0, flags, Q, W, coarse);
@@ -1964,9 +1964,9 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     const bool whole = vec_ok && n == kVec;
     if (whole) load_p2raw<GD>(T, e0, R);
     const uint32_t flags =
-        whole ? p2_iter<GD, INJ, SMALL, SCALED, true, false>(T, C, e0, n, R, k0, k1, Q, W, coarse,
+        whole ? p2_iter<GD, INJ, REG, SCALED, true, false>(T, C, e0, n, R, k0, k1, Q, W, coarse,
                                                              nullptr, acc)
-              : p2_iter<GD, INJ, SMALL, SCALED, false, false>(T, C, e0, n, R, k0, k1, Q, W,
+              : p2_iter<GD, INJ, REG, SCALED, false, false>(T, C, e0, n, R, k0, k1, Q, W,
                                                               coarse, nullptr, acc);
     take(e0, flags, Q, W, coarse);
   }
@@ -1984,23 +1984,31 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   if (lane < qlen_w) run_w(queue_w[(head_w + lane) & (kQueueCapW - 1)]);
 }
 
+template <int GD, bool SCALED, bool INJ_OK, bool INJ>
+__device__ __forceinline__ void pass2_dispatch_r(const Tensor &T, const Hyper &h,
+                                                 const LUMA_GLOBAL Grid *old,
+                                                 const LUMA_GLOBAL Grid *nw, float inv, int64_t ci,
+                                                 int64_t beg, int64_t end, uint32_t k0,
+                                                 uint32_t k1, int reg, uint4 *q) {
+  if (reg == kRegSmall)
+    pass2_fast_body<GD, INJ, kRegSmall, SCALED, INJ_OK>(T, h, old, nw, inv, ci, beg, end, k0, k1, q);
+  else if (reg == kRegMedium)
+    pass2_fast_body<GD, INJ, kRegMedium, SCALED, INJ_OK>(T, h, old, nw, inv, ci, beg, end, k0, k1, q);
+  else
+    pass2_fast_body<GD, INJ, kRegGeneral, SCALED, INJ_OK>(T, h, old, nw, inv, ci, beg, end, k0, k1,
+                                                          q);
+}
+
 template <int GD, bool SCALED, bool INJ_OK>
 __device__ __forceinline__ void pass2_dispatch_s(const Tensor &T, const Hyper &h,
                                                  const LUMA_GLOBAL Grid *old,
                                                  const LUMA_GLOBAL Grid *nw, float inv, int64_t ci,
                                                  int64_t beg, int64_t end, uint32_t k0,
-                                                 uint32_t k1, bool inj, bool small, uint4 *q) {
-  if (INJ_OK && inj) {
-    if (small)
-      pass2_fast_body<GD, true, true, SCALED, INJ_OK>(T, h, old, nw, inv, ci, beg, end, k0, k1, q);
-    else
-      pass2_fast_body<GD, true, false, SCALED, INJ_OK>(T, h, old, nw, inv, ci, beg, end, k0, k1, q);
-  } else {
-    if (small)
-      pass2_fast_body<GD, false, true, SCALED, INJ_OK>(T, h, old, nw, inv, ci, beg, end, k0, k1, q);
-    else
-      pass2_fast_body<GD, false, false, SCALED, INJ_OK>(T, h, old, nw, inv, ci, beg, end, k0, k1, q);
-  }
+                                                 uint32_t k1, bool inj, int reg, uint4 *q) {
+  if (INJ_OK && inj)
+    pass2_dispatch_r<GD, SCALED, INJ_OK, true>(T, h, old, nw, inv, ci, beg, end, k0, k1, reg, q);
+  else
+    pass2_dispatch_r<GD, SCALED, INJ_OK, false>(T, h, old, nw, inv, ci, beg, end, k0, k1, reg, q);
 }
 
 template <int GD, bool INJ_OK>
@@ -2008,11 +2016,11 @@ __device__ __forceinline__ void pass2_dispatch(const Tensor &T, const Hyper &h,
                                                const LUMA_GLOBAL Grid *old,
                                                const LUMA_GLOBAL Grid *nw, float inv, bool scaled,
                                                int64_t ci, int64_t beg, int64_t end, uint32_t k0,
-                                               uint32_t k1, bool inj, bool small, uint4 *q) {
+                                               uint32_t k1, bool inj, int reg, uint4 *q) {
   if (scaled)
-    pass2_dispatch_s<GD, true, INJ_OK>(T, h, old, nw, inv, ci, beg, end, k0, k1, inj, small, q);
+    pass2_dispatch_s<GD, true, INJ_OK>(T, h, old, nw, inv, ci, beg, end, k0, k1, inj, reg, q);
   else
-    pass2_dispatch_s<GD, false, INJ_OK>(T, h, old, nw, inv, ci, beg, end, k0, k1, inj, small, q);
+    pass2_dispatch_s<GD, false, INJ_OK>(T, h, old, nw, inv, ci, beg, end, k0, k1, inj, reg, q);
 }
 
 // INJ_OK: a launch with injected uniforms.  Philox launches use the kernel
@@ -2038,20 +2046,24 @@ __global__ __launch_bounds__(kThreads) void pass2_fast_kernel(StepSrc src, uint6
   uint32_t k0, k1;
   step_key(base_seed, t, T.param_id, k0, k1);
   const bool inj = injected(T, noise_mode);
-  const bool small = (old == nullptr || old->fast[kXTopM] <= kSmall) && nw->sm <= kSmall;
+  // momentum regime (see luma_fast.h): old grid's decode range, new scale
+  const float x_top = old == nullptr ? 0.0f : old->fast[kXTopM];
+  const int reg = (x_top <= kSmall && nw->sm <= kSmall)  ? kRegSmall
+                  : (x_top < kMedium && nw->sm <= kMedium) ? kRegMedium
+                                                           : kRegGeneral;
   const bool scaled = src.scaling.grad_scale != nullptr;
   const float inv = inv_scale(src);
   __shared__ uint4 qbuf[kThreads / 64][kQueueCapM + kQueueCapW + kStage * 64];
   uint4 *q = qbuf[threadIdx.x >> 6];
   if (T.grad_dtype == LUMA_GRAD_BF16)
     pass2_dispatch<LUMA_GRAD_BF16, INJ_OK>(T, h, old, nw, inv, scaled, ci, beg, end, k0, k1, inj,
-                                           small, q);
+                                           reg, q);
   else if (T.grad_dtype == LUMA_GRAD_F16)
     pass2_dispatch<LUMA_GRAD_F16, INJ_OK>(T, h, old, nw, inv, scaled, ci, beg, end, k0, k1, inj,
-                                          small, q);
+                                          reg, q);
   else
     pass2_dispatch<LUMA_GRAD_F32, INJ_OK>(T, h, old, nw, inv, scaled, ci, beg, end, k0, k1, inj,
-                                          small, q);
+                                          reg, q);
 }
 
 // ---------------------------------------------------------------------------
