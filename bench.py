@@ -250,12 +250,22 @@ def ceilings(reps=5):
     print(json.dumps({"hbm_ceilings": out, "peak_GB_s": HBM_PEAK / 1e9}))
 
 
+def kernel_key(name):
+    """A profiler's kernel name without its return type, template arguments
+    and parameter list: "void luma::pass2_fast_kernel<false>(...)" ->
+    "luma::pass2_fast_kernel"."""
+    name = name.split("(")[0]
+    if name.startswith("void "):
+        name = name[5:]
+    return name.split("<")[0]
+
+
 def _pmc_per_dispatch(path, kernel_prefix, counter):
     import csv
     vals = {}
     with open(path) as f:
         for r in csv.DictReader(f):
-            if r["Counter_Name"] == counter and r["Kernel_Name"].startswith(kernel_prefix):
+            if r["Counter_Name"] == counter and kernel_key(r["Kernel_Name"]).startswith(kernel_prefix):
                 key = int(r["Dispatch_Id"])
                 vals[key] = vals.get(key, 0.0) + float(r["Counter_Value"])
     if not vals:
@@ -271,8 +281,8 @@ def traffic_report(config, kernel, fetch_csv, write_csv, copy_fetch_csv, copy_wr
     algo = {"luma::pass1": pass1_bytes(cfg, n_params, gbytes),
             "luma::pass2": n_params * (gbytes + 16)}[kernel]
     copy_bytes = COPY_ELEMS * 4
-    cf = _pmc_per_dispatch(copy_fetch_csv, "void at::native::vectorized_elementwise_kernel", "FETCH_SIZE")
-    cw = _pmc_per_dispatch(copy_write_csv, "void at::native::vectorized_elementwise_kernel", "WRITE_SIZE")
+    cf = _pmc_per_dispatch(copy_fetch_csv, "at::native::vectorized_elementwise_kernel", "FETCH_SIZE")
+    cw = _pmc_per_dispatch(copy_write_csv, "at::native::vectorized_elementwise_kernel", "WRITE_SIZE")
     # the calibration copy is the largest elementwise launch of its run
     f_scale = copy_bytes / (max(cf) * 1024.0)
     w_scale = copy_bytes / (max(cw) * 1024.0)
@@ -319,9 +329,8 @@ def stats_report(config, trace_csv, bench_json, out):
     with open(trace_csv) as f:
         rows = list(csv.DictReader(f))
     for r in sorted(rows, key=lambda r: int(r["Start_Timestamp"])):
-        name = r["Kernel_Name"]
-        if name.startswith("luma::"):
-            key = name.split("(")[0]
+        key = kernel_key(r["Kernel_Name"])
+        if key.startswith("luma::"):
             durs.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e6)
     total = sum((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e6 for r in rows)
     bench = None
