@@ -368,20 +368,18 @@ __global__ __launch_bounds__(kThreads) void pass1_small_kernel(StepSrc src,
   const uint32_t lane = lane_id();
   float am = 0.0f, av = 0.0f;
   uint32_t im = kNoArg, iv = kNoArg;
-  for (int64_t e0 = beg + (int64_t)lane * kVec; e0 < end; e0 += 64 * kVec) {
-    for (int j = 0; j < kVec; ++j) {
-      const int64_t i = e0 + j;
-      if (i >= end) break;
-      float mn, vn;
-      element_ema(T, h, old, i, scaled, inv, mn, vn);
-      if (beats(fabsf(mn), am)) {
-        am = fabsf(mn);
-        im = (uint32_t)(i - beg);
-      }
-      if (beats(vn, av)) {
-        av = vn;
-        iv = (uint32_t)(i - beg);
-      }
+  // one element per lane and pass: a tensor of n elements takes
+  // ceil(n / 64) passes through the exact path
+  for (int64_t i = beg + (int64_t)lane; i < end; i += 64) {
+    float mn, vn;
+    element_ema(T, h, old, i, scaled, inv, mn, vn);
+    if (beats(fabsf(mn), am)) {
+      am = fabsf(mn);
+      im = (uint32_t)(i - beg);
+    }
+    if (beats(vn, av)) {
+      av = vn;
+      iv = (uint32_t)(i - beg);
     }
   }
   wave_argmax(am, im);
@@ -392,16 +390,28 @@ __global__ __launch_bounds__(kThreads) void pass1_small_kernel(StepSrc src,
 // S' = max(max, floor) with Python's max() semantics (a NaN maximum stays NaN).
 __device__ __forceinline__ double py_max(double a, double floor_) { return floor_ > a ? floor_ : a; }
 
-__global__ __launch_bounds__(64) void finalize_kernel(StepSrc src,
-                                                      const float *__restrict__ partials) {
+// One wavefront per tensor, four per workgroup (fewer workgroups to
+// dispatch when there are thousands of small tensors).
+__global__ __launch_bounds__(kThreads) void finalize_kernel(StepSrc src,
+                                                            const float *__restrict__ partials,
+                                                            int32_t n_tensors) {
   if (skip_step(src)) return;
+  const int64_t ti = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (ti >= n_tensors) return;   // no barriers below
   Tensor T;
   LumaGroup grp;
-  tensor_job(src, T, grp);
+  if (src.tensors) {
+    T = src.tensors[ti];
+    grp = src.groups[T.group];
+  } else {
+    T = src.one;
+    grp = src.group;
+  }
+  const uint32_t lane = lane_id();
   const int nch = (int)(((T.numel - 1) >> src.chunk_shift) + 1);
   float am = 0.0f, av = 0.0f;
   uint32_t cm = kNoArg, cv = kNoArg;   // chunk (within the tensor) of each maximum
-  for (int i = threadIdx.x; i < nch; i += 64) {
+  for (int i = (int)lane; i < nch; i += 64) {
     const float *p = partials + kPartialWords * ((int64_t)T.first_chunk + i);
     if (beats(p[0], am)) {
       am = p[0];
@@ -414,7 +424,7 @@ __global__ __launch_bounds__(64) void finalize_kernel(StepSrc src,
   }
   wave_argmax(am, cm);
   wave_argmax(av, cv);
-  if (threadIdx.x == 0) {
+  if (lane == 0) {
     // the seeds: chunk * C + the offset pass 1 recorded in that chunk
     auto seed = [&](uint32_t c, int word) -> int64_t {
       if (c == kNoArg) return -1;
@@ -524,8 +534,25 @@ __global__ __launch_bounds__(kThreads) void pass2_small_kernel(StepSrc src, uint
   step_key(base_seed, t, T.param_id, k0, k1);
   const PhiloxBase pb = philox_base(T.elem_offset);
   const bool inj = injected(T, noise_mode);
-  for (int64_t e0 = beg + (int64_t)lane_id() * kVec; e0 < end; e0 += 64 * kVec)
-    exact_group(T, h, old, G, e0, end, scaled, inv, inj, pb, k0, k1);
+  // one element per lane and pass (see pass1_small_kernel)
+  for (int64_t i = beg + (int64_t)lane_id(); i < end; i += 64) {
+    float mn, vn;
+    element_ema(T, h, old, i, scaled, inv, mn, vn);
+    T.param[i] = exact_param_update(T.param[i], mn, vn, h);
+    float um, uw;
+    if (!inj) {
+      uint32_t bm, bw;
+      philox_uniform_bits(philox_coarse_block((uint64_t)i, pb, k0, k1),
+                          philox_fine_block((uint64_t)i, pb, k0, k1), (uint64_t)i, bm, bw);
+      um = (float)bm * 0x1p-24f;
+      uw = (float)bw * 0x1p-24f;
+    } else {
+      um = T.u_m[i];
+      uw = T.u_w[i];
+    }
+    T.q_m[i] = (int16_t)exact_quant_m(mn, G, um);
+    T.q_w[i] = (int16_t)(uint16_t)exact_quant_w(vn, G, h.eps, uw);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -2304,8 +2331,8 @@ static int launch_step(StepSrc src, int32_t n_tensors, int32_t n_chunks, float *
     if (int r = check_launch("luma_step: pass 1 (small tensors) launch")) return r;
   }
   if (int r = mark(1)) return r;
-  hipLaunchKernelGGL(finalize_kernel, dim3(n_tensors), dim3(64), 0, s, src,
-                     (const float *)partials);
+  hipLaunchKernelGGL(finalize_kernel, dim3((n_tensors + kThreads / 64 - 1) / (kThreads / 64)),
+                     dim3(kThreads), 0, s, src, (const float *)partials, n_tensors);
   if (int r = check_launch("luma_step: finalize launch")) return r;
   if (int r = mark(2)) return r;
   if (n_big > 0) {
