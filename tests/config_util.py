@@ -1,4 +1,4 @@
-"""Parity of the HIP step with the CPU oracle on whole BASELINE workloads.
+"""Parity of the HIP step with the CPU oracle on whole benchmark workloads.
 
 The HIP optimizer steps every tensor of a parameter set on the GPU; the
 oracle steps a chosen sample of them on the CPU (all of them for the smaller

@@ -1,4 +1,4 @@
-"""The BASELINE workloads against the CPU oracle, on the GPU at full size.
+"""The five benchmark workloads against the CPU oracle, on the GPU at full size.
 
 Each test builds one configuration's parameter set on the GPU, steps it with
 the HIP optimizer, and steps the same tensors (all of them, or a sample for
