@@ -72,6 +72,11 @@ constexpr float kExpm1Poly[5] = {1.0f, 4.999999702e-01f, 1.666688621e-01f, 4.161
                                  8.779187687e-03f};
 constexpr float kLog1pPoly[6] = {1.0f, -4.999998808e-01f, 3.333228827e-01f, -2.496366203e-01f,
                                  1.942020208e-01f, -1.225474551e-01f};
+// expm1(x)/x on (0, 1/2] for the medium regime (same fit, degree 5): float32
+// Horner evaluation of x * c(x) measured at most 2.0u (tests/test_fast_poly.py),
+// against 1.97u for the degree-7 Taylor polynomial of the general form.
+constexpr float kExpm1PolyMed[6] = {1.0f, 5.000001788e-01f, 1.666617095e-01f, 4.171263799e-02f,
+                                    8.149511181e-03f, 1.715260907e-03f};
 
 // expm1 on [0, x_top]: kExpm1Poly when x_top <= 1/8, else degree-8 Taylor
 // below 0.5 and exp2 - 1 above.
@@ -139,31 +144,36 @@ __device__ __forceinline__ float fast_log1p_relerr(float a_top) {
 // Momentum regimes of a tensor's fast path, from its largest decode argument
 // x_top = 32767 dm (old grid) and its largest |m'|, S_m (new scale):
 //   kRegSmall    x_top <= 1/8 and S_m <= 1/8: the minimax polynomials;
-//   kRegMedium   x_top < 1/2 and S_m <= 1/2: the general functions' first
-//                branches alone (the Taylor expm1 and the atanh series), the
-//                ones the general functions pick for every argument below
-//                1/2 -- the same values without the second branch, its
-//                transcendentals and the per-element select;
-//   kRegGeneral  both branches and a select per element.
-// The error bounds are the general ones (fast_*_relerr of x_top and S_m).
-// The atanh series stays within them for arguments somewhat above 1/2
-// (its truncation at s <= 0.2: below 0.02u), which covers a fast |m'| a few
-// ulp above S_m.
+//   kRegMedium   x_top < 1/2 and S_m <= 1/2: a degree-5 minimax expm1 on
+//                (0, 1/2] and the atanh-series log1p to s^9, no second
+//                branch and no per-element select;
+//   kRegGeneral  both branches of each and a select per element.
+// Bounds charged (make_bounds): expm1, fast_expm1_relerr(x_top) in every
+// regime (3u up to 1/8, above that at least 10.5u; the medium and general
+// polynomials stay within 2u); log1p, 3u in the small regime and 10u
+// otherwise, whatever S_m is (the atanh forms: the rounding of 2 + a, of
+// v_rcp_f32 and of the product give s within 3.6u, the series to s^9 adds
+// 2.9u at most, to s^11 2.9u as well: below 7u).  The series stays within
+// that for a fast |m'| a few ulp above S_m.
 constexpr int kRegSmall = 0, kRegMedium = 1, kRegGeneral = 2;
 constexpr float kMedium = 0.5f;
+
+__device__ __forceinline__ int momentum_regime(float x_top, float sm) {
+  if (x_top <= kSmall && sm <= kSmall) return kRegSmall;
+  if (x_top < kMedium && sm <= kMedium) return kRegMedium;
+  return kRegGeneral;
+}
 
 template <int REG>
 __device__ __forceinline__ float fast_expm1(float x) {
   if (REG == kRegSmall) return fast_expm1_small(x);
   if (REG == kRegGeneral) return fast_expm1_general(x);
-  float p = fmaf(x, 1.0f / 40320.0f, 1.0f / 5040.0f);
-  p = fmaf(x, p, 1.0f / 720.0f);
-  p = fmaf(x, p, 1.0f / 120.0f);
-  p = fmaf(x, p, 1.0f / 24.0f);
-  p = fmaf(x, p, 1.0f / 6.0f);
-  p = fmaf(x, p, 0.5f);
-  p = fmaf(x, p, 1.0f);
-  return x * p;
+  float c = fmaf(x, kExpm1PolyMed[5], kExpm1PolyMed[4]);
+  c = fmaf(x, c, kExpm1PolyMed[3]);
+  c = fmaf(x, c, kExpm1PolyMed[2]);
+  c = fmaf(x, c, kExpm1PolyMed[1]);
+  c = fmaf(x, c, kExpm1PolyMed[0]);
+  return x * c;
 }
 
 template <int REG>
@@ -172,8 +182,7 @@ __device__ __forceinline__ float fast_log1p(float a) {
   if (REG == kRegGeneral) return fast_log1p_general(a);
   const float s = a * __builtin_amdgcn_rcpf(2.0f + a);
   const float s2 = s * s;
-  float c = fmaf(s2, 2.0f / 11.0f, 2.0f / 9.0f);
-  c = fmaf(s2, c, 2.0f / 7.0f);
+  float c = fmaf(s2, 2.0f / 9.0f, 2.0f / 7.0f);
   c = fmaf(s2, c, 2.0f / 5.0f);
   c = fmaf(s2, c, 2.0f / 3.0f);
   c = fmaf(s2, c, 2.0f);
@@ -314,7 +323,9 @@ __device__ inline Bounds make_bounds(const Grid *old, const Grid *nw, float b1, 
   B.k1 = B.k2 = B.k3 = B.k7 = B.k8 = 0.0f;
   if (nw) {
     const float rho_e = old ? fast_expm1_relerr(old->fast[kXTopM]) : 0.0f;
-    const float rho_l = fast_log1p_relerr(nw->sm);
+    // the log1p form is the regime's, which also depends on the old grid
+    const int reg = momentum_regime(old ? old->fast[kXTopM] : 0.0f, nw->sm);
+    const float rho_l = reg == kRegSmall ? fast_log1p_relerr(nw->sm) : 10.0f * kU;
     B.k1 = old ? kSafety2 * b1 * (rho_e + 2.0f * kU) * nw->fast[kIdm] : 0.0f;
     B.k2 = kSafety2 * (rho_l + 6.0f * kU);
     B.k3 = kSafety2 * kU + nw->dm * 0.125f + 1e-6f;

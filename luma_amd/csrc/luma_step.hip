@@ -2075,9 +2075,7 @@ __global__ __launch_bounds__(kThreads) void pass2_fast_kernel(StepSrc src, uint6
   const bool inj = injected(T, noise_mode);
   // momentum regime (see luma_fast.h): old grid's decode range, new scale
   const float x_top = old == nullptr ? 0.0f : old->fast[kXTopM];
-  const int reg = (x_top <= kSmall && nw->sm <= kSmall)  ? kRegSmall
-                  : (x_top < kMedium && nw->sm <= kMedium) ? kRegMedium
-                                                           : kRegGeneral;
+  const int reg = momentum_regime(x_top, nw->sm);
   const bool scaled = src.scaling.grad_scale != nullptr;
   const float inv = inv_scale(src);
   __shared__ uint4 qbuf[kThreads / 64][kQueueCapM + kQueueCapW + kStage * 64];

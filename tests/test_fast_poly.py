@@ -60,3 +60,40 @@ def test_polynomial_error_within_bound(name, ref):
 
 def test_small_tier_is_one_eighth():
     assert _small_tier() == 0.125
+
+
+def _medium_points(top):
+    rng = np.random.default_rng(1)
+    x = np.concatenate([rng.uniform(0.0, top, 2_000_000),
+                        np.linspace(0.0, top, 200_001),
+                        np.geomspace(1e-30, top, 100_000)]).astype(np.float32)
+    return x[x > 0]
+
+
+def test_medium_expm1_polynomial_within_small_bound():
+    """The medium regime's degree-5 expm1 on (0, 1/2]: within the 3u that
+    make_bounds charges when x_top <= 1/8 (and so within the 10.5u or more
+    it charges above)."""
+    x = _medium_points(0.5)
+    got = _horner_f32(_coeffs("kExpm1PolyMed"), x).astype(np.float64)
+    want = np.expm1(x.astype(np.float64))
+    rel = np.abs(got - want) / want
+    assert rel.max() < BOUND, rel.max() / U
+
+
+def test_medium_log1p_series_truncation():
+    """The medium regime's log1p, 2 s (1 + s^2/3 + ... + s^8/9) with s = a/(2+a),
+    on (0, 0.52]: with s rounded once, the series' truncation and roundings
+    stay within 3u, leaving 7u of the 10u charged for the rounding of 2 + a,
+    v_rcp_f32 (1.54u) and the product a * rcp."""
+    a = _medium_points(0.52)
+    a64 = a.astype(np.float64)
+    s = (a64 / (2.0 + a64)).astype(np.float32)
+    s2 = (s.astype(np.float64) ** 2).astype(np.float32)
+    c = np.full(s2.shape, np.float32(2.0 / 9.0), dtype=np.float32)
+    for k in (2.0 / 7.0, 2.0 / 5.0, 2.0 / 3.0, 2.0):
+        c = (c.astype(np.float64) * s2.astype(np.float64) + np.float64(np.float32(k))).astype(np.float32)
+    got = (s.astype(np.float64) * c.astype(np.float64)).astype(np.float32).astype(np.float64)
+    want = np.log1p(a64)
+    rel = np.abs(got - want) / want
+    assert rel.max() < BOUND, rel.max() / U
