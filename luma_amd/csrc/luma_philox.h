@@ -8,11 +8,12 @@
 // How the LUMA step uses it (the uniform stream of one (param, step)):
 //   key      = seed = ((t << 32) | 2*param_id) ^ base_seed  (the reference's
 //              per-step seed, functional.py:99-106), split lo/hi.
-//   element e gets two 24-bit uniforms u_m(e), u_w(e) in [0, 1):
-//     high 8 bits  -- bytes 2j, 2j+1 (j = e & 7) of the coarse block
-//                     ctr = (B + (e >> 3), 0, r)
-//     low 16 bits  -- halves 2i, 2i+1 (i = e & 3) of the fine block
-//                     ctr = (2B + (e >> 2), 1, r)
+//   element e gets two 24-bit uniforms u_m(e), u_w(e) in [0, 1); with
+//   j = e & 7 and the three blocks of its group of 8 elements,
+//     T_m = ctr (B + (e >> 3), 0, r),  L = ctr (B + (e >> 3), 1, r),
+//     T_w = ctr (B + (e >> 3), 2, r):
+//     u_m: high 16 bits -- half j of T_m;  low 8 bits -- byte 2j of L
+//     u_w: high 16 bits -- half j of T_w;  low 8 bits -- byte 2j + 1 of L
 //   (counter words: c0 = lo32(index), c1 = hi32(index), c2 = stream, c3 = r).
 // B = o >> 3 and r = o & 7 come from the tensor's element offset o: the
 // index of its element 0 in the whole parameter when the tensor is one shard
@@ -21,9 +22,9 @@
 // parameter; shards with another offset draw from the disjoint counter
 // space r != 0, and two shards of one parameter never share a block (their
 // element ranges are disjoint, so their block ranges are too).
-// The split lets the fast path decide most roundings from one block per 8
-// elements and fetch the low bits only for the rare elements whose decision
-// depends on them.
+// The split lets the fast path decide almost every rounding from the two
+// 16-bit blocks and fetch the low bits only for the rare elements whose
+// decision depends on them.
 #pragma once
 
 #include <stdint.h>
@@ -115,15 +116,13 @@ LUMA_PHILOX_FN PhiloxBase philox_base(int64_t elem_offset) {
   return b;
 }
 
-// The coarse and fine blocks of element e of a tensor.
-LUMA_PHILOX_FN U4 philox_coarse_block(uint64_t e, PhiloxBase o, uint32_t k0, uint32_t k1) {
-  const uint64_t b = o.blk + (e >> 3);
-  return philox4x32_10((uint32_t)b, (uint32_t)(b >> 32), 0u, o.rot, k0, k1);
-}
+// Block `stream` of element e's group of 8 (kBlockTopM, kBlockLow, kBlockTopW).
+constexpr uint32_t kBlockTopM = 0u, kBlockLow = 1u, kBlockTopW = 2u;
 
-LUMA_PHILOX_FN U4 philox_fine_block(uint64_t e, PhiloxBase o, uint32_t k0, uint32_t k1) {
-  const uint64_t b = 2 * o.blk + (e >> 2);
-  return philox4x32_10((uint32_t)b, (uint32_t)(b >> 32), 1u, o.rot, k0, k1);
+LUMA_PHILOX_FN U4 philox_block(uint64_t e, PhiloxBase o, uint32_t stream, uint32_t k0,
+                               uint32_t k1) {
+  const uint64_t b = o.blk + (e >> 3);
+  return philox4x32_10((uint32_t)b, (uint32_t)(b >> 32), stream, o.rot, k0, k1);
 }
 
 LUMA_PHILOX_FN uint32_t u4_word(const U4 &v, int i) {
@@ -136,12 +135,12 @@ LUMA_PHILOX_FN uint32_t u4_byte(const U4 &v, int i) { return (u4_word(v, i >> 2)
 // 16-bit half i (0..7) of a block.
 LUMA_PHILOX_FN uint32_t u4_half(const U4 &v, int i) { return (u4_word(v, i >> 1) >> (16 * (i & 1))) & 0xFFFFu; }
 
-// The two 24-bit integers (u * 2^24) of element e, from its two blocks.
-LUMA_PHILOX_FN void philox_uniform_bits(const U4 &coarse, const U4 &fine, uint64_t e, uint32_t &bits_m,
-                                 uint32_t &bits_w) {
-  const int j = (int)(e & 7), i = (int)(e & 3);
-  bits_m = (u4_byte(coarse, 2 * j) << 16) | u4_half(fine, 2 * i);
-  bits_w = (u4_byte(coarse, 2 * j + 1) << 16) | u4_half(fine, 2 * i + 1);
+// The two 24-bit integers (u * 2^24) of element e, from its group's blocks.
+LUMA_PHILOX_FN void philox_uniform_bits(const U4 &top_m, const U4 &top_w, const U4 &low, uint64_t e,
+                                        uint32_t &bits_m, uint32_t &bits_w) {
+  const int j = (int)(e & 7);
+  bits_m = (u4_half(top_m, j) << 8) | u4_byte(low, 2 * j);
+  bits_w = (u4_half(top_w, j) << 8) | u4_byte(low, 2 * j + 1);
 }
 
 }  // namespace luma

@@ -461,11 +461,11 @@ __device__ __forceinline__ void exact_group(const Tensor &T, const Hyper &h, con
                                             const Grid &G, int64_t e0, int64_t end, bool scaled,
                                             float inv, bool inj, const PhiloxBase &pb, uint32_t k0,
                                             uint32_t k1) {
-  U4 coarse{}, fine0{}, fine1{};
+  U4 top_m{}, top_w{}, low{};   // e0 is a multiple of 8: one group of blocks
   if (!inj) {
-    coarse = philox_coarse_block((uint64_t)e0, pb, k0, k1);
-    fine0 = philox_fine_block((uint64_t)e0, pb, k0, k1);
-    fine1 = philox_fine_block((uint64_t)e0 + 4, pb, k0, k1);
+    top_m = philox_block((uint64_t)e0, pb, kBlockTopM, k0, k1);
+    top_w = philox_block((uint64_t)e0, pb, kBlockTopW, k0, k1);
+    low = philox_block((uint64_t)e0, pb, kBlockLow, k0, k1);
   }
   for (int j = 0; j < kVec; ++j) {
     const int64_t i = e0 + j;
@@ -476,7 +476,7 @@ __device__ __forceinline__ void exact_group(const Tensor &T, const Hyper &h, con
     float um, uw;
     if (!inj) {
       uint32_t bm, bw;
-      philox_uniform_bits(coarse, j < 4 ? fine0 : fine1, (uint64_t)i, bm, bw);
+      philox_uniform_bits(top_m, top_w, low, (uint64_t)i, bm, bw);
       um = (float)bm * 0x1p-24f;
       uw = (float)bw * 0x1p-24f;
     } else {
@@ -542,8 +542,9 @@ __global__ __launch_bounds__(kThreads) void pass2_small_kernel(StepSrc src, uint
     float um, uw;
     if (!inj) {
       uint32_t bm, bw;
-      philox_uniform_bits(philox_coarse_block((uint64_t)i, pb, k0, k1),
-                          philox_fine_block((uint64_t)i, pb, k0, k1), (uint64_t)i, bm, bw);
+      philox_uniform_bits(philox_block((uint64_t)i, pb, kBlockTopM, k0, k1),
+                          philox_block((uint64_t)i, pb, kBlockTopW, k0, k1),
+                          philox_block((uint64_t)i, pb, kBlockLow, k0, k1), (uint64_t)i, bm, bw);
       um = (float)bm * 0x1p-24f;
       uw = (float)bw * 0x1p-24f;
     } else {
@@ -757,8 +758,8 @@ __global__ __launch_bounds__(kThreads) void seed_kernel(StepSrc src, int32_t n_t
 // New code of one element before its draw is final (exact path): the
 // 16-bit code when the uniform u >= p (lo) and when u < p (hi), and the
 // argument a of p = exact_sr_prob(a, z).  The caller knows u to an interval
-// [ulo, uhi] (the injected u itself, or with Philox its top byte's
-// interval); codes that interval decides come back as lo = hi.  p is first
+// [ulo, uhi] (the injected u itself, or with Philox the interval of its
+// top 16 bits); codes that interval decides come back as lo = hi.  p is first
 // bracketed without the double expm1, which then runs only when the bracket
 // overlaps the interval.  Returned packed in one 64-bit value (lo | hi << 16
 // | bits(a) << 32) so that the call needs no stack.
@@ -1507,7 +1508,7 @@ __device__ __forceinline__ void launder(P2Const &C) {
 // One iteration of 8 consecutive elements.  FULL: all 8 valid and 16-byte
 // aligned (vector loads/stores, no masking).  Returns which codes need the
 // exact path (bit j: momentum code of element j, bit 8 + j: preconditioner
-// code); Q and coarse are kept for the queues.
+// code); Q, W and top_w (block T_w) are kept for the queues.
 // STAGE (FULL only): the preconditioner codes go to *stage (LDS) instead
 // of HBM.
 
@@ -1554,16 +1555,24 @@ struct P2Raw {
   vf4 p0, p1;
 };
 
+// float32 gradients (two vectors) are loaded by the iteration itself, not a
+// whole iteration ahead: two buffers of them would take the kernel past the
+// 168 VGPRs that keep three waves per SIMD.
+template <int GD>
+__device__ __forceinline__ void load_p2_grads(const Tensor &T, int64_t e0, Raw8 &r) {
+  if (GD == LUMA_GRAD_F32) {
+    r.g0 = load_stream((const LUMA_GLOBAL vu4 *)((const LUMA_GLOBAL float *)T.grad + e0));
+    r.g1 = load_stream((const LUMA_GLOBAL vu4 *)((const LUMA_GLOBAL float *)T.grad + e0 + 4));
+  } else {
+    r.g0 = load_stream((const LUMA_GLOBAL vu4 *)((const LUMA_GLOBAL uint16_t *)T.grad + e0));
+  }
+}
+
 template <int GD>
 __device__ __forceinline__ void load_p2raw(const Tensor &T, int64_t e0, P2Raw &R) {
   R.r.qm = *(const LUMA_GLOBAL vu4 *)(T.q_m + e0);
   R.r.qw = load_stream((const LUMA_GLOBAL vu4 *)(T.q_w + e0));
-  if (GD == LUMA_GRAD_F32) {
-    R.r.g0 = load_stream((const LUMA_GLOBAL vu4 *)((const LUMA_GLOBAL float *)T.grad + e0));
-    R.r.g1 = load_stream((const LUMA_GLOBAL vu4 *)((const LUMA_GLOBAL float *)T.grad + e0 + 4));
-  } else {
-    R.r.g0 = load_stream((const LUMA_GLOBAL vu4 *)((const LUMA_GLOBAL uint16_t *)T.grad + e0));
-  }
+  if (GD != LUMA_GRAD_F32) load_p2_grads<GD>(T, e0, R.r);
   R.p0 = load_stream((const LUMA_GLOBAL vf4 *)(T.param + e0));
   R.p1 = load_stream((const LUMA_GLOBAL vf4 *)(T.param + e0 + 4));
 }
@@ -1574,9 +1583,10 @@ __device__ __forceinline__ void load_p2raw(const Tensor &T, int64_t e0, P2Raw &R
 template <int GD, bool INJ, int REG, bool SCALED, bool FULL, bool STAGE>
 __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, int64_t e0, int n,
                                             const P2Raw &RW, uint32_t k0, uint32_t k1, Group8 &Q,
-                                            Words4 &W, U4 &coarse, uint4 *stage, CodeAcc &acc) {
+                                            Words4 &W, U4 &top_w, uint4 *stage, CodeAcc &acc) {
   if (FULL) {
-    const Raw8 &R = RW.r;
+    Raw8 R = RW.r;
+    if (GD == LUMA_GRAD_F32) load_p2_grads<GD>(T, e0, R);
     unpack_raw<GD>(R, Q);
     W.qm[0] = R.qm.x; W.qm[1] = R.qm.y; W.qm[2] = R.qm.z; W.qm[3] = R.qm.w;
     W.qw[0] = R.qw.x; W.qw[1] = R.qw.y; W.qw[2] = R.qw.z; W.qw[3] = R.qw.w;
@@ -1615,14 +1625,19 @@ __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, i
       zmu_w[j] = C.zoff - ((FULL || j < n) ? T.u_w[e0 + j] : 0.5f);
     }
   } else {
-    const uint64_t b = C.pblk + ((uint64_t)e0 >> 3);   // coarse block of elements e0 .. e0+7
-    coarse = philox4x32_10_v((uint32_t)b, (uint32_t)(b >> 32), 0u, C.prot, C.pk0, C.pk1, C.pm0,
-                             C.pm1);
+    // the top 16 bits of both uniforms of elements e0 .. e0+7, one block at a
+    // time; T_w is kept for the queue entries (T_m is recomputed by the rare
+    // iteration that queues a momentum code)
+    const uint64_t b = C.pblk + ((uint64_t)e0 >> 3);
+    const U4 tm = philox4x32_10_v((uint32_t)b, (uint32_t)(b >> 32), kBlockTopM, C.prot, C.pk0,
+                                  C.pk1, C.pm0, C.pm1);
 #pragma unroll
-    for (int j = 0; j < kVec; ++j) {
-      zmu_m[j] = fmaf((float)u4_byte(coarse, 2 * j), -1.0f / 256.0f, C.zoff);
-      zmu_w[j] = fmaf((float)u4_byte(coarse, 2 * j + 1), -1.0f / 256.0f, C.zoff);
-    }
+    for (int j = 0; j < kVec; ++j) zmu_m[j] = fmaf((float)u4_half(tm, j), -1.0f / 65536.0f, C.zoff);
+    __builtin_amdgcn_sched_barrier(0);
+    top_w = philox4x32_10_v((uint32_t)b, (uint32_t)(b >> 32), kBlockTopW, C.prot, C.pk0, C.pk1,
+                            C.pm0, C.pm1);
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) zmu_w[j] = fmaf((float)u4_half(top_w, j), -1.0f / 65536.0f, C.zoff);
   }
   uint32_t om[kVec], ow[kVec];   // codes in the low 16 bits (kCodeBias)
   uint32_t flags = 0;
@@ -1725,8 +1740,9 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     C.eps_u = ne != 0.0 ? (float)((double)h.eps / ne) : INFINITY;
   }
   // z = y + zoff - u_low has floor(z) = the LogSR code when u is known to
-  // lie in [u_low, u_low + 2 hb): zoff = 1 - hb (Philox: 1/256 buckets).
-  const float hb = INJ ? 0.0f : 1.0f / 512.0f;
+  // lie in [u_low, u_low + 2 hb): zoff = 1 - hb (Philox: buckets of 2^-16,
+  // the uniform's top 16 bits).
+  const float hb = INJ ? 0.0f : 0x1p-17f;
   C.zoff = 1.0f - hb;
   C.idm = nw->fast[kIdm];
   C.cf = nw->fast[kNl2dw];
@@ -1776,8 +1792,9 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   uint32_t qlen_m = 0, qlen_w = 0;   // pending entries
   uint32_t head_m = 0, head_w = 0;   // ring position of the oldest
   // Queue entry of element k of a group: x = chunk offset (k = x & 7),
-  // y = the coarse Philox word holding the element's top uniform bytes (its
-  // low 16 bits come from the fine block), z = the gradient (bfloat16: the
+  // y = the word of T_m (momentum) or T_w (preconditioner) holding the top
+  // 16 bits of the element's uniform (its low 8 bits come from block L),
+  // z = the gradient (bfloat16: the
   // word of two unscaled gradients holding it; otherwise its float32 bits;
   // no second read of HBM), w = the word of two old codes holding its code.
   // The entry keeps whole words so that building it costs two selects per
@@ -1785,21 +1802,21 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   // fast codes were already stored (or staged); the exact ones overwrite
   // them (same wavefront, so the stores stay in program order).
   // The code of a queued element from its pair: lo = hi when the uniform's
-  // interval decided it; else (Philox) the fine block gives u's low 16 bits.
+  // interval decided it; else (Philox) block L gives u's low 8 bits.
   const float zm_new = nw->zm, zw_new = nw->zw;
   auto draw = [&](const CodePair &c, float z, int64_t i, uint32_t top, int which) -> int {
     if (c.lo == c.hi) return c.lo;
-    const U4 fine = philox_fine_block((uint64_t)i, pb, k0, k1);
-    const float u = (float)((top << 16) | u4_half(fine, 2 * (int)(i & 3) + which)) * 0x1p-24f;
+    const U4 low = philox_block((uint64_t)i, pb, kBlockLow, k0, k1);
+    const float u = (float)((top << 8) | u4_byte(low, 2 * (int)(i & 7) + which)) * 0x1p-24f;
     return sr_below<KTAG>(c.a, z, u) ? c.hi : c.lo;
   };
   // The interval of an entry's uniform: the injected u itself, or (Philox)
-  // the interval of its top byte.
+  // the interval of its top 16 bits.
   auto u_lo = [&](uint32_t top, const LUMA_GLOBAL float *u, int64_t i) -> float {
-    return INJ ? u[i] : (float)(top << 16) * 0x1p-24f;
+    return INJ ? u[i] : (float)(top << 8) * 0x1p-24f;
   };
   auto u_hi = [&](uint32_t top, const LUMA_GLOBAL float *u, int64_t i) -> float {
-    return INJ ? u[i] : (float)((top << 16) | 0xFFFFu) * 0x1p-24f;
+    return INJ ? u[i] : (float)((top << 8) | 0xFFu) * 0x1p-24f;
   };
   // Staging: whole-group iterations [staged_lo, staged_hi) keep their
   // preconditioner codes in stage[(it % kStage) * 64 + lane] until written
@@ -1814,7 +1831,7 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   auto run_m = [&](uint4 ent) {
     const int64_t i = beg + ent.x;
     const uint32_t sh = (ent.x & 1u) << 4;
-    const uint32_t top = INJ ? 0u : (ent.y >> sh) & 0xFFu;
+    const uint32_t top = INJ ? 0u : (ent.y >> sh) & 0xFFFFu;
     const CodePair c = unpack_pair(exact_pair_m<KTAG>((int)(int16_t)(ent.w >> sh), ent_grad(ent, sh),
                                                 old, nw, h, u_lo(top, T.u_m, i),
                                                 u_hi(top, T.u_m, i)));
@@ -1824,7 +1841,7 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     const uint32_t o = ent.x;
     const int64_t i = beg + o;
     const uint32_t sh = (o & 1u) << 4;
-    const uint32_t top = INJ ? 0u : (ent.y >> (sh + 8u)) & 0xFFu;
+    const uint32_t top = INJ ? 0u : (ent.y >> sh) & 0xFFFFu;
     const CodePair c = unpack_pair(exact_pair_w<KTAG>((int)((ent.w >> sh) & 0xFFFFu), ent_grad(ent, sh),
                                                 old, nw, h, u_lo(top, T.u_w, i),
                                                 u_hi(top, T.u_w, i)));
@@ -1840,7 +1857,7 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   // Queue the codes of one iteration that the fast path could not certify,
   // and run full batches of 64, oldest first.
   auto take = [&](int64_t e0, uint32_t flags, const Group8 &Q, const Words4 &W,
-                  const U4 &coarse) {
+                  const U4 &top_w) {
     if (!__ballot(flags != 0)) return;
     const uint32_t off0 = (uint32_t)(e0 - beg);
     // queue positions: a wave prefix sum of (momentum count | preconditioner
@@ -1851,10 +1868,17 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
     const uint32_t excl = incl - cnt;
     const uint32_t tot_m = tot & 0xFFFFu, tot_w = tot >> 16;
-    // queue entry of element off0 + k: its top uniform bytes are bytes 2k
-    // (momentum) and 2k + 1 (preconditioner) of the coarse block, in word k/2
-    const uint32_t cw[4] = {coarse.x, coarse.y, coarse.z, coarse.w};
-    auto entry = [&](uint32_t k, const uint32_t (&codes)[4]) {
+    // queue entry of element off0 + k: the top 16 bits of its uniform are
+    // half k of T_m (momentum) or T_w (preconditioner), in word k/2
+    const uint32_t cw[4] = {top_w.x, top_w.y, top_w.z, top_w.w};
+    uint32_t cm[4] = {0u, 0u, 0u, 0u};
+    if (!INJ && __ballot(fm != 0u)) {
+      const uint64_t b = C.pblk + ((uint64_t)e0 >> 3);
+      const U4 tm = philox4x32_10_v((uint32_t)b, (uint32_t)(b >> 32), kBlockTopM, C.prot, C.pk0,
+                                    C.pk1, C.pm0, C.pm1);
+      cm[0] = tm.x; cm[1] = tm.y; cm[2] = tm.z; cm[3] = tm.w;
+    }
+    auto entry = [&](uint32_t k, const uint32_t (&codes)[4], const uint32_t (&tops)[4]) {
       const uint32_t m1 = bit_mask(k, 1), m2 = bit_mask(k, 2);
       uint32_t g;
       if (GD == LUMA_GRAD_BF16) {
@@ -1865,33 +1889,33 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
         for (int j = 0; j < kVec; ++j) gb[j] = __float_as_uint(Q.g[j]);
         g = sel8(gb, k);
       }
-      return make_uint4(off0 + k, INJ ? 0u : word_of(cw, m1, m2), g, word_of(codes, m1, m2));
+      return make_uint4(off0 + k, INJ ? 0u : word_of(tops, m1, m2), g, word_of(codes, m1, m2));
     };
     if (qlen_m + tot_m <= (uint32_t)kQueueCapM) {
       uint32_t pos = head_m + qlen_m + (excl & 0xFFFFu);
       for (uint32_t f = fm; f != 0u; f &= f - 1u) {
         const uint32_t k = (uint32_t)__builtin_ctz(f);
-        queue_m[pos++ & (kQueueCapM - 1)] = entry(k, W.qm);
+        queue_m[pos++ & (kQueueCapM - 1)] = entry(k, W.qm, cm);
       }
       qlen_m += tot_m;
     } else {
       // more than the queue holds (only when most codes are uncertain): in place
       for (uint32_t f = fm; f != 0u; f &= f - 1u) {
         const uint32_t k = (uint32_t)__builtin_ctz(f);
-        run_m(entry(k, W.qm));
+        run_m(entry(k, W.qm, cm));
       }
     }
     if (qlen_w + tot_w <= (uint32_t)kQueueCapW) {
       uint32_t pos = head_w + qlen_w + (excl >> 16);
       for (uint32_t f = fw; f != 0u; f &= f - 1u) {
         const uint32_t k = (uint32_t)__builtin_ctz(f);
-        queue_w[pos++ & (kQueueCapW - 1)] = entry(k, W.qw);
+        queue_w[pos++ & (kQueueCapW - 1)] = entry(k, W.qw, cw);
       }
       qlen_w += tot_w;
     } else {
       for (uint32_t f = fw; f != 0u; f &= f - 1u) {
         const uint32_t k = (uint32_t)__builtin_ctz(f);
-        run_w(entry(k, W.qw));
+        run_w(entry(k, W.qw, cw));
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -1949,11 +1973,11 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     const int64_t e0 = group_at(j);
     Group8 Q;
     Words4 W;
-    U4 coarse{};
+    U4 top_w{};
     const uint32_t flags = p2_iter<GD, INJ, REG, SCALED, true, true>(
-        T, C, e0, kVec, R, k0, k1, Q, W, coarse, &stage[(j % kStage) * 64 + lane], acc);
+        T, C, e0, kVec, R, k0, k1, Q, W, top_w, &stage[(j % kStage) * 64 + lane], acc);
     staged_hi = j + 1;
-    take(e0, flags, Q, W, coarse);
+    take(e0, flags, Q, W, top_w);
     const int wb = j + 1 - kStage;   // the slot iteration j + 1 will use
     if (wb >= 0) {
       while (qlen_w > 0 && oldest_w() <= wb) batch_w();
@@ -1986,16 +2010,16 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     const int n = rem <= 0 ? 0 : (rem < kVec ? (int)rem : kVec);
     Group8 Q;
     Words4 W;
-    U4 coarse{};
+    U4 top_w{};
     P2Raw R;
     const bool whole = vec_ok && n == kVec;
     if (whole) load_p2raw<GD>(T, e0, R);
     const uint32_t flags =
-        whole ? p2_iter<GD, INJ, REG, SCALED, true, false>(T, C, e0, n, R, k0, k1, Q, W, coarse,
+        whole ? p2_iter<GD, INJ, REG, SCALED, true, false>(T, C, e0, n, R, k0, k1, Q, W, top_w,
                                                              nullptr, acc)
               : p2_iter<GD, INJ, REG, SCALED, false, false>(T, C, e0, n, R, k0, k1, Q, W,
-                                                              coarse, nullptr, acc);
-    take(e0, flags, Q, W, coarse);
+                                                              top_w, nullptr, acc);
+    take(e0, flags, Q, W, top_w);
   }
   // The thread's summary word: its largest |Q_m| + margin, its smallest
   // Q_w - margin (clamped to the code ranges).
@@ -2191,11 +2215,11 @@ __global__ __launch_bounds__(kThreads) void quant_kernel(const float *__restrict
   const int64_t beg = (int64_t)blockIdx.x * kChunk;
   const int64_t end = beg + kChunk < n ? beg + kChunk : n;
   for (int64_t e0 = beg + (int64_t)threadIdx.x * kVec; e0 < end; e0 += (int64_t)kThreads * kVec) {
-    U4 coarse{}, fine0{}, fine1{};
+    U4 top_m{}, top_w{}, low{};
     if (noise_mode == LUMA_NOISE_PHILOX) {
-      coarse = philox_coarse_block((uint64_t)e0, PhiloxBase{0, 0}, k0, k1);
-      fine0 = philox_fine_block((uint64_t)e0, PhiloxBase{0, 0}, k0, k1);
-      fine1 = philox_fine_block((uint64_t)e0 + 4, PhiloxBase{0, 0}, k0, k1);
+      top_m = philox_block((uint64_t)e0, PhiloxBase{0, 0}, kBlockTopM, k0, k1);
+      top_w = philox_block((uint64_t)e0, PhiloxBase{0, 0}, kBlockTopW, k0, k1);
+      low = philox_block((uint64_t)e0, PhiloxBase{0, 0}, kBlockLow, k0, k1);
     }
     for (int j = 0; j < kVec; ++j) {
       const int64_t i = e0 + j;
@@ -2203,7 +2227,7 @@ __global__ __launch_bounds__(kThreads) void quant_kernel(const float *__restrict
       float um, uw;
       if (noise_mode == LUMA_NOISE_PHILOX) {
         uint32_t bm, bw;
-        philox_uniform_bits(coarse, j < 4 ? fine0 : fine1, (uint64_t)i, bm, bw);
+        philox_uniform_bits(top_m, top_w, low, (uint64_t)i, bm, bw);
         um = (float)bm * 0x1p-24f;
         uw = (float)bw * 0x1p-24f;
       } else {
