@@ -3,9 +3,9 @@
 Every element but the first of a 10^7 + 1 element tensor has the same codes
 and gradient, so all of them share one m', v' and one continuous bin index y
 on the new grid; the first element sets the scales.  One ``LUMA.step()`` then
-rounds those 10^7 copies of y with pass 2's production decision (the top 8
-uniform bits decide, the low 16 bits are drawn only for elements whose
-threshold falls inside their 1/256 bucket).  The round-up frequency must
+rounds those 10^7 copies of y with pass 2's production decision (the top 16
+uniform bits decide, the low 8 bits are drawn only for elements whose
+threshold falls inside their 2^-16 bucket).  The round-up frequency must
 match the oracle's p* (z < 5) and the mean decoded value must equal the
 linear value (the reference's TestLogSR, tests/test_correctness.py:40-103,
 scaled to 10^7 draws; the draws are those of the step,
@@ -13,8 +13,8 @@ src/luma_optimizer/triton_kernel.py:93-128).
 
 The gradient of the shared elements is chosen, among consecutive float32
 values, to put p* of the momentum code at a target: inside a bucket, and just
-above the bucket edge 100/256 (where almost every draw needs its low 16
-bits).  The preconditioner code's p* falls where that gradient puts it.
+above the bucket edge 100/256 (where the draws in the edge's 2^-16 bucket
+need their low 8 bits).  The preconditioner code's p* falls where that gradient puts it.
 """
 
 import math
