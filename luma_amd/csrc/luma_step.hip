@@ -534,23 +534,41 @@ __global__ __launch_bounds__(kThreads) void pass2_small_kernel(StepSrc src, uint
   step_key(base_seed, t, T.param_id, k0, k1);
   const PhiloxBase pb = philox_base(T.elem_offset);
   const bool inj = injected(T, noise_mode);
-  // one element per lane and pass (see pass1_small_kernel)
-  for (int64_t i = beg + (int64_t)lane_id(); i < end; i += 64) {
+  // One element per lane and pass (see pass1_small_kernel).  The 8 lanes of
+  // a group of elements (beg is a multiple of 8) share its three Philox
+  // blocks: lanes 0, 1 and 2 of the group evaluate T_m, L and T_w, and every
+  // lane takes the words it needs from them, so each pass costs one block
+  // per lane instead of three.  Every lane runs every pass (the blocks are
+  // evaluated and exchanged by lanes past the end too); only lanes on an
+  // element touch memory.
+  const uint32_t lane = lane_id(), r = lane & 7u;
+  const int first = (int)(lane & ~7u);   // lane 0 of the group
+  const uint32_t stream = r == 1u ? kBlockLow : (r == 2u ? kBlockTopW : kBlockTopM);
+  const uint32_t sh = (r & 1u) << 4;
+  for (int64_t i0 = beg; i0 < end; i0 += 64) {
+    const int64_t i = i0 + (int64_t)lane;
+    uint32_t bm = 0u, bw = 0u;
+    if (!inj) {
+      const U4 blk = philox_block((uint64_t)i, pb, stream, k0, k1);
+      // word r >> 1 of the block held by lane first + s
+      auto word = [&](int s) -> uint32_t {
+        const uint32_t x = (uint32_t)__shfl((int)blk.x, first + s, 64);
+        const uint32_t y = (uint32_t)__shfl((int)blk.y, first + s, 64);
+        const uint32_t z = (uint32_t)__shfl((int)blk.z, first + s, 64);
+        const uint32_t w = (uint32_t)__shfl((int)blk.w, first + s, 64);
+        return (r & 4u) ? ((r & 2u) ? w : z) : ((r & 2u) ? y : x);
+      };
+      const uint32_t wm = word(0), wl = word(1), ww = word(2);
+      // philox_uniform_bits: half r of T_m / T_w, bytes 2r and 2r + 1 of L
+      bm = (((wm >> sh) & 0xFFFFu) << 8) | ((wl >> sh) & 0xFFu);
+      bw = (((ww >> sh) & 0xFFFFu) << 8) | ((wl >> (sh + 8u)) & 0xFFu);
+    }
+    if (i >= end) continue;
     float mn, vn;
     element_ema(T, h, old, i, scaled, inv, mn, vn);
     T.param[i] = exact_param_update(T.param[i], mn, vn, h);
-    float um, uw;
-    if (!inj) {
-      uint32_t bm, bw;
-      philox_uniform_bits(philox_block((uint64_t)i, pb, kBlockTopM, k0, k1),
-                          philox_block((uint64_t)i, pb, kBlockTopW, k0, k1),
-                          philox_block((uint64_t)i, pb, kBlockLow, k0, k1), (uint64_t)i, bm, bw);
-      um = (float)bm * 0x1p-24f;
-      uw = (float)bw * 0x1p-24f;
-    } else {
-      um = T.u_m[i];
-      uw = T.u_w[i];
-    }
+    const float um = inj ? T.u_m[i] : (float)bm * 0x1p-24f;
+    const float uw = inj ? T.u_w[i] : (float)bw * 0x1p-24f;
     T.q_m[i] = (int16_t)exact_quant_m(mn, G, um);
     T.q_w[i] = (int16_t)(uint16_t)exact_quant_w(vn, G, h.eps, uw);
   }
