@@ -865,18 +865,18 @@ __device__ __noinline__ uint64_t exact_pair_w(int qw, float g, const LUMA_GLOBAL
 // likely to still be in L2.
 constexpr int kQueueCap = kVec * 64 + 64;
 constexpr int kQueueCapW = 256;   // pass 2 preconditioner ring (entries)
-constexpr int kQueueCapM = 128;   // pass 2 momentum ring (uncertain 8x less often)
+constexpr int kQueueCapM = 64;    // pass 2 momentum ring (uncertain codes are rare)
 static_assert((kQueueCapW & (kQueueCapW - 1)) == 0 && (kQueueCapM & (kQueueCapM - 1)) == 0,
               "pass 2 queues are power-of-two rings");
 // Pass 2 stages the new preconditioner codes of its last kStage iterations
 // in LDS (one 16-byte group per lane per iteration) and writes an
 // iteration's codes to HBM only once its queued exact codes are in: the
 // exact codes then land in LDS instead of in lines already written back.
-// With about 15 uncertain preconditioner codes per wave iteration, the ring
-// fills a 64-entry batch every 4-5 iterations, so 7 slots rarely force a
-// partial batch.  LDS per workgroup: 4 x (128 + 256 + 7 x 64) x 16 B = 52 KB,
+// With about 9 uncertain preconditioner codes per wave iteration, the ring
+// fills a 64-entry batch every 7 iterations, so 8 slots seldom force a
+// partial batch.  LDS per workgroup: 4 x (64 + 256 + 8 x 64) x 16 B = 52 KB,
 // so three workgroups (the VGPR limit) still fit a CU's 160 KB.
-constexpr int kStage = 7;
+constexpr int kStage = 8;
 
 // Keeps a wave-uniform value in a VGPR.  On gfx950 a VALU instruction with
 // an SGPR source operand issues at about half the rate of one whose sources
