@@ -197,7 +197,9 @@ def chunk_elems(shapes):
     import numpy as np
     from luma_amd.optimizer import _Engine
     numels = np.array([math.prod(s) for s in shapes], dtype=np.int64)
-    return _Engine.chunk_for(types.SimpleNamespace(chunk_elems=0), numels)
+    eng = types.SimpleNamespace(chunk_elems=0, small_tensors=True)
+    eng._small_limit = lambda: _Engine._small_limit(eng)
+    return _Engine.chunk_for(eng, numels)
 
 
 def pass1_bytes(cfg, n_params, gbytes):

@@ -173,8 +173,12 @@ class _Engine:
         of two from CHUNK_ELEMS down to STEP_CHUNK_MIN with STEP_TARGET_CHUNKS
         chunks of it at most the set's total size.  Small sets get shorter
         chunks; so do sets of many tensors whose total is small, where one
-        chunk per tensor would leave the largest tensors' workgroups running
-        alone at the end of the launch.  The result does not depend on it:
+        chunk per tensor in parameter order would leave the largest tensors'
+        workgroups running alone at the end of the launch.  A set with at least
+        STEP_TARGET_CHUNKS tensors above the wavefront-per-tensor limit fills
+        the chip with one chunk per tensor: it takes a chunk as long as its
+        largest tensor (at most CHUNK_ELEMS), and chunk_layout puts the
+        largest tensors first.  The result does not depend on the length:
         every element is computed alone and the per-tensor maxima are exact."""
         if self.chunk_elems:
             return self.chunk_elems
@@ -182,6 +186,10 @@ class _Engine:
         c = L.CHUNK_ELEMS
         while c > STEP_CHUNK_MIN and c * STEP_TARGET_CHUNKS > total:
             c //= 2
+        big = numels[numels > self._small_limit()]
+        if len(big) >= STEP_TARGET_CHUNKS:
+            while c < L.CHUNK_ELEMS and c < int(big.max()):
+                c *= 2
         return c
 
     def table(self, rows) -> np.ndarray:
@@ -267,16 +275,18 @@ class _Engine:
         first chunk of every tensor, the chunk records (tensor, index) and the
         number of trailing records that belong to small tensors.  Tensors of at
         most SMALL_TENSOR elements come last, stepped a wavefront per chunk
-        (luma.h, LumaStepArgs.small_chunks); the others keep their order."""
+        (luma.h, LumaStepArgs.small_chunks).  The others keep their order,
+        unless there are STEP_TARGET_CHUNKS of them or more (chunk_for gives
+        such a set one chunk per tensor): then the largest come first, so the
+        launch ends on its shortest workgroups (ties keep their order)."""
         n = len(numels)
         nch = (numels + c - 1) // c
-        if self.small_tensors:
-            small = numels <= L.SMALL_TENSOR
-            order = np.concatenate([np.nonzero(~small)[0], np.nonzero(small)[0]])
-            n_small = int(nch[small].sum())
-        else:
-            order = np.arange(n)
-            n_small = 0
+        small = numels <= self._small_limit()
+        big = np.nonzero(~small)[0]
+        if len(big) >= STEP_TARGET_CHUNKS:
+            big = big[np.argsort(-numels[big], kind="stable")]
+        order = np.concatenate([big, np.nonzero(small)[0]])
+        n_small = int(nch[small].sum())
         nch_o = nch[order]
         first_o = np.zeros(n, dtype=np.int64)
         np.cumsum(nch_o[:-1], out=first_o[1:])

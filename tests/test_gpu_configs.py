@@ -99,11 +99,12 @@ def test_cfg3_many_small():
         gen = _gen(3000 + t)
         gd = [normal_grad(p.shape, 1e-4, gen, DEV, torch.float32, zeros=0.01) for p in params]
         pair.step(gd, {i: g.cpu() for i, g in enumerate(gd)})
-        # 4096 chunks of 16384 exceed the set's total: the automatic choice
-        # is the shortest chunk, so the largest tensors take up to 4 chunks
-        n_chunks = sum(-(-p.numel() // 16384) for p in params)
-        assert pair.opt._engine._chunk == 16384 and pair.opt._engine._n_chunks == n_chunks
-        assert n_chunks > len(params)
+        # more than 4096 tensors above the wavefront limit: one chunk per
+        # tensor (the largest has 32769 to 65536 elements), largest first
+        eng = pair.opt._engine
+        assert 32768 < max(p.numel() for p in params) <= 65536
+        assert eng._chunk == 65536 and eng._n_chunks == len(params)
+        assert eng._small_chunks == sum(1 for p in params if p.numel() <= 512)
         rows = pair.check()
         assert sum(r["n"] for r in rows) == total
 

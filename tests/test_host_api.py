@@ -16,6 +16,15 @@ from luma_amd.optimizer import make_step_seed
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
+def _engine_stub(chunk_elems=0, small_tensors=True):
+    """The attributes _Engine.chunk_for and _Engine.chunk_layout read."""
+    import types
+    from luma_amd.optimizer import _Engine
+    eng = types.SimpleNamespace(chunk_elems=chunk_elems, small_tensors=small_tensors)
+    eng._small_limit = lambda: _Engine._small_limit(eng)
+    return eng
+
+
 def _declared_symbols():
     text = open(os.path.join(ROOT, "include", "luma.h")).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
@@ -144,7 +153,7 @@ def test_step_chunk_policy():
     import numpy as np
     from luma_amd.optimizer import _Engine
     pick = _Engine.chunk_for
-    auto = types.SimpleNamespace(chunk_elems=0)
+    auto = _engine_stub(chunk_elems=0)
     assert pick(auto, np.array([4096 * 4096], dtype=np.int64)) == 16384
     assert pick(auto, np.array([65536] * 4096, dtype=np.int64)) == 65536
     assert pick(auto, np.array([65536] * 8192, dtype=np.int64)) == 131072
@@ -154,7 +163,15 @@ def test_step_chunk_policy():
     assert pick(auto, np.array([65536] * 2047, dtype=np.int64)) == 16384
     assert pick(auto, np.array([1] * 20000, dtype=np.int64)) == 16384
     assert pick(auto, np.array([65536] * 1000 + [1] * 20000, dtype=np.int64)) == 16384
-    assert pick(types.SimpleNamespace(chunk_elems=2048), np.array([10], dtype=np.int64)) == 2048
+    assert pick(_engine_stub(chunk_elems=2048), np.array([10], dtype=np.int64)) == 2048
+    # 4096 or more tensors above the wavefront limit: one chunk per tensor,
+    # as long as the largest of them (at most 131072)
+    assert pick(auto, np.array([600] * 4095 + [40000], dtype=np.int64)) == 65536
+    assert pick(auto, np.array([600] * 4096 + [300000], dtype=np.int64)) == 131072
+    assert pick(auto, np.array([600] * 4095 + [40000] + [1] * 10, dtype=np.int64)) == 65536
+    assert pick(auto, np.array([600] * 4095 + [1] * 10, dtype=np.int64)) == 16384
+    assert pick(_engine_stub(small_tensors=False),
+                np.array([600] * 4095 + [1] * 10, dtype=np.int64)) == 16384
 
 
 def test_step_rejects_bad_chunk_length():
@@ -201,7 +218,7 @@ def test_chunk_layout_small_tensors_last():
     import numpy as np
     from luma_amd.optimizer import _Engine
     numels = np.array([5000, 3, 512, 513, 40000, 1, 20000], dtype=np.int64)
-    eng = types.SimpleNamespace(small_tensors=True)
+    eng = _engine_stub(small_tensors=True)
     first, ch, n_small = _Engine.chunk_layout(eng, numels, 16384)
     assert n_small == 3
     assert ch["tensor"].tolist() == [0, 3, 4, 4, 4, 6, 6, 1, 2, 5]
@@ -214,3 +231,30 @@ def test_chunk_layout_small_tensors_last():
     assert n_small == 0
     assert ch["tensor"].tolist() == [0, 1, 2, 3, 4, 4, 4, 5, 6, 6]
     assert first.tolist() == [0, 1, 2, 3, 4, 7, 8]
+
+
+def test_chunk_layout_many_tensors_largest_first(monkeypatch):
+    """With STEP_TARGET_CHUNKS or more tensors above the wavefront limit, their
+    chunk records come largest tensor first (ties in parameter order), the
+    small tensors still last; first_chunk points at each tensor's records."""
+    import numpy as np
+    import luma_amd.optimizer as O
+    numels = np.array([5000, 3, 512, 513, 40000, 1, 20000, 5000], dtype=np.int64)
+    eng = _engine_stub()
+    monkeypatch.setattr(O, "STEP_TARGET_CHUNKS", 5)
+    assert O._Engine.chunk_for(eng, numels) == 65536
+    first, ch, n_small = O._Engine.chunk_layout(eng, numels, 65536)
+    assert n_small == 3
+    assert ch["tensor"].tolist() == [4, 6, 0, 7, 3, 1, 2, 5]
+    assert ch["index"].tolist() == [0] * 8
+    for t in range(len(numels)):
+        assert ch["tensor"][first[t]] == t
+    # chunks of 16384: the 40000-element tensor's three records stay together
+    first, ch, n_small = O._Engine.chunk_layout(eng, numels, 16384)
+    assert ch["tensor"].tolist() == [4, 4, 4, 6, 6, 0, 7, 3, 1, 2, 5]
+    assert ch["index"].tolist() == [0, 1, 2, 0, 1, 0, 0, 0, 0, 0, 0]
+    assert first.tolist() == [5, 8, 9, 7, 0, 10, 3, 6]
+    # one tensor fewer above the limit: parameter order
+    monkeypatch.setattr(O, "STEP_TARGET_CHUNKS", 6)
+    first, ch, n_small = O._Engine.chunk_layout(eng, numels, 65536)
+    assert ch["tensor"].tolist() == [0, 3, 4, 6, 7, 1, 2, 5]
