@@ -275,17 +275,22 @@ class _Engine:
         first chunk of every tensor, the chunk records (tensor, index) and the
         number of trailing records that belong to small tensors.  Tensors of at
         most SMALL_TENSOR elements come last, stepped a wavefront per chunk
-        (luma.h, LumaStepArgs.small_chunks).  The others keep their order,
-        unless there are STEP_TARGET_CHUNKS of them or more (chunk_for gives
-        such a set one chunk per tensor): then the largest come first, so the
-        launch ends on its shortest workgroups (ties keep their order)."""
+        (luma.h, LumaStepArgs.small_chunks), largest first: the four
+        wavefronts of a workgroup then step tensors of about one size, and
+        none holds the workgroup long after the other three are done.  The
+        others keep their order, unless there are STEP_TARGET_CHUNKS of them
+        or more (chunk_for gives such a set one chunk per tensor): then the
+        largest come first, so the launch ends on its shortest workgroups.
+        Ties keep their order."""
         n = len(numels)
         nch = (numels + c - 1) // c
         small = numels <= self._small_limit()
         big = np.nonzero(~small)[0]
         if len(big) >= STEP_TARGET_CHUNKS:
             big = big[np.argsort(-numels[big], kind="stable")]
-        order = np.concatenate([big, np.nonzero(small)[0]])
+        little = np.nonzero(small)[0]
+        little = little[np.argsort(-numels[little], kind="stable")]
+        order = np.concatenate([big, little])
         n_small = int(nch[small].sum())
         nch_o = nch[order]
         first_o = np.zeros(n, dtype=np.int64)

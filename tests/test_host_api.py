@@ -212,8 +212,8 @@ def test_state_arena_layout():
 
 def test_chunk_layout_small_tensors_last():
     """Tensors of at most SMALL_TENSOR elements take the last chunk records
-    (one each); the others keep their order; first_chunk points at each
-    tensor's records."""
+    (one each, largest first); the others keep their order; first_chunk
+    points at each tensor's records."""
     import types
     import numpy as np
     from luma_amd.optimizer import _Engine
@@ -221,9 +221,9 @@ def test_chunk_layout_small_tensors_last():
     eng = _engine_stub(small_tensors=True)
     first, ch, n_small = _Engine.chunk_layout(eng, numels, 16384)
     assert n_small == 3
-    assert ch["tensor"].tolist() == [0, 3, 4, 4, 4, 6, 6, 1, 2, 5]
+    assert ch["tensor"].tolist() == [0, 3, 4, 4, 4, 6, 6, 2, 1, 5]
     assert ch["index"].tolist() == [0, 0, 0, 1, 2, 0, 1, 0, 0, 0]
-    assert first.tolist() == [0, 7, 8, 1, 2, 9, 5]
+    assert first.tolist() == [0, 8, 7, 1, 2, 9, 5]
     for t in range(len(numels)):
         assert ch["tensor"][first[t]] == t and ch["index"][first[t]] == 0
     eng.small_tensors = False
@@ -245,16 +245,16 @@ def test_chunk_layout_many_tensors_largest_first(monkeypatch):
     assert O._Engine.chunk_for(eng, numels) == 65536
     first, ch, n_small = O._Engine.chunk_layout(eng, numels, 65536)
     assert n_small == 3
-    assert ch["tensor"].tolist() == [4, 6, 0, 7, 3, 1, 2, 5]
+    assert ch["tensor"].tolist() == [4, 6, 0, 7, 3, 2, 1, 5]
     assert ch["index"].tolist() == [0] * 8
     for t in range(len(numels)):
         assert ch["tensor"][first[t]] == t
     # chunks of 16384: the 40000-element tensor's three records stay together
     first, ch, n_small = O._Engine.chunk_layout(eng, numels, 16384)
-    assert ch["tensor"].tolist() == [4, 4, 4, 6, 6, 0, 7, 3, 1, 2, 5]
+    assert ch["tensor"].tolist() == [4, 4, 4, 6, 6, 0, 7, 3, 2, 1, 5]
     assert ch["index"].tolist() == [0, 1, 2, 0, 1, 0, 0, 0, 0, 0, 0]
-    assert first.tolist() == [5, 8, 9, 7, 0, 10, 3, 6]
+    assert first.tolist() == [5, 9, 8, 7, 0, 10, 3, 6]
     # one tensor fewer above the limit: parameter order
     monkeypatch.setattr(O, "STEP_TARGET_CHUNKS", 6)
     first, ch, n_small = O._Engine.chunk_layout(eng, numels, 65536)
-    assert ch["tensor"].tolist() == [0, 3, 4, 6, 7, 1, 2, 5]
+    assert ch["tensor"].tolist() == [0, 3, 4, 6, 7, 2, 1, 5]
