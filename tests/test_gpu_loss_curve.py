@@ -1,184 +1,80 @@
 """1,000-step training curves: HIP LUMA vs the CPU oracle (the reference's
-PyTorch backend restated) on a nanoGPT-shaped model.
-
-The model follows the reference's benchmark configuration
-(benchmarks/bench_nanogpt.py): 4 layers, 4 heads, 128-wide, block 64,
-batch 32, betas (0.9, 0.95), lr 3e-4, weight decay 0.1 on matrices,
-gradient clipping at 1.0.  The text is synthetic (a seeded word-level Markov
-chain rendered as characters); nothing is downloaded.
+PyTorch backend restated) on a nanoGPT-shaped model (tests/loss_curve_model.py:
+the reference benchmark's 4-layer, 128-wide configuration, on synthetic text).
 
 Two identical models see the same batches.  Model A steps with ``luma_amd.LUMA``
 on the GPU; model B's gradients go to the CPU, the oracle steps its float32
 copies, and the parameters come back.  Evaluation losses on fixed held-out
-batches are compared every 100 steps against the reference's own backend-
-agreement threshold, 0.5% relative (tests/test_correctness.py:333-339):
+batches are compared every 100 steps, in three modes:
 
-* injected noise -- the oracle's generator draws are fed to the HIP step, so
-  the two runs differ only by the parameter update's float rounding (the
-  codes are identical, the update within 1e-6 per step);
-* native noise -- HIP draws from Philox, the oracle from torch.Generator, so
-  the curves are two independent samples of the same stochastic rounding.
+* exact -- injected noise (the oracle's generator draws fed to the HIP step)
+  and the library's exact per-element path (LUMA_FLAG_EXACT_ONLY), whose
+  parameter update is the reference's float32 operation sequence: the two
+  runs must stay identical to within 1e-6 at every evaluation point;
+* injected -- injected noise, production (fast) path: the codes are
+  identical and the update within 1e-6 per step, but not the reference's
+  bits;
+* native -- HIP draws from Philox, the oracle from torch.Generator, so the
+  curves are two independent samples of the same stochastic rounding.
 
-* injected noise, exact path -- the library's exact per-element path
-  (LUMA_FLAG_EXACT_ONLY), whose parameter update is the reference's float32
-  operation sequence with correctly rounded sqrt: the two runs must stay
-  identical to within 1e-6 at every evaluation point.
+The per-point tolerance of the last two is the criterion's own noise floor,
+measured with the oracle against itself (tests/loss_curve_floor.py, CPU):
+up to step 600 every perturbed run stays within 5e-4, but while the loss
+falls fastest (steps 700-1000) training amplifies any difference, a one-ulp
+one included.  The reference's ATen math against correctly rounded math,
+same draws, differs by up to 1.09% (step 1000); four other base seeds by up
+to 0.98%, 1.17%, 0.31% and 1.61%.  The reference's own backend-agreement
+threshold, 0.5% (tests/test_correctness.py:333-339, a 100-step quadratic),
+is below that floor.  So:
 
-While the loss falls fastest (steps 700-1000 here) training amplifies any
-difference: with injected noise the fast path's curve agrees to 5e-6 up to
-step 600, and at step 1000 the update's rounding (within 1e-6 per step, but
-not the reference's bits) has grown to 0.84% (measured on MI355X; native
-noise: 0.77%).  The exact-path run shows that nothing else differs.  So each
-evaluation point of the fast path must be within 1.0% (the measured 0.84%
-plus a 20% margin), and the mean over the curve -- which a bias in the
-noise, the rounding or the update would move -- within 0.2% (injected) and
-0.5% (native; the reference's backend-agreement threshold,
-tests/test_correctness.py:333-339).
+* injected: every point within 1.1% (the largest same-draws spread, ATen
+  against correctly rounded math; measured on MI355X: 0.84% at step 1000),
+  and the curve means within 2e-3 (floor 5.3e-4);
+* native: every point within 1.7% (the largest other-seed spread, 1.61%;
+  measured on MI355X: 0.77%), and the curve means within 5e-3 (floor 1.1e-3).
 """
 
-import math
 import time
 
-import numpy as np
 import pytest
 import torch
-import torch.nn as nn
-import torch.nn.functional as F
 
+import loss_curve_model as M
 from luma_amd import LUMA
 from luma_amd import _lib as L
 from oracle import luma_oracle as O
 
 pytestmark = pytest.mark.gpu
 
-STEPS = 1000
-EVAL_EVERY = 100
-BLOCK, BATCH = 64, 32
-N_LAYER, N_HEAD, N_EMBD = 4, 4, 128
-LR, BETAS, WD, CLIP = 3e-4, (0.9, 0.95), 0.1, 1.0
-POINT_TOL = {"injected": 1.0e-2, "native": 1.0e-2, "exact": 1e-6}
+POINT_TOL = {"injected": 1.1e-2, "native": 1.7e-2, "exact": 1e-6}
 MEAN_TOL = {"injected": 2e-3, "native": 5e-3, "exact": 1e-6}
 
 
-def synthetic_text(n_chars=400_000, seed=0):
-    """A word-level Markov chain over 300 pseudo-words, rendered as characters."""
-    rng = np.random.default_rng(seed)
-    letters = np.array(list("abcdefghijklmnopqrstuvwxyz"))
-    words = ["".join(rng.choice(letters, size=rng.integers(2, 8))) for _ in range(300)]
-    # each word has 5 likely successors (Zipf-like), plus a small uniform floor
-    trans = np.full((300, 300), 0.02 / 300)
-    for i in range(300):
-        succ = rng.choice(300, size=5, replace=False)
-        trans[i, succ] += 0.98 * np.array([0.4, 0.25, 0.15, 0.12, 0.08])
-    trans /= trans.sum(axis=1, keepdims=True)
-    out, w, total = [], 0, 0
-    while total < n_chars:
-        s = words[w] + (". " if rng.random() < 0.1 else " ")
-        out.append(s)
-        total += len(s)
-        w = rng.choice(300, p=trans[w])
-    text = "".join(out)[:n_chars]
-    chars = sorted(set(text))
-    data = torch.tensor([chars.index(c) for c in text], dtype=torch.long)
-    return data, len(chars)
-
-
-class Block(nn.Module):
-    def __init__(self):
-        super().__init__()
-        self.ln1 = nn.LayerNorm(N_EMBD)
-        self.qkv = nn.Linear(N_EMBD, 3 * N_EMBD)
-        self.proj = nn.Linear(N_EMBD, N_EMBD)
-        self.ln2 = nn.LayerNorm(N_EMBD)
-        self.fc = nn.Linear(N_EMBD, 4 * N_EMBD)
-        self.out = nn.Linear(4 * N_EMBD, N_EMBD)
-
-    def forward(self, x):
-        b, t, c = x.shape
-        q, k, v = self.qkv(self.ln1(x)).split(N_EMBD, dim=2)
-        q, k, v = (z.view(b, t, N_HEAD, c // N_HEAD).transpose(1, 2) for z in (q, k, v))
-        att = (q @ k.transpose(-2, -1).contiguous()) / math.sqrt(c // N_HEAD)
-        mask = torch.ones(t, t, device=x.device, dtype=torch.bool).tril()
-        att = att.masked_fill(~mask, float("-inf")).softmax(dim=-1)
-        y = (att @ v).transpose(1, 2).reshape(b, t, c)
-        x = x + self.proj(y)
-        return x + self.out(F.gelu(self.fc(self.ln2(x))))
-
-
-class TinyGPT(nn.Module):
-    def __init__(self, vocab):
-        super().__init__()
-        self.wte = nn.Embedding(vocab, N_EMBD)
-        self.wpe = nn.Embedding(BLOCK, N_EMBD)
-        self.blocks = nn.ModuleList(Block() for _ in range(N_LAYER))
-        self.ln_f = nn.LayerNorm(N_EMBD)
-        self.head = nn.Linear(N_EMBD, vocab, bias=False)
-        self.head.weight = self.wte.weight          # tied, as in nanoGPT
-        for m in self.modules():
-            if isinstance(m, (nn.Linear, nn.Embedding)):
-                nn.init.normal_(m.weight, 0.0, 0.02)
-            if isinstance(m, nn.Linear) and m.bias is not None:
-                nn.init.zeros_(m.bias)
-
-    def forward(self, idx, targets):
-        x = self.wte(idx) + self.wpe(torch.arange(idx.shape[1], device=idx.device))
-        for blk in self.blocks:
-            x = blk(x)
-        logits = self.head(self.ln_f(x))
-        return F.cross_entropy(logits.view(-1, logits.shape[-1]), targets.view(-1))
-
-
-def _groups(params, lr=LR):
-    decay = [p for p in params if p.dim() >= 2]
-    no_decay = [p for p in params if p.dim() < 2]
-    return [dict(params=decay, lr=lr, betas=BETAS, eps=1e-8, weight_decay=WD),
-            dict(params=no_decay, lr=lr, betas=BETAS, eps=1e-8, weight_decay=0.0)]
-
-
-def _batches(data, seed):
-    g = torch.Generator().manual_seed(seed)
-    while True:
-        ix = torch.randint(len(data) - BLOCK - 1, (BATCH,), generator=g)
-        x = torch.stack([data[i:i + BLOCK] for i in ix])
-        y = torch.stack([data[i + 1:i + BLOCK + 1] for i in ix])
-        yield x.cuda(), y.cuda()
-
-
-@torch.no_grad()
-def _eval(model, batches):
-    return sum(float(model(x, y)) for x, y in batches) / len(batches)
-
-
 def _run(inject, exact=False):
-    torch.manual_seed(1234)
-    data, vocab = synthetic_text()
-    split = int(0.9 * len(data))
-    train, val = data[:split], data[split:]
-    gen = _batches(val, 99)
-    val_batches = [next(gen) for _ in range(4)]
-
-    model_a = TinyGPT(vocab).cuda()
-    model_b = TinyGPT(vocab).cuda()
+    model_a, train, val_batches = M.setup("cuda")
+    # a second model initialised as the first was (drawing from the global
+    # generator, which LUMA's _base_seed draw follows), then made equal to it
+    model_b = M.TinyGPT(model_a.wte.num_embeddings).cuda()
     model_b.load_state_dict(model_a.state_dict())
     params_a = list(model_a.parameters())
     params_b = list(model_b.parameters())
     cpu_b = [p.detach().cpu().clone() for p in params_b]
 
-    opt = LUMA(_groups(params_a))
+    opt = LUMA(M.groups(params_a))
     if exact:
         opt._flags = L.FLAG_EXACT_ONLY
-    oracle = O.OracleLUMA(_groups(cpu_b), opt._base_seed, math_mode="cr")
+    oracle = O.OracleLUMA(M.groups(cpu_b), opt._base_seed, math_mode="cr")
     order_a = [p for g in opt.param_groups for p in g["params"]]
 
     curve = []
-    batches = _batches(train, 7)
+    batches = M.batches(train, 7, "cuda")
     t0 = time.time()
-    for step in range(1, STEPS + 1):
+    for step in range(1, M.STEPS + 1):
         x, y = next(batches)
         for model in (model_a, model_b):
             model.zero_grad(set_to_none=True)
             model(x, y).backward()
-            torch.nn.utils.clip_grad_norm_(model.parameters(), CLIP)
+            torch.nn.utils.clip_grad_norm_(model.parameters(), M.CLIP)
         for pb, cb in zip(params_b, cpu_b):
             cb.grad = pb.grad.detach().cpu()
         oracle.step()
@@ -192,8 +88,8 @@ def _run(inject, exact=False):
         with torch.no_grad():
             for pb, cb in zip(params_b, cpu_b):
                 pb.copy_(cb)
-        if step % EVAL_EVERY == 0:
-            la, lb = _eval(model_a, val_batches), _eval(model_b, val_batches)
+        if step % M.EVAL_EVERY == 0:
+            la, lb = M.evaluate(model_a, val_batches), M.evaluate(model_b, val_batches)
             curve.append((step, la, lb))
             print(f"step {step}: HIP {la:.4f} oracle {lb:.4f} rel {abs(la - lb) / lb:.2e} "
                   f"({time.time() - t0:.0f}s)", flush=True)
