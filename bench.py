@@ -1,14 +1,24 @@
 """Benchmark of the LUMA optimizer step on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config llama3_8b]
+                    [--no-cpu] [--no-others]
 
 A step is one ``LUMA.step()`` over the whole synthetic parameter set with
-gradients already resident in HBM.  Prints one JSON line with:
-  value        Gparams/s of the whole step (params / ms_per_step)
+gradients already resident in HBM.  Two gradient sets, drawn independently
+from the workload's distribution, alternate through the warm-up and timed
+steps, so that every step sees fresh gradients.  Prints one JSON line with:
+  value        Gparams/s of the whole step (params / ms_per_step) on the
+               headline workload (the 8B-parameter Llama-3-shaped set)
   roofline     the dominant kernel's algorithmic HBM bytes per launch over its
                average launch time (HIP events on the launch stream) vs 8 TB/s
   cpu_baseline the CPU oracle (the reference's PyTorch backend restated) timed
                on this host on a bounded sample of the same workload
+  other_configs  (default run) the single 4096x4096 tensor, the GPT-2-small list
+               and the 20,000-tensor set at their stated step counts: step time
+               from HIP events around each step() (the gradient switch between
+               steps is host work outside them), Gparams/s, the reference
+               bytes model's fraction of 8 TB/s, and each one's CPU baseline
+               on its whole parameter set
 Bytes per parameter (G = gradient element size):
   reference algorithm  pass 1 reads grad + Q_m + Q_w (G + 4), pass 2 reads grad +
                        Q_m + Q_w + param and writes Q_m + Q_w + param (G + 16):
@@ -85,7 +95,11 @@ CONFIGS = {
 }
 
 
-def make_set(cfg, device):
+def make_set(cfg, device, grad_sets=2):
+    """Parameters and `grad_sets` gradient sets of a configuration (each set
+    drawn afresh from the configuration's distribution); the steps of a run
+    cycle through the sets, so that no two consecutive steps see the same
+    gradients."""
     shapes = cfg["shapes"]()
     torch.manual_seed(0)
     stds = None
@@ -94,31 +108,33 @@ def make_set(cfg, device):
         gen = torch.Generator().manual_seed(seed)
         stds = torch.exp(torch.empty(len(shapes), dtype=torch.float64)
                          .uniform_(math.log(lo), math.log(hi), generator=gen)).tolist()
-    params, grads = [], []
-    for i, s in enumerate(shapes):
+    params = []
+    for s in shapes:
         p = torch.randn(s, device=device) * 0.02
         if len(s) == 1 and cfg["shapes"] is not many_small_shapes:
             p.fill_(1.0)                             # norm weights
-        if stds is not None:
-            # GradScaler: the backward pass produces grads scaled by 2^16 in fp16,
-            # unscale_ multiplies by 2^-16 in fp32 and stores fp16 again
-            g16 = (torch.randn(s, device=device) * (stds[i] * 2.0 ** 16)).half()
-            g = g16.float() * 2.0 ** -16
-            p.requires_grad_(True)
-            p.grad_dtype = None
-            params.append(p)
-            grads.append(g.half())
-            continue
-        g = torch.randn(s, device=device) * cfg["std"]
-        if cfg.get("outliers"):
-            g = torch.where(torch.rand(s, device=device) < cfg["outliers"], g * 100.0, g)
-        if cfg.get("zeros"):
-            g = torch.where(torch.rand(s, device=device) < cfg["zeros"], torch.zeros_like(g), g)
         p.requires_grad_(True)
         p.grad_dtype = None        # allow bf16 / fp16 grads on fp32 params
         params.append(p)
-        grads.append(g.to(cfg["grad"]))
-    return params, grads
+    sets = []
+    for k in range(grad_sets):
+        torch.manual_seed(1000 + k)
+        grads = []
+        for i, s in enumerate(shapes):
+            if stds is not None:
+                # GradScaler: the backward pass produces grads scaled by 2^16 in
+                # fp16, unscale_ multiplies by 2^-16 in fp32 and stores fp16 again
+                g16 = (torch.randn(s, device=device) * (stds[i] * 2.0 ** 16)).half()
+                grads.append((g16.float() * 2.0 ** -16).half())
+                continue
+            g = torch.randn(s, device=device) * cfg["std"]
+            if cfg.get("outliers"):
+                g = torch.where(torch.rand(s, device=device) < cfg["outliers"], g * 100.0, g)
+            if cfg.get("zeros"):
+                g = torch.where(torch.rand(s, device=device) < cfg["zeros"], torch.zeros_like(g), g)
+            grads.append(g.to(cfg["grad"]))
+        sets.append(grads)
+    return params, sets
 
 
 # ── CPU baseline: the oracle on a bounded sample ─────────────────────────────
@@ -148,45 +164,69 @@ def cpu_model():
     return ""
 
 
-def cpu_baseline(cfg_name, warmup=2, timed=5):
-    """The oracle in the reference's own math ("torch": ATen's CPU kernels) on
-    the configuration's largest tensor, with every core this process may use:
-    the init step and warmup - 1 update steps untimed, then the median of
-    ``timed`` update steps (time.perf_counter around each step)."""
+def _cpu_grads(shapes, cfg, gen, n_sets=2):
+    """Gradient sets for the CPU baseline, drawn as make_set draws them."""
+    sets = []
+    for _ in range(n_sets):
+        grads = []
+        for s in shapes:
+            g = torch.randn(s, generator=gen) * cfg.get("std", 1e-3)
+            if cfg.get("outliers"):
+                g = torch.where(torch.rand(s, generator=gen) < cfg["outliers"], g * 100.0, g)
+            if cfg.get("zeros"):
+                g = torch.where(torch.rand(s, generator=gen) < cfg["zeros"], torch.zeros_like(g), g)
+            grads.append(g.to(cfg["grad"]))
+        sets.append(grads)
+    return sets
+
+
+def cpu_baseline(cfg_name, warmup=2, timed=5, whole=False):
+    """The oracle in the reference's own math ("torch": ATen's CPU kernels)
+    with every core this process may use, on the configuration's largest
+    tensor (or, with ``whole``, its whole parameter set), two gradient sets
+    alternating: the init step and warmup - 1 update steps untimed, then the
+    median of ``timed`` update steps (time.perf_counter around each step)."""
     from oracle import luma_oracle as O
 
     cores = host_cores()
     torch.set_num_threads(cores)
     cfg = CONFIGS[cfg_name]
-    shape = max(cfg["shapes"](), key=math.prod)
-    n = math.prod(shape)
+    shapes = cfg["shapes"]() if whole else [max(cfg["shapes"](), key=math.prod)]
+    n = sum(math.prod(s) for s in shapes)
     gen = torch.Generator().manual_seed(1)
-    p = torch.randn(n, generator=gen) * 0.02
-    p.grad_dtype = None
-    gdt = cfg["grad"]
-    grads = [(torch.randn(n, generator=gen) * 1e-3).to(gdt) for _ in range(2)]
-    opt = O.OracleLUMA([dict(params=[p], lr=1e-3, betas=(0.9, 0.999), eps=1e-8,
+    params = []
+    for s in shapes:
+        p = torch.randn(s, generator=gen) * 0.02
+        p.grad_dtype = None
+        params.append(p)
+    sets = _cpu_grads(shapes, cfg, gen)
+    opt = O.OracleLUMA([dict(params=params, lr=1e-3, betas=(0.9, 0.999), eps=1e-8,
                              weight_decay=0.01)], 12345, "torch")
     times = []
+    t_all = time.perf_counter()
     for i in range(warmup + timed):
-        p.grad = grads[i % 2]
+        for p, g in zip(params, sets[i % 2]):
+            p.grad = g
         t0 = time.perf_counter()
         opt.step()
         dt = time.perf_counter() - t0
         if i >= warmup:
             times.append(dt)
-        print(f"bench: cpu baseline step {i + 1}/{warmup + timed} {dt:.2f} s", file=sys.stderr,
-              flush=True)
-    times.sort()
-    med = times[len(times) // 2]
+        if i < 3 or (i + 1) % 10 == 0 or i + 1 == warmup + timed:
+            print(f"bench: cpu baseline {cfg_name} step {i + 1}/{warmup + timed} {dt:.3f} s",
+                  file=sys.stderr, flush=True)
+    total = time.perf_counter() - t_all
+    med = sorted(times)[len(times) // 2]
+    what = (f"its whole parameter set ({len(shapes)} tensors, {n} fp32 params)" if whole else
+            f"the configuration's largest tensor {tuple(shapes[0])} ({n} fp32 params)")
     return {"value": round(n / med / 1e9, 6), "unit": "Gparams/s", "cores": cores,
-            "kind": "port", "ms_per_step": round(med * 1e3, 1),
-            "sample": f"oracle (the reference's PyTorch backend restated, torch CPU ops) on the "
-                      f"configuration's largest tensor {tuple(shape)} ({n} fp32 params, "
-                      f"{str(gdt).replace('torch.', '')} grads); median of {timed} update steps "
-                      f"after the init step and {warmup - 1} untimed update step; "
-                      f"{cores} threads (all cores this process may use; os.cpu_count() "
-                      f"{os.cpu_count()}); {cpu_model()}"}
+            "kind": "port", "ms_per_step": round(med * 1e3, 2),
+            "steps": warmup + timed, "total_s": round(total, 1),
+            "sample": f"oracle (the reference's PyTorch backend restated, torch CPU ops) on "
+                      f"{what}, {str(cfg['grad']).replace('torch.', '')} grads, two gradient "
+                      f"sets alternating; median of {timed} update steps after the init step "
+                      f"and {warmup - 1} untimed update step(s); {cores} threads (all cores "
+                      f"this process may use; os.cpu_count() {os.cpu_count()}); {cpu_model()}"}
 
 
 # ── bytes model ───────────────────────────────────────────────────────────────
@@ -197,17 +237,23 @@ def chunk_elems(shapes):
     import numpy as np
     from luma_amd.optimizer import _Engine
     numels = np.array([math.prod(s) for s in shapes], dtype=np.int64)
-    eng = types.SimpleNamespace(chunk_elems=0, small_tensors=True)
+    eng = types.SimpleNamespace(chunk_elems=0, small_tensors=True, medium_tensors=True)
     eng._small_limit = lambda: _Engine._small_limit(eng)
+    eng._medium_limit = lambda: _Engine._medium_limit(eng)
+    eng._wave_limit = lambda: _Engine._wave_limit(eng)
     return _Engine.chunk_for(eng, numels)
 
 
 def pass1_bytes(cfg, n_params, gbytes):
     """Pass 1's algorithmic bytes per launch in steady state: the gradients
-    and one 4-byte summary word per thread (256) of every chunk."""
+    and one 4-byte summary word per thread (256) of every chunk of the
+    tensors that keep summaries (above the single-wavefront routes and at
+    least one whole 2048-element iteration)."""
+    from luma_amd import _lib as L
     shapes = cfg["shapes"]()
     c = chunk_elems(shapes)
-    words = sum(-(-math.prod(s) // c) * 256 for s in shapes)
+    least = max(2048, max(L.SMALL_TENSOR, L.MEDIUM_TENSOR) + 1)
+    words = sum(-(-math.prod(s) // c) * 256 for s in shapes if math.prod(s) >= least)
     return n_params * gbytes + 4 * words
 
 
@@ -437,13 +483,97 @@ def read_traffic(config, kernel):
 
 # ── main ─────────────────────────────────────────────────────────────────────
 
+GRAD_SETS = 2            # gradient sets that alternate through every run's steps
+# the other BASELINE workloads timed by the default run (name, timed steps:
+# the step counts the workloads are stated with), and their CPU baselines on
+# the whole parameter set (untimed warm-up steps incl. the init step, timed)
+OTHER_CONFIGS = (("single_4096", 100), ("gpt2_small", 200), ("many_small", 100))
+OTHER_CPU = {"single_4096": (1, 99), "gpt2_small": (1, 10), "many_small": (1, 10)}
+
+
+def run_gpu(name, steps, warmup, dev, grad_sets=GRAD_SETS):
+    """Time `steps` LUMA steps of workload `name` after `warmup` untimed ones.
+    The steps run back to back, as in a training loop; before each, the
+    gradients switch to the next of GRAD_SETS sets (host work outside the
+    timed events).  Per step: an event before step() and the four the step
+    records around its kernels.  Returns the wall time per step (every
+    step between two synchronisations), the mean event time per step, and
+    the mean time of pass 1, finalize and pass 2."""
+    from luma_amd import LUMA
+
+    cfg = CONFIGS[name]
+    params, sets = make_set(cfg, dev, grad_sets)
+    n_params = sum(p.numel() for p in params)
+    gbytes = torch.tensor([], dtype=cfg["grad"]).element_size()
+    print(f"bench: {name} {len(params)} tensors {n_params} params", file=sys.stderr, flush=True)
+
+    def use(i):
+        for p, g in zip(params, sets[i % grad_sets]):
+            p.grad = g
+
+    opt = LUMA(params, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01)
+    i = 0
+    for _ in range(warmup):
+        use(i)
+        opt.step()
+        i += 1
+    torch.cuda.synchronize()
+    if cfg.get("restore"):
+        # resume from a checkpoint: the timed steps run on a fresh optimizer
+        sd = opt.state_dict()
+        opt = LUMA(params, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01)
+        opt.load_state_dict(sd)
+        del sd
+        use(i)
+        opt.step()
+        i += 1
+        torch.cuda.synchronize()
+    print(f"bench: {name} warmup done", file=sys.stderr, flush=True)
+
+    # five events per timed step: before step(), then before pass 1, after
+    # pass 1, after finalize, after pass 2 (recorded by the step itself)
+    ev_sets = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(steps)]
+    for es in ev_sets:
+        for e in es:
+            e.record()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for es in ev_sets:
+        use(i)
+        i += 1
+        es[0].record()
+        opt._engine.profile_events = es[1:]
+        opt.step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    opt._engine.profile_events = None
+    k_times = [[es[k + 1].elapsed_time(es[k + 2]) for es in ev_sets] for k in range(3)]
+    ev_ms = sum(es[0].elapsed_time(es[4]) for es in ev_sets) / steps
+    avg = [sum(v) / len(v) for v in k_times]
+    print(f"bench: {name} kernel ms pass1 {avg[0]:.3f} finalize {avg[1]:.3f} pass2 {avg[2]:.3f}; "
+          f"step {wall * 1e3 / steps:.3f} ms wall, {ev_ms:.3f} ms events",
+          file=sys.stderr, flush=True)
+    out = {"params": n_params, "tensors": len(params), "gbytes": gbytes,
+           "wall_ms": wall * 1e3 / steps, "event_ms": ev_ms, "kernel_avg": avg}
+    del opt, params, sets
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="llama3_8b", choices=sorted(CONFIGS))
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--grad-sets", type=int, default=GRAD_SETS,
+                    help="gradient sets that alternate through the steps (1: the same "
+                         "gradients every step)")
+    ap.add_argument("--no-others", dest="others", action="store_false",
+                    help="time the headline workload only (default: also the single 4096^2 "
+                         "tensor, the GPT-2-small list and the 20,000-tensor set)")
     ap.add_argument("--ceilings", action="store_true",
                     help="time torch's copy and max over 16 GiB (achievable HBM rates)")
     ap.add_argument("--copy-calibration", type=int, metavar="REPS",
@@ -477,50 +607,11 @@ def main():
               "the LUMA step is rank-local and shards with no exchange", file=sys.stderr)
         sys.exit(2)
 
-    from luma_amd import LUMA
-
-    cfg = CONFIGS[args.config]
+    t_start = time.perf_counter()
     dev = torch.device("cuda:0")
-    params, grads = make_set(cfg, dev)
-    n_params = sum(p.numel() for p in params)
-    gbytes = torch.tensor([], dtype=cfg["grad"]).element_size()
-    opt = LUMA(params, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01)
-    for p, g in zip(params, grads):
-        p.grad = g
-    print(f"bench: {args.config} {len(params)} tensors {n_params} params", file=sys.stderr, flush=True)
-
-    for _ in range(args.warmup):
-        opt.step()
-    torch.cuda.synchronize()
-    if cfg.get("restore"):
-        # resume from a checkpoint: the timed steps run on a fresh optimizer
-        sd = opt.state_dict()
-        opt = LUMA(params, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01)
-        opt.load_state_dict(sd)
-        del sd
-        opt.step()
-        torch.cuda.synchronize()
-    print("bench: warmup done", file=sys.stderr, flush=True)
-
-    # one set of four events per timed step (before pass 1, after pass 1,
-    # after finalize, after pass 2), so that the steps run back to back as
-    # in a training loop, with no synchronisation between them
-    ev_sets = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
-    for es in ev_sets:
-        for e in es:
-            e.record()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for es in ev_sets:
-        opt._engine.profile_events = es
-        opt.step()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    opt._engine.profile_events = None
-    k_times = [[es[k].elapsed_time(es[k + 1]) for es in ev_sets] for k in range(3)]
-    ms = wall * 1e3 / args.steps
-
-    avg = [sum(v) / len(v) for v in k_times]
+    head = run_gpu(args.config, args.steps, args.warmup, dev, args.grad_sets)
+    cfg = CONFIGS[args.config]
+    n_params, gbytes, avg, ms = head["params"], head["gbytes"], head["kernel_avg"], head["wall_ms"]
     pass_bytes = [pass1_bytes(cfg, n_params, gbytes), 0, n_params * (gbytes + 16)]
     dom = 0 if avg[0] > avg[2] else 2
     achieved = pass_bytes[dom] / (avg[dom] * 1e-3)
@@ -528,11 +619,31 @@ def main():
     step_gbps = step_bytes / (ms * 1e-3)
     ref_gbps = n_params * (2 * gbytes + 20) / (ms * 1e-3)
     names = ["luma_pass1", "luma_finalize", "luma_pass2"]
-    print(f"bench: kernel ms pass1 {avg[0]:.3f} finalize {avg[1]:.3f} pass2 {avg[2]:.3f}; "
-          f"step {ms:.3f} ms", file=sys.stderr, flush=True)
-
     traffic, traffic_src = read_traffic(args.config, "luma::" + names[dom][5:])
+
+    others = {}
+    if args.others and args.config == "llama3_8b":
+        # the other BASELINE workloads at their stated step counts, after the
+        # headline's memory is released
+        for name, steps in OTHER_CONFIGS:
+            r = run_gpu(name, steps, 3, dev)
+            o = CONFIGS[name]
+            ref_bytes = r["params"] * (2 * r["gbytes"] + 20)
+            others[name] = {
+                "workload": o["desc"], "params": r["params"], "tensors": r["tensors"],
+                "steps": steps, "warmup": 3,
+                "ms_per_step": round(r["event_ms"], 4),
+                "wall_ms_per_step": round(r["wall_ms"], 4),
+                "gparams_s": round(r["params"] / (r["event_ms"] * 1e-3) / 1e9, 2),
+                "reference_model_gbps": round(ref_bytes / (r["event_ms"] * 1e-3) / 1e9, 1),
+                "reference_model_frac": round(ref_bytes / (r["event_ms"] * 1e-3) / HBM_PEAK, 4),
+                "kernel_ms": {names[i]: round(r["kernel_avg"][i], 4) for i in range(3)},
+            }
     cpu = None if args.no_cpu else cpu_baseline(args.config)
+    if not args.no_cpu:
+        for name, (warm, timed) in OTHER_CPU.items():
+            if name in others:
+                others[name]["cpu_baseline"] = cpu_baseline(name, warm, timed, whole=True)
     out = {
         "metric": METRIC,
         "value": round(n_params / (ms * 1e-3) / 1e9, 3),
@@ -546,13 +657,15 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": cfg["desc"], "params": n_params, "tensors": len(params),
+        "config": {"workload": cfg["desc"], "params": n_params, "tensors": head["tensors"],
                    "grad_dtype": str(cfg["grad"]).replace("torch.", ""),
+                   "grad_sets": args.grad_sets,
                    "bytes_per_param": round(step_bytes / n_params, 3),
                    "reference_bytes_per_param": 2 * gbytes + 20},
         "step_hbm_gbps": round(step_gbps / 1e9, 1),
         "step_hbm_frac": round(step_gbps / HBM_PEAK, 4),
         "step_reference_model_gbps": round(ref_gbps / 1e9, 1),
+        "step_reference_model_frac": round(ref_gbps / HBM_PEAK, 4),
         "kernel_ms": {names[i]: round(avg[i], 4) for i in range(3)},
         "roofline": {"bound": "hbm", "kernel": names[dom],
                      "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9,
@@ -562,6 +675,9 @@ def main():
                      "algorithmic_bytes": pass_bytes[dom]},
         "cpu_baseline": cpu,
     }
+    if others:
+        out["other_configs"] = others
+    out["bench_wall_s"] = round(time.perf_counter() - t_start, 1)
     print(json.dumps(out), flush=True)
 
 

@@ -57,7 +57,7 @@
 extern "C" {
 #endif
 
-#define LUMA_ABI_VERSION 8
+#define LUMA_ABI_VERSION 9
 
 /*
  * Elements per chunk-table entry (one workgroup's share of a tensor): the
@@ -75,6 +75,13 @@ extern "C" {
  * its time in set-up.
  */
 #define LUMA_SMALL_TENSOR 512
+
+/*
+ * Tensors above LUMA_SMALL_TENSOR and of at most this many elements are best
+ * stepped by a workgroup of one wavefront each (LumaStepArgs.medium_chunks):
+ * a workgroup of four would leave most of its wavefronts idle on them.
+ */
+#define LUMA_MEDIUM_TENSOR 4096
 
 /*
  * Bytes of one slot: a tensor's persistent device state (step count, S_m,
@@ -184,7 +191,7 @@ typedef struct LumaStepArgs {
   int32_t n_chunks;
   const LumaChunk *chunks;   /* device */
   const LumaGroup *groups;   /* device */
-  float *partials;           /* device workspace, luma_workspace_bytes(n_chunks) */
+  float *partials;           /* device workspace, luma_workspace_bytes(n_chunks), 16-byte aligned */
   uint64_t base_seed;        /* LUMA._base_seed as its two's-complement bits */
   int32_t noise_mode;        /* LUMA_NOISE_* */
   int32_t flags;             /* LUMA_FLAG_* */
@@ -195,6 +202,14 @@ typedef struct LumaStepArgs {
                                 per workgroup) by the exact path; meant for tensors of at
                                 most LUMA_SMALL_TENSOR elements (any tensor is stepped
                                 correctly).  0: every chunk takes a workgroup */
+  int32_t medium_chunks;     /* the medium_chunks records just before the small ones
+                                are stepped by a workgroup of one wavefront each (the
+                                same fast kernels as the others, 8 elements per lane and
+                                iteration); meant for tensors of at most
+                                LUMA_MEDIUM_TENSOR elements, one chunk each (any chunk is
+                                stepped correctly).  Such tensors keep no code summaries.
+                                0: none */
+  int32_t reserved;          /* 0 */
   LumaScaling scaling;       /* both NULL: unscaled gradients, always step */
 } LumaStepArgs;
 
@@ -227,9 +242,11 @@ int64_t luma_summary_words(int64_t numel, int32_t chunk_elems);
  * per-chunk maxima), per-tensor finalize (new S_m/S_v and grid in float64,
  * step count + 1, step scalars), pass 2 (re-decode + EMA + AdamW update +
  * LogSR re-quantisation).  A tensor whose slot holds step count 0 takes the
- * init step.  Three to five kernel launches on `stream` (a hipStream_t), no host
- * synchronisation; no device table is written, so the sequence may be
- * captured into a HIP graph and replayed.
+ * init step.  Three kernel launches on `stream` (a hipStream_t), plus one
+ * per pass for the medium tensors (medium_chunks > 0) and one per pass for
+ * the small tensors (small_chunks > 0), which follow the workgroup kernels;
+ * no host synchronisation.  No device table is written, so the sequence may
+ * be captured into a HIP graph and replayed.
  */
 int luma_step(const LumaStepArgs *args, void *stream);
 

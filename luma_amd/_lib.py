@@ -19,11 +19,12 @@ LIB_PATH = os.path.join(HERE, LIB_NAME)
 CHUNK_ELEMS = 131072         # LUMA_CHUNK_ELEMS (default and largest chunk length)
 CHUNK_ELEMS_MIN = 2048       # LUMA_CHUNK_ELEMS_MIN
 SMALL_TENSOR = 512           # LUMA_SMALL_TENSOR
+MEDIUM_TENSOR = 4096         # LUMA_MEDIUM_TENSOR
 STEP_TENSOR_CHUNK_MIN = 16384  # LUMA_STEP_TENSOR_CHUNK_MIN
 SLOT_BYTES = 512             # LUMA_SLOT_BYTES
 NOALLOC_MAX_CHUNKS = 262144  # LUMA_NOALLOC_MAX_CHUNKS
 SUMMARY_WORDS = 256          # LUMA_SUMMARY_WORDS (per chunk)
-ABI_VERSION = 8              # LUMA_ABI_VERSION
+ABI_VERSION = 9              # LUMA_ABI_VERSION
 
 GRAD_F32, GRAD_BF16, GRAD_F16 = 0, 1, 2
 NOISE_PHILOX, NOISE_INJECTED = 0, 1
@@ -65,6 +66,8 @@ class StepArgs(ctypes.Structure):
         ("flags", ctypes.c_int32),
         ("chunk_elems", ctypes.c_int32),
         ("small_chunks", ctypes.c_int32),
+        ("medium_chunks", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
         ("scaling", Scaling),
     ]
 
@@ -124,13 +127,27 @@ def load(path: str = LIB_PATH):
 
 def load_host():
     """The host bookkeeping module (luma_amd/_luma_host*.so, built with the
-    library): pointer refresh of a re-used step table and the step counts."""
+    library): pointer refresh of a re-used step table and the step counts.
+    None (with a warning) when it is missing or was built against another
+    torch (it reads tensor fields in its build's layout): the optimizer then
+    rebuilds its step table on every step, which is slower for large
+    parameter lists but gives the same results."""
+    import warnings
+
+    import torch
+
     try:
         from . import _luma_host
     except ImportError as e:
-        raise LumaLibraryError(
-            "luma_amd._luma_host not found or not loadable; build it with "
-            "`python -c 'import luma_amd.build as b; b.build()'`") from e
+        warnings.warn(f"luma_amd._luma_host not loadable ({e}); LUMA rebuilds its step table "
+                      "every step.  Build it with `python -m luma_amd.build`.")
+        return None
+    built = getattr(_luma_host, "torch_version", None)
+    if built != torch.__version__:
+        warnings.warn(f"luma_amd._luma_host was built against torch {built}, this is torch "
+                      f"{torch.__version__}: not used (LUMA rebuilds its step table every "
+                      "step).  Rebuild it with `python -m luma_amd.build`.")
+        return None
     return _luma_host
 
 

@@ -64,6 +64,7 @@ def host_command():
     abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
     return [shutil.which("g++") or "g++", "-O2", "-std=c++17", "-fPIC", "-shared",
             f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-DTORCH_EXTENSION_NAME=_luma_host",
+            f'-DLUMA_TORCH_VERSION="{torch.__version__}"',
             "-I", inc, "-I", os.path.join(inc, "torch", "csrc", "api", "include"),
             "-I", sysconfig.get_paths()["include"], HOST_SOURCE,
             "-L", os.path.join(tdir, "lib"), "-Wl,-rpath," + os.path.join(tdir, "lib"),

@@ -57,10 +57,7 @@ struct Slot {
   int64_t seed_m, seed_v;
   int32_t summ_shift;   // log2 of the chunk length the code summaries were written with
   int32_t reserved2;
-  // |m'| and v' of the two seeds at step seed_t, evaluated exactly before
-  // that step's pass 1 (seed_t != the running step: not evaluated)
-  float seed_xm, seed_xv;
-  int64_t seed_t;
+  uint8_t reserved3[16];
   uint8_t pad[LUMA_SLOT_BYTES - 88 - 2 * sizeof(Grid) - 24 - 16];
 };
 static_assert(sizeof(Hyper) == 40, "hyper layout");

@@ -102,15 +102,22 @@ int check_range(const Plan &P, int64_t a, int64_t b, int64_t ra, int64_t rb) noe
         prefetch_impl(gimpl[P.row_param[r + kAhead] - a]);
       const int64_t j = P.row_param[r] - a;
       const c10::TensorImpl *p = pimpl[j], *g = gimpl[j];
-      if (!g || grad_code(g->dtype().toScalarType()) != P.grad_dtype[r]) return 0;
+      if (!g) return 0;
+      // A tensor subclass (e.g. a DTensor) handles its own dispatch, and one
+      // with a custom device or sizes policy answers is_cuda(), device(),
+      // dim() and sizes() in Python, which needs the GIL that the calling
+      // thread holds while the workers run: so the key set (a plain field)
+      // is checked before anything else is asked of either tensor.
+      if (g->key_set().has(c10::DispatchKey::Python) || p->key_set().has(c10::DispatchKey::Python) ||
+          g->key_set().has(c10::DispatchKey::PythonTLSSnapshot) ||
+          p->key_set().has(c10::DispatchKey::PythonTLSSnapshot))
+        return 0;
+      if (grad_code(g->dtype().toScalarType()) != P.grad_dtype[r]) return 0;
       if (p->dtype().toScalarType() != at::kFloat || !p->is_cuda() || !g->is_cuda() ||
           p->device().index() != P.device || g->device().index() != P.device)
         return 0;
       if (g->layout() != at::kStrided || p->layout() != at::kStrided || g->is_neg() ||
           p->is_neg())
-        return 0;
-      // a tensor subclass (e.g. a DTensor) handles its own dispatch
-      if (g->key_set().has(c10::DispatchKey::Python) || p->key_set().has(c10::DispatchKey::Python))
         return 0;
       const int64_t *lay = P.layout + P.layout_at[r];
       const int64_t nd = lay[0];
@@ -257,4 +264,7 @@ PYBIND11_MODULE(_luma_host, m) {
   Py_INCREF(g_param_type);
   m.def("refresh", &refresh);
   m.def("bump_steps", &bump_steps);
+  // the torch whose headers this module was compiled against: it reads
+  // TensorImpl fields in that version's inline layout
+  m.attr("torch_version") = LUMA_TORCH_VERSION;
 }

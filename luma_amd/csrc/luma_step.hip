@@ -11,9 +11,11 @@
 //   pass 2   (grid = chunks)  recompute m', v' bit-identically, AdamW update of
 //                             the parameter, LogSR re-quantisation on the new
 //                             grid (functional.py:278-279, 293-295).
-// Nothing is materialised between the passes except 8 bytes per chunk.  With
-// GradScaler's scaling (LumaScaling) every kernel unscales the gradients as
-// it loads them, and returns at once when the overflow flag is set.
+// Tensors of at most LUMA_SMALL_TENSOR elements take a kernel of their own in
+// each pass (a wavefront per tensor).  Nothing is materialised between the
+// passes except 16 bytes per chunk.  With GradScaler's scaling (LumaScaling)
+// every kernel unscales the gradients as it loads them, and returns at once
+// when the overflow flag is set.
 //
 // Both passes take each rounding decision from fast float32 arithmetic when an
 // error bound proves it equal to the exact path's (luma_fast.h), and queue
@@ -77,7 +79,12 @@ static_assert(sizeof(Tensor) == sizeof(LumaTensor), "tensor layout");
 
 // Where a launch finds its tensors: the device tables of luma_step, or (when
 // `tensors` is null) the single tensor and group passed by value by
-// luma_step_tensor, whose chunks are then the workgroups in order.
+// luma_step_tensor, whose chunks are then the workgroups in order.  The
+// chunk records come in three runs: [0, medium_from) take a workgroup of
+// kThreads each, [medium_from, small_from) a workgroup of one wavefront
+// each (medium tensors, through the same kernels), [small_from, n_chunks)
+// the wavefront-per-tensor exact kernels (small tensors).  A launch over
+// one run starts at record chunk_base.
 struct StepSrc {
   const Tensor *tensors;
   const LumaChunk *chunks;
@@ -89,6 +96,8 @@ struct StepSrc {
   int32_t summaries;     // this launch's pass 2 writes the code summaries
   int32_t small_from;    // chunks from here on: small tensors, one wavefront each
   int32_t n_chunks;
+  int32_t medium_from;   // chunks from here on (to small_from): medium tensors
+  int32_t chunk_base;    // record of this launch's workgroup 0
 };
 
 // Elements [beg, end) of chunk ci of tensor T.
@@ -140,7 +149,7 @@ __device__ __forceinline__ float unscale_rt(float g, float inv, int dt) {
 __device__ __forceinline__ void chunk_job(const StepSrc &src, Tensor &T, LumaGroup &g,
                                           int64_t &index) {
   if (src.tensors) {
-    const LumaChunk c = src.chunks[blockIdx.x];
+    const LumaChunk c = src.chunks[src.chunk_base + blockIdx.x];
     T = src.tensors[c.tensor];
     g = src.groups[T.group];
     index = c.index;
@@ -202,7 +211,7 @@ __device__ __forceinline__ void block_max2(float &a, float &b) {
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int i = 1; i < kThreads / 64; ++i) {
+    for (int i = 1; i < (int)(blockDim.x >> 6); ++i) {
       a = nan_max(a, sa[i]);
       b = nan_max(b, sb[i]);
     }
@@ -262,7 +271,7 @@ __device__ __forceinline__ void block_argmax2(float &a, uint32_t &ia, float &b, 
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int k = 1; k < kThreads / 64; ++k) {
+    for (int k = 1; k < (int)(blockDim.x >> 6); ++k) {
       if (beats(sa[k], a)) {
         a = sa[k];
         ia = sia[k];
@@ -273,6 +282,96 @@ __device__ __forceinline__ void block_argmax2(float &a, uint32_t &ia, float &b, 
       }
     }
   }
+}
+
+// S' = max(max, floor) with Python's max() semantics (a NaN maximum stays NaN).
+__device__ __forceinline__ double py_max(double a, double floor_) { return floor_ > a ? floor_ : a; }
+
+// The per-tensor stage of a step, one wavefront per tensor after pass 1:
+// reduce the tensor's chunk records to S_m', S_v' (functional.py:282-284;
+// init 217-219), derive the new grid in float64 (functional.py:74-92),
+// advance the step count, derive the step's scalars (functional.py:209-213,
+// 262-264), and keep the maxima's elements as the next step's seeds.
+__device__ __forceinline__ void finalize_tensor(const StepSrc &src, const Tensor &T,
+                                                const LumaGroup &grp, const float *partials) {
+  const uint32_t lane = lane_id();
+  const int nch = (int)(((T.numel - 1) >> src.chunk_shift) + 1);
+  float am = 0.0f, av = 0.0f;
+  uint32_t cm = kNoArg, cv = kNoArg;   // chunk (within the tensor) of each maximum
+  // each lane reads its records 16 bytes at a time, four loads in flight
+  // (the loop is latency-bound: a tensor of a few thousand chunks reads
+  // them in a few round trips instead of one per 64 records)
+  const vf4 *rec = (const vf4 *)(partials + kPartialWords * (int64_t)T.first_chunk);
+  auto fold = [&](const vf4 &r, int i) {
+    if (beats(r.x, am)) {
+      am = r.x;
+      cm = (uint32_t)i;
+    }
+    if (beats(r.y, av)) {
+      av = r.y;
+      cv = (uint32_t)i;
+    }
+  };
+  int i = (int)lane;
+  for (; i + 3 * 64 < nch; i += 4 * 64) {
+    const vf4 r0 = rec[i], r1 = rec[i + 64], r2 = rec[i + 128], r3 = rec[i + 192];
+    fold(r0, i);
+    fold(r1, i + 64);
+    fold(r2, i + 128);
+    fold(r3, i + 192);
+  }
+  for (; i < nch; i += 64) fold(rec[i], i);
+  wave_argmax(am, cm);
+  wave_argmax(av, cv);
+  if (lane == 0) {
+    // the seeds: chunk * C + the offset pass 1 recorded in that chunk
+    auto seed = [&](uint32_t c, int word) -> int64_t {
+      if (c == kNoArg) return -1;
+      const uint32_t off =
+          __float_as_uint(partials[kPartialWords * ((int64_t)T.first_chunk + c) + word]);
+      return off == kNoArg ? -1 : ((int64_t)c << src.chunk_shift) + off;
+    };
+    const int64_t seed_m = seed(cm, 2), seed_v = seed(cv, 3);
+    const double s_m = py_max((double)am, 1e-9);  // SCALE_FLOOR_M (config.py:25)
+    const double s_v = py_max((double)av, 0.0);
+    LUMA_GLOBAL Slot &s = *T.slot;
+    const int64_t t = s.step + 1;
+    const int par = (int)(t & 1);
+    const Hyper h = step_hyper(grp, t);
+    s.s_m[par] = s_m;
+    s.s_v[par] = s_v;
+    Grid g;
+    make_grid(s_m, s_v, grp.eps, g);
+    make_fast(g, h.eps);
+    s.grid[par] = g;
+    s.hyp = h;
+    s.step = t;
+    // (only the kThreads-workgroup route writes summaries)
+    s.summ_step = (src.summaries && T.summary && T.first_chunk < src.medium_from) ? t : 0;
+    s.summ_shift = src.chunk_shift;
+    s.seed_m = seed_m;
+    s.seed_v = seed_v;
+  }
+}
+
+// One wavefront per tensor, four per workgroup (fewer workgroups to
+// dispatch when there are thousands of small tensors).
+__global__ __launch_bounds__(kThreads) void finalize_kernel(StepSrc src,
+                                                            const float *__restrict__ partials,
+                                                            int32_t n_tensors) {
+  if (skip_step(src)) return;
+  const int64_t ti = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (ti >= n_tensors) return;   // no barriers below
+  Tensor T;
+  LumaGroup grp;
+  if (src.tensors) {
+    T = src.tensors[ti];
+    grp = src.groups[T.group];
+  } else {
+    T = src.one;
+    grp = src.group;
+  }
+  finalize_tensor(src, T, grp, partials);
 }
 
 // m', v' of element i of tensor T (exact path).
@@ -307,7 +406,7 @@ __global__ __launch_bounds__(kThreads) void pass1_exact_kernel(StepSrc src,
 
   float am = 0.0f, av = 0.0f;
   uint32_t im = kNoArg, iv = kNoArg;
-  for (int64_t e0 = beg + (int64_t)threadIdx.x * kVec; e0 < end; e0 += (int64_t)kThreads * kVec) {
+  for (int64_t e0 = beg + (int64_t)threadIdx.x * kVec; e0 < end; e0 += (int64_t)blockDim.x * kVec) {
     for (int j = 0; j < kVec; ++j) {
       const int64_t i = e0 + j;
       if (i >= end) break;
@@ -324,7 +423,7 @@ __global__ __launch_bounds__(kThreads) void pass1_exact_kernel(StepSrc src,
     }
   }
   block_argmax2(am, im, av, iv);
-  if (threadIdx.x == 0) put_partial(partials, blockIdx.x, am, av, im, iv);
+  if (threadIdx.x == 0) put_partial(partials, src.chunk_base + blockIdx.x, am, av, im, iv);
 }
 
 // ---------------------------------------------------------------------------
@@ -387,74 +486,6 @@ __global__ __launch_bounds__(kThreads) void pass1_small_kernel(StepSrc src,
   if (lane == 0) put_partial(partials, cidx, am, av, im, iv);
 }
 
-// S' = max(max, floor) with Python's max() semantics (a NaN maximum stays NaN).
-__device__ __forceinline__ double py_max(double a, double floor_) { return floor_ > a ? floor_ : a; }
-
-// One wavefront per tensor, four per workgroup (fewer workgroups to
-// dispatch when there are thousands of small tensors).
-__global__ __launch_bounds__(kThreads) void finalize_kernel(StepSrc src,
-                                                            const float *__restrict__ partials,
-                                                            int32_t n_tensors) {
-  if (skip_step(src)) return;
-  const int64_t ti = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
-  if (ti >= n_tensors) return;   // no barriers below
-  Tensor T;
-  LumaGroup grp;
-  if (src.tensors) {
-    T = src.tensors[ti];
-    grp = src.groups[T.group];
-  } else {
-    T = src.one;
-    grp = src.group;
-  }
-  const uint32_t lane = lane_id();
-  const int nch = (int)(((T.numel - 1) >> src.chunk_shift) + 1);
-  float am = 0.0f, av = 0.0f;
-  uint32_t cm = kNoArg, cv = kNoArg;   // chunk (within the tensor) of each maximum
-  for (int i = (int)lane; i < nch; i += 64) {
-    const float *p = partials + kPartialWords * ((int64_t)T.first_chunk + i);
-    if (beats(p[0], am)) {
-      am = p[0];
-      cm = (uint32_t)i;
-    }
-    if (beats(p[1], av)) {
-      av = p[1];
-      cv = (uint32_t)i;
-    }
-  }
-  wave_argmax(am, cm);
-  wave_argmax(av, cv);
-  if (lane == 0) {
-    // the seeds: chunk * C + the offset pass 1 recorded in that chunk
-    auto seed = [&](uint32_t c, int word) -> int64_t {
-      if (c == kNoArg) return -1;
-      const uint32_t off =
-          __float_as_uint(partials[kPartialWords * ((int64_t)T.first_chunk + c) + word]);
-      return off == kNoArg ? -1 : ((int64_t)c << src.chunk_shift) + off;
-    };
-    const int64_t seed_m = seed(cm, 2), seed_v = seed(cv, 3);
-    const double s_m = py_max((double)am, 1e-9);  // SCALE_FLOOR_M (config.py:25)
-    const double s_v = py_max((double)av, 0.0);
-    LUMA_GLOBAL Slot &s = *T.slot;
-    const int64_t t = s.step + 1;
-    const int par = (int)(t & 1);
-    const Hyper h = step_hyper(grp, t);
-    s.s_m[par] = s_m;
-    s.s_v[par] = s_v;
-    Grid g;
-    make_grid(s_m, s_v, grp.eps, g);
-    make_fast(g, h.eps);
-    s.grid[par] = g;
-    s.hyp = h;
-    s.step = t;
-    // (the small-tensor kernels write no summaries)
-    s.summ_step = (src.summaries && T.summary && T.first_chunk < src.small_from) ? t : 0;
-    s.summ_shift = src.chunk_shift;
-    s.seed_m = seed_m;
-    s.seed_v = seed_v;
-  }
-}
-
 // The exact pass 2 of elements e0 .. min(e0 + 8, end) - 1: update, draws
 // (Philox or injected), new codes.
 __device__ __forceinline__ void exact_group(const Tensor &T, const Hyper &h, const Grid *old,
@@ -509,7 +540,7 @@ __global__ __launch_bounds__(kThreads) void pass2_exact_kernel(StepSrc src, uint
   const PhiloxBase pb = philox_base(T.elem_offset);
   const bool inj = injected(T, noise_mode);
 
-  for (int64_t e0 = beg + (int64_t)threadIdx.x * kVec; e0 < end; e0 += (int64_t)kThreads * kVec)
+  for (int64_t e0 = beg + (int64_t)threadIdx.x * kVec; e0 < end; e0 += (int64_t)blockDim.x * kVec)
     exact_group(T, h, old, G, e0, end, scaled, inv, inj, pb, k0, k1);
 }
 
@@ -733,46 +764,6 @@ __device__ __noinline__ float2 exact_mv(int qm, int qw, float g, const LUMA_GLOB
   return make_float2(mn, vn);
 }
 
-// The exact |m'| and v' of each tensor's two seeds (the elements that held
-// its maxima at the previous step), for pass 1's initial thresholds: one
-// wavefront per tensor (lane 0 the momentum seed, lane 1 the preconditioner
-// seed), instead of every wavefront of every chunk evaluating them.  Tensors
-// without state and small-route tensors (exact pass 1) need none.
-__global__ __launch_bounds__(kThreads) void seed_kernel(StepSrc src, int32_t n_tensors) {
-  if (skip_step(src)) return;
-  const int64_t ti = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
-  if (ti >= n_tensors) return;
-  Tensor T;
-  LumaGroup grp;
-  if (src.tensors) {
-    T = src.tensors[ti];
-    grp = src.groups[T.group];
-  } else {
-    T = src.one;
-    grp = src.group;
-  }
-  if (T.first_chunk >= src.small_from) return;
-  LUMA_GLOBAL Slot &S = *T.slot;
-  const int64_t prev = S.step;
-  if (prev < 1) return;
-  const Hyper h = group_hyper(grp);
-  const LUMA_GLOBAL Grid *old = &S.grid[prev & 1];
-  const uint32_t lane = lane_id();
-  const int64_t si = lane == 0 ? S.seed_m : S.seed_v;
-  float2 e = make_float2(0.0f, 0.0f);
-  if (lane < 2 && si >= 0 && si < T.numel) {
-    float g = load_grad(T.grad, si, T.grad_dtype);
-    if (src.scaling.grad_scale != nullptr) g = unscale_rt(g, inv_scale(src), T.grad_dtype);
-    e = exact_mv(T.q_m[si], (int)(uint16_t)T.q_w[si], g, old, h);
-  }
-  const float xm = __shfl(e.x, 0, 64), xv = __shfl(e.y, 1, 64);
-  if (lane == 0) {
-    S.seed_xm = fabsf(xm);
-    S.seed_xv = xv;
-    S.seed_t = prev + 1;
-  }
-}
-
 // New code of one element before its draw is final (exact path): the
 // 16-bit code when the uniform u >= p (lo) and when u < p (hi), and the
 // argument a of p = exact_sr_prob(a, z).  The caller knows u to an interval
@@ -877,6 +868,8 @@ static_assert((kQueueCapW & (kQueueCapW - 1)) == 0 && (kQueueCapM & (kQueueCapM 
 // partial batch.  LDS per workgroup: 4 x (64 + 256 + 8 x 64) x 16 B = 52 KB,
 // so three workgroups (the VGPR limit) still fit a CU's 160 KB.
 constexpr int kStage = 8;
+// LDS entries (16 bytes) of one pass-2 wavefront: both queues and the ring.
+constexpr int kWaveLds = kQueueCapM + kQueueCapW + kStage * 64;
 
 // Keeps a wave-uniform value in a VGPR.  On gfx950 a VALU instruction with
 // an SGPR source operand issues at about half the rate of one whose sources
@@ -1085,7 +1078,7 @@ __device__ __forceinline__ void unpack_grads(const Raw8 &r, Group8 &G) {
   }
 }
 
-// Pass 1 body: exact max |m'| and max v' of the chunk.  The wave keeps a
+// Pass 1 body (t >= 2, old != null): exact max |m'| and max v' of the chunk.  The wave keeps a
 // running maximum of the fast values and from it a certified lower bound of
 // the exact maximum (the threshold, uniform across the wave).  An element
 // whose fast value is below the threshold cannot be the exact maximum; the
@@ -1128,15 +1121,6 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   const uint32_t lane = lane_id();
   uint32_t Mm = 0, Mv = 0, Tm = 0, Tv = 0;  // wave maxima / thresholds (bits)
   uint32_t T0m = 0, T0v = 0;                 // thresholds from the seeds (below)
-  // Thresholds from exact values: an element whose fast value is below
-  // (x - abs) / (1 + dlt) has an exact value below x (zero for a
-  // non-finite or non-positive x).
-  auto exact_threshold = [](float x, float abs_, float hi) -> uint32_t {
-    const float t = (x - abs_) * hi;
-    return (t > 0.0f && t < INFINITY) ? __float_as_uint(t) : 0u;
-  };
-  const bool exact_fast = old == nullptr;
-  uint32_t xbm = 0, xbv = 0;                 // exact maxima when exact_fast (bits)
   uint32_t qlen = 0;
   // exact m', v' of element i (any element of the tensor)
   auto exact_at = [&](int64_t i) -> float2 {
@@ -1162,12 +1146,6 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
                             max(max(am[4], am[5]), max(am[6], am[7])));
     const uint32_t iv = max(max(max(av[0], av[1]), max(av[2], av[3])),
                             max(max(av[4], av[5]), max(av[6], av[7])));
-    if (exact_fast) {
-      // t = 1: no decode, the fast m', v' are the exact ones
-      xbm = max(xbm, im);
-      xbv = max(xbv, iv);
-      return;
-    }
     if (!__ballot(im >= Tm || iv >= Tv)) return;
     // some lane reached the threshold: raise the wave maximum, then queue
     // the elements that still reach the new threshold
@@ -1190,29 +1168,47 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     }
   };
   // Seeds: the elements that held the tensor's maxima at the previous step
-  // (recorded by its finalize).  Their exact m', v' now (seed_kernel, once
-  // per tensor before this pass) are lower bounds of this step's maxima,
-  // whichever elements hold those, so they start the thresholds high: blocks
-  // below them are skipped from the first iteration.
-  if (old) {
-    const LUMA_GLOBAL Slot &S = *T.slot;
-    if (S.seed_t == S.step + 1) {
-      T0m = exact_threshold(S.seed_xm, B.abs_m, hi_m);
-      T0v = exact_threshold(S.seed_xv, B.abs_v, hi_v);
-      Tm = T0m;
-      Tv = T0v;
-    }
-  }
+  // (recorded by its finalize), wherever they lie in the tensor.  The fast
+  // value at such an element gives a threshold as a running maximum does
+  // (an element whose fast value is below it has an exact value below the
+  // seed's, so it is not the tensor's maximum, and the seed's own fast value
+  // is above it), so the thresholds start high: blocks below them are
+  // skipped from the first iteration.  Every lane loads the momentum seed
+  // (even lanes) or the preconditioner seed (odd lanes); the loads are
+  // issued before the first group's, which they do not wait for.
+  const LUMA_GLOBAL Slot &S = *T.slot;
+  const int64_t si = (lane & 1u) ? S.seed_v : S.seed_m;
+  const bool s_ok = si >= 0 && si < T.numel;
+  const int64_t sj = s_ok ? si : 0;
+  const int s_qm = (int)T.q_m[sj];
+  const int s_qw = (int)((uint32_t)(uint16_t)T.q_w[sj] | kCodeFloat);
+  const float s_g = load_grad(T.grad, sj, GD);
+  auto seed_thresholds = [&]() {
+    float g = s_g;
+    if (SCALED) g = unscale<GD>(g, inv);
+    const FastEma f = fast_ema<SMALL ? kRegSmall : kRegGeneral, false>(
+        s_qm, s_qw, g, K.dm, K.ndw, K.nbias, K.iwmin, K.eps, K.b1, K.omb1, K.b2, K.omb2, K.sign);
+    const uint32_t xb = s_ok ? (__float_as_uint((lane & 1u) ? f.vn : f.mn) & 0x7FFFFFFFu) : 0u;
+    T0m = threshold_bits((uint32_t)__shfl((int)xb, 0, 64), lo_m, sub_m, hi_m);
+    T0v = threshold_bits((uint32_t)__shfl((int)xb, 1, 64), lo_v, sub_v, hi_v);
+    Tm = T0m;
+    Tv = T0v;
+  };
   // Every lane of a wave runs the same iterations (lanes past the end carry
   // n = 0), so the ballots and the queue length stay uniform across the wave;
   // a wave stops once all its groups lie past the end.
-  constexpr int64_t kStride = (int64_t)kThreads * kVec;
-  const int n_it = (int)((end - beg + kStride - 1) / kStride);
+  // Threads per chunk: kThreads, or one wavefront for a medium tensor; an
+  // iteration covers nt * kVec consecutive elements.
+  const int nt = (int)blockDim.x;
+  const int it_shift = __builtin_ctz((unsigned)nt) + 3;
+  const int64_t kStride = (int64_t)1 << it_shift;
+  const int n_it = (int)((end - beg + kStride - 1) >> it_shift);
   // Iterations in which every lane's group is whole run in a loop of their
   // own that loads each group one iteration ahead: raw holds the codes and
   // gradients of the lane's next group (the current one again after the last
   // whole group, so that every iteration issues the same loads).
-  const int n_whole = vec_ok ? (int)((end - beg) / kStride) : 0;
+  // (uniform: readfirstlane keeps the loop's group offsets in SGPRs)
+  const int n_whole = __builtin_amdgcn_readfirstlane(vec_ok ? (int)((end - beg) >> it_shift) : 0);
   int it = 0;
   if (SUMM && n_whole > 0) {
     // This thread's summary word (written by the previous pass 2 for the
@@ -1228,7 +1224,7 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     // p1_reach); only when it reaches a threshold in some lane are the
     // wave's codes read and decoded.
     auto visit = [&](const Raw8 &cur, int j) {
-      const int64_t e0 = beg + ((int64_t)j * kThreads + threadIdx.x) * kVec;
+      const int64_t e0 = beg + ((int64_t)j * nt + threadIdx.x) * kVec;
       {
         const float g = raw_gmax<GD, SCALED>(cur, K.inv);
         const float mn = fmaf(K.b1, d.am, K.omb1 * g);
@@ -1259,10 +1255,11 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     // single buffer carried across iterations) would make every iteration
     // wait for the load just issued.
     auto group_at = [&](int j) {
-      return beg + ((int64_t)(j < n_whole ? j : n_whole - 1) * kThreads + threadIdx.x) * kVec;
+      return beg + ((int64_t)(j < n_whole ? j : n_whole - 1) * nt + threadIdx.x) * kVec;
     };
     Raw8 ra, rb;
     load_grads<GD>(T, group_at(0), ra);
+    seed_thresholds();
     for (; it < n_whole; it += 2) {
       load_grads<GD>(T, group_at(it + 1), rb);
       visit(ra, it);
@@ -1274,21 +1271,20 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   } else if (n_whole > 0) {
     Raw8 raw;
     load_raw<GD>(T, beg + (int64_t)threadIdx.x * kVec, raw);
+    seed_thresholds();
     for (; it < n_whole; ++it) {
-      const int64_t e0 = beg + ((int64_t)it * kThreads + threadIdx.x) * kVec;
+      const int64_t e0 = beg + ((int64_t)it * nt + threadIdx.x) * kVec;
       const int64_t en = end - e0 - kStride >= kVec ? e0 + kStride : e0;
       uint32_t am[kVec], av[kVec];
-      if (exact_fast)
-        p1_iter<GD, SMALL, SCALED, true, false>(T, K, e0, kVec, raw, en, Tm, Tv, am, av);
-      else
-        p1_iter<GD, SMALL, SCALED, true, true>(T, K, e0, kVec, raw, en, Tm, Tv, am, av);
+      p1_iter<GD, SMALL, SCALED, true, true>(T, K, e0, kVec, raw, en, Tm, Tv, am, av);
       take(e0, kVec, am, av);
     }
   }
+  if (n_whole == 0) seed_thresholds();
   for (; it < n_it; ++it) {
     // a wave whose groups all lie past the end is done (small tensors)
-    if (beg + ((int64_t)it * kThreads + (threadIdx.x & ~63u)) * kVec >= end) break;
-    const int64_t e0 = beg + ((int64_t)it * kThreads + threadIdx.x) * kVec;
+    if (beg + ((int64_t)it * nt + (threadIdx.x & ~63u)) * kVec >= end) break;
+    const int64_t e0 = beg + ((int64_t)it * nt + threadIdx.x) * kVec;
     const int64_t rem = end - e0;
     const int n = rem <= 0 ? 0 : (rem < kVec ? (int)rem : kVec);
     uint32_t am[kVec], av[kVec];
@@ -1298,17 +1294,47 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   }
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   if (lane < qlen) run(queue[lane]);
-  if (exact_fast) {
-    // t = 1: the maxima of the fast values (exact here), positions not kept
-    if (beats(__uint_as_float(xbm), exm)) {
-      exm = __uint_as_float(xbm);
-      exi_m = kNoArg;
+}
+
+// Pass 1 of the init step (t = 1: no codes to decode).  m' = (1 - beta1) g
+// and v' = (1 - beta2) g^2 are each a product (of a product) rounded to
+// float32, so both are non-decreasing in |g|: the chunk's maxima are those
+// of its largest |g|, and that element is recorded as both maxima's
+// position, the seeds of the next step.  Only the gradients are read.
+struct InitMax {
+  uint32_t gb, gi;   // the lane's largest |g| (float bits, NaN above +Inf) and its offset
+};
+
+// The lane's largest |g| of the chunk [beg, end).  Out of line, and given
+// the gradient pointer rather than the tensor record, so that the kernel's
+// copy of the record stays in registers.
+template <int GD>
+__device__ __noinline__ InitMax pass1_init_scan(const LUMA_GLOBAL void *grad, int64_t beg,
+                                                int64_t end, bool vec_ok) {
+  const int64_t kStride = (int64_t)blockDim.x * kVec;
+  Tensor T{};
+  T.grad = grad;
+  InitMax r{0u, kNoArg};
+  auto fold = [&](float g, int64_t i) {
+    const uint32_t b = __float_as_uint(g) & 0x7FFFFFFFu;
+    if (b > r.gb) {
+      r.gb = b;
+      r.gi = (uint32_t)(i - beg);
     }
-    if (beats(__uint_as_float(xbv), exv)) {
-      exv = __uint_as_float(xbv);
-      exi_v = kNoArg;
+  };
+  for (int64_t e0 = beg + (int64_t)threadIdx.x * kVec; e0 < end; e0 += kStride) {
+    if (vec_ok && end - e0 >= kVec) {
+      Raw8 rw;
+      load_grads<GD>(T, e0, rw);
+      Group8 G;
+      unpack_grads<GD>(rw, G);
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) fold(G.g[j], e0 + j);
+    } else {
+      for (int j = 0; j < kVec && e0 + j < end; ++j) fold(load_grad(T.grad, e0 + j, GD), e0 + j);
     }
   }
+  return r;
 }
 
 template <int GD, bool SUMM>
@@ -1348,7 +1374,8 @@ __device__ __forceinline__ void pass1_dispatch(const Tensor &T, const Hyper &h,
 // aligned (the whole-group loop).
 __device__ __forceinline__ bool summaries_valid(const Tensor &T, const LUMA_GLOBAL Grid *old,
                                                 int64_t prev, int64_t ci, int32_t shift) {
-  return T.summary != nullptr && (ci + 1) * LUMA_SUMMARY_WORDS <= T.summary_words &&
+  return blockDim.x == kThreads && T.summary != nullptr &&
+         (ci + 1) * LUMA_SUMMARY_WORDS <= T.summary_words &&
          old != nullptr && T.slot->summ_step == prev && T.slot->summ_shift == shift &&
          __builtin_isfinite(old->dm) && __builtin_isfinite(old->dw) &&
          __builtin_isfinite(old->fast[kIwmin]) && tensor_vec_ok(T);
@@ -1375,7 +1402,21 @@ __global__ __launch_bounds__(kThreads, 4) void pass1_fast_kernel(StepSrc src,
   const bool summ = summaries_valid(T, old, prev, ci, src.chunk_shift);
   float exm = 0.0f, exv = 0.0f;
   uint32_t exi_m = kNoArg, exi_v = kNoArg;
-  if (T.grad_dtype == LUMA_GRAD_BF16)
+  if (old == nullptr) {
+    const bool vec_ok = tensor_vec_ok(T);
+    const InitMax r =
+        T.grad_dtype == LUMA_GRAD_BF16  ? pass1_init_scan<LUMA_GRAD_BF16>(T.grad, beg, end, vec_ok)
+        : T.grad_dtype == LUMA_GRAD_F16 ? pass1_init_scan<LUMA_GRAD_F16>(T.grad, beg, end, vec_ok)
+                                        : pass1_init_scan<LUMA_GRAD_F32>(T.grad, beg, end, vec_ok);
+    // unscaling is monotone in |g|: only the largest is unscaled
+    float g = __uint_as_float(r.gb);
+    if (scaled) g = unscale_rt(g, inv, T.grad_dtype);
+    float mn, vn;
+    exact_ema(0.0f, 0.0f, g, h, mn, vn);
+    exm = fabsf(mn);
+    exv = vn;
+    exi_m = exi_v = r.gi;
+  } else if (T.grad_dtype == LUMA_GRAD_BF16)
     pass1_dispatch<LUMA_GRAD_BF16>(T, h, old, inv, ci, beg, end, small, scaled, summ, exm, exv,
                                    exi_m, exi_v, q);
   else if (T.grad_dtype == LUMA_GRAD_F16)
@@ -1385,7 +1426,7 @@ __global__ __launch_bounds__(kThreads, 4) void pass1_fast_kernel(StepSrc src,
     pass1_dispatch<LUMA_GRAD_F32>(T, h, old, inv, ci, beg, end, small, scaled, summ, exm, exv,
                                   exi_m, exi_v, q);
   block_argmax2(exm, exi_m, exv, exi_v);
-  if (threadIdx.x == 0) put_partial(partials, blockIdx.x, exm, exv, exi_m, exi_v);
+  if (threadIdx.x == 0) put_partial(partials, src.chunk_base + blockIdx.x, exm, exv, exi_m, exi_v);
 }
 
 // Inclusive prefix sum over the 64 lanes of a wave (all lanes active): three
@@ -1836,11 +1877,14 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   auto u_hi = [&](uint32_t top, const LUMA_GLOBAL float *u, int64_t i) -> float {
     return INJ ? u[i] : (float)((top << 8) | 0xFFu) * 0x1p-24f;
   };
+  // Threads per chunk: kThreads, or one wavefront for a medium tensor; an
+  // iteration covers nt * kVec = 1 << it_shift consecutive elements.
+  const int nt = (int)blockDim.x;
+  const int it_shift = __builtin_ctz((unsigned)nt) + 3;
   // Staging: whole-group iterations [staged_lo, staged_hi) keep their
   // preconditioner codes in stage[(it % kStage) * 64 + lane] until written
-  // back.  Chunk offset o belongs to iteration o >> 11 (kThreads * kVec =
-  // 2048 elements per iteration) and to lane (o >> 3) & 63 of this wave.
-  static_assert(kThreads * kVec == 2048, "iteration of a chunk offset");
+  // back.  Chunk offset o belongs to iteration o >> it_shift and to lane
+  // (o >> 3) & 63 of this wave.
   int staged_lo = 0, staged_hi = 0;
   // an entry's element: its half of the words (sh = 16 for odd k)
   auto ent_grad = [&](const uint4 &ent, uint32_t sh) -> float {
@@ -1864,7 +1908,7 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
                                                 old, nw, h, u_lo(top, T.u_w, i),
                                                 u_hi(top, T.u_w, i)));
     const uint16_t code = (uint16_t)draw(c, zw_new, i, top, 1);
-    const int it_e = (int)(o >> 11);
+    const int it_e = (int)(o >> it_shift);
     if (it_e >= staged_lo && it_e < staged_hi) {
       uint16_t *slot = (uint16_t *)&stage[(it_e % kStage) * 64 + ((o >> 3) & 63u)];
       slot[o & 7u] = code;
@@ -1959,13 +2003,13 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   // Oldest pending preconditioner entry's iteration (the ring is FIFO).
   auto oldest_w = [&]() -> int {
     const uint32_t x = queue_w[head_w & (kQueueCapW - 1)].x;
-    return (int)((uint32_t)__builtin_amdgcn_readfirstlane((int)x) >> 11);
+    return (int)((uint32_t)__builtin_amdgcn_readfirstlane((int)x) >> it_shift);
   };
   // Write iteration j's staged preconditioner codes to HBM.
   auto write_back = [&](int j) {
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     const uint4 v = stage[(j % kStage) * 64 + lane];
-    const int64_t e = beg + ((int64_t)j * kThreads + threadIdx.x) * kVec;
+    const int64_t e = beg + ((int64_t)j * nt + threadIdx.x) * kVec;
     vu4 w;
     w.x = v.x; w.y = v.y; w.z = v.z; w.w = v.w;
     store_stream(w, (LUMA_GLOBAL vu4 *)(T.q_w + e));
@@ -1973,19 +2017,19 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   // Every lane of a wave runs the same iterations (lanes past the end carry
   // n = 0), so the ballots and the queue lengths stay uniform across the wave;
   // a wave stops once all its groups lie past the end.
-  constexpr int64_t kStride = (int64_t)kThreads * kVec;
-  const int n_it = (int)((end - beg + kStride - 1) / kStride);
+  const int64_t kStride = (int64_t)1 << it_shift;
+  const int n_it = (int)((end - beg + kStride - 1) >> it_shift);
   CodeAcc acc{0u, 0u, 0xFFFFFFFFu};
   // Iterations in which every lane's group is whole stage their
   // preconditioner codes; before a slot is reused, the iteration it holds has
   // its queued entries run and is written back.
-  const int n_whole = vec_ok ? (int)((end - beg) / kStride) : 0;
+  const int n_whole = vec_ok ? (int)((end - beg) >> it_shift) : 0;
   // Each iteration's vectors are loaded one iteration ahead, into two
   // buffers in a loop unrolled by two (copying a buffer whose loads are in
   // flight would make the copy wait for them); past the last whole group the
   // loads repeat the last group, and are not used.
   auto group_at = [&](int j) {
-    return beg + ((int64_t)(j < n_whole ? j : n_whole - 1) * kThreads + threadIdx.x) * kVec;
+    return beg + ((int64_t)(j < n_whole ? j : n_whole - 1) * nt + threadIdx.x) * kVec;
   };
   auto whole_iter = [&](const P2Raw &R, int j) {
     const int64_t e0 = group_at(j);
@@ -2022,8 +2066,8 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   staged_lo = staged_hi = 0;
   for (; it < n_it; ++it) {
     // a wave whose groups all lie past the end is done (small tensors)
-    if (beg + ((int64_t)it * kThreads + (threadIdx.x & ~63u)) * kVec >= end) break;
-    const int64_t e0 = beg + ((int64_t)it * kThreads + threadIdx.x) * kVec;
+    if (beg + ((int64_t)it * nt + (threadIdx.x & ~63u)) * kVec >= end) break;
+    const int64_t e0 = beg + ((int64_t)it * nt + threadIdx.x) * kVec;
     const int64_t rem = end - e0;
     const int n = rem <= 0 ? 0 : (rem < kVec ? (int)rem : kVec);
     Group8 Q;
@@ -2041,7 +2085,8 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   }
   // The thread's summary word: its largest |Q_m| + margin, its smallest
   // Q_w - margin (clamped to the code ranges).
-  if (T.summary != nullptr && (ci + 1) * LUMA_SUMMARY_WORDS <= T.summary_words) {
+  // (one word per thread of a kThreads workgroup: the wavefront route writes none)
+  if (nt == kThreads && T.summary != nullptr && (ci + 1) * LUMA_SUMMARY_WORDS <= T.summary_words) {
     const int mx = max((int)(int16_t)(acc.mx & 0xFFFFu), (int)(int16_t)(acc.mx >> 16));
     const int mn = min((int)(int16_t)(acc.mn & 0xFFFFu), (int)(int16_t)(acc.mn >> 16));
     const uint32_t qa = (uint32_t)max(mx, -mn), qw = min(acc.wn & 0xFFFFu, acc.wn >> 16);
@@ -2120,8 +2165,10 @@ __global__ __launch_bounds__(kThreads) void pass2_fast_kernel(StepSrc src, uint6
   const int reg = momentum_regime(x_top, nw->sm);
   const bool scaled = src.scaling.grad_scale != nullptr;
   const float inv = inv_scale(src);
-  __shared__ uint4 qbuf[kThreads / 64][kQueueCapM + kQueueCapW + kStage * 64];
-  uint4 *q = qbuf[threadIdx.x >> 6];
+  // each wavefront's queues and staging ring: launched with blockDim.x / 64
+  // blocks of kWaveLds entries of dynamic LDS
+  extern __shared__ uint4 p2_lds[];
+  uint4 *q = p2_lds + (threadIdx.x >> 6) * kWaveLds;
   if (T.grad_dtype == LUMA_GRAD_BF16)
     pass2_dispatch<LUMA_GRAD_BF16, INJ_OK>(T, h, old, nw, inv, scaled, ci, beg, end, k0, k1, inj,
                                            reg, q);
@@ -2148,7 +2195,6 @@ __device__ void write_slot(Slot &s, int64_t t, double s_m, double s_v, double ep
   s.summ_step = 0;   // codes written by other means: no summaries for them
   s.summ_shift = 0;
   s.seed_m = s.seed_v = -1;
-  s.seed_t = 0;
 }
 
 __global__ void set_scales_kernel(const LumaScaleInit *__restrict__ items, int n) {
@@ -2335,8 +2381,9 @@ void luma_layout(int32_t out[8]) {
   out[7] = 0;
 }
 
-// The three launches of one step over `n_chunks` chunks of `n_tensors`
-// tensors, with optional event records between them.
+// The launches of one step over `n_chunks` chunks of `n_tensors` tensors,
+// with optional event records between them: pass 1, finalize, pass 2; sets
+// with small tensors add the wavefront-per-tensor kernel of each pass.
 static int launch_step(StepSrc src, int32_t n_tensors, int32_t n_chunks, float *partials,
                        uint64_t base_seed, int32_t noise_mode, int32_t flags, hipStream_t s,
                        void *const *events) {
@@ -2351,21 +2398,30 @@ static int launch_step(StepSrc src, int32_t n_tensors, int32_t n_chunks, float *
   };
   if (int r = mark(0)) return r;
   const bool exact = (flags & LUMA_FLAG_EXACT_ONLY) != 0;
-  // chunks [0, small_from): a workgroup each; [small_from, n_chunks): small
-  // tensors, a wavefront each
-  const int32_t n_big = src.small_from;
-  const int32_t small_blocks = (n_chunks - n_big + kThreads / 64 - 1) / (kThreads / 64);
-  if (n_big > 0) {
-    if (exact) {
-      hipLaunchKernelGGL(pass1_exact_kernel, dim3(n_big), dim3(kThreads), 0, s, src, partials);
-    } else {
-      hipLaunchKernelGGL(seed_kernel, dim3((n_tensors + kThreads / 64 - 1) / (kThreads / 64)),
-                         dim3(kThreads), 0, s, src, n_tensors);
-      if (int r = check_launch("luma_step: seed launch")) return r;
-      hipLaunchKernelGGL(pass1_fast_kernel, dim3(n_big), dim3(kThreads), 0, s, src, partials);
+  // chunks [0, medium_from): a workgroup of kThreads each; [medium_from,
+  // small_from): a workgroup of one wavefront each (same kernels);
+  // [small_from, n_chunks): small tensors, a wavefront each
+  const int32_t n_big = src.medium_from;
+  const int32_t n_med = src.small_from - src.medium_from;
+  const int32_t small_blocks = (n_chunks - src.small_from + kThreads / 64 - 1) / (kThreads / 64);
+  StepSrc med = src;
+  med.chunk_base = src.medium_from;
+  // the runs of pass 1 or pass 2: kernel k over [0, n_big) and [medium_from, small_from)
+  auto runs = [&](auto kernel, size_t lds_per_wave, auto... args) -> int {
+    if (n_big > 0) {
+      hipLaunchKernelGGL(kernel, dim3(n_big), dim3(kThreads), lds_per_wave * (kThreads / 64), s,
+                         src, args...);
+      if (int r = check_launch("luma_step: launch")) return r;
     }
-    if (int r = check_launch("luma_step: pass 1 launch")) return r;
-  }
+    if (n_med > 0) {
+      hipLaunchKernelGGL(kernel, dim3(n_med), dim3(64), lds_per_wave, s, med, args...);
+      if (int r = check_launch("luma_step: launch (medium tensors)")) return r;
+    }
+    return 0;
+  };
+  constexpr size_t kP2Lds = sizeof(uint4) * kWaveLds;
+  if (int r = exact ? runs(pass1_exact_kernel, 0, partials) : runs(pass1_fast_kernel, 0, partials))
+    return r;
   if (small_blocks > 0) {
     hipLaunchKernelGGL(pass1_small_kernel, dim3(small_blocks), dim3(kThreads), 0, s, src, partials);
     if (int r = check_launch("luma_step: pass 1 (small tensors) launch")) return r;
@@ -2375,18 +2431,14 @@ static int launch_step(StepSrc src, int32_t n_tensors, int32_t n_chunks, float *
                      dim3(kThreads), 0, s, src, (const float *)partials, n_tensors);
   if (int r = check_launch("luma_step: finalize launch")) return r;
   if (int r = mark(2)) return r;
-  if (n_big > 0) {
-    if (exact)
-      hipLaunchKernelGGL(pass2_exact_kernel, dim3(n_big), dim3(kThreads), 0, s, src, base_seed,
-                         (int)noise_mode);
-    else if (noise_mode == LUMA_NOISE_INJECTED)
-      hipLaunchKernelGGL(pass2_fast_kernel<true>, dim3(n_big), dim3(kThreads), 0, s, src,
-                         base_seed, (int)noise_mode);
-    else
-      hipLaunchKernelGGL(pass2_fast_kernel<false>, dim3(n_big), dim3(kThreads), 0, s, src,
-                         base_seed, (int)noise_mode);
-    if (int r = check_launch("luma_step: pass 2 launch")) return r;
-  }
+  int r2;
+  if (exact)
+    r2 = runs(pass2_exact_kernel, 0, base_seed, (int)noise_mode);
+  else if (noise_mode == LUMA_NOISE_INJECTED)
+    r2 = runs(pass2_fast_kernel<true>, kP2Lds, base_seed, (int)noise_mode);
+  else
+    r2 = runs(pass2_fast_kernel<false>, kP2Lds, base_seed, (int)noise_mode);
+  if (r2) return r2;
   if (small_blocks > 0) {
     hipLaunchKernelGGL(pass2_small_kernel, dim3(small_blocks), dim3(kThreads), 0, s, src,
                        base_seed, (int)noise_mode);
@@ -2400,6 +2452,7 @@ static int step_impl(const LumaStepArgs *a, void *stream, void *const *events) {
   if (a->n_tensors <= 0 || a->n_chunks <= 0) return 0;
   if (!a->tensors || !a->chunks || !a->groups || !a->partials)
     return fail("luma_step: null table pointer");
+  if ((uintptr_t)a->partials & 15u) return fail("luma_step: partials must be 16-byte aligned");
   const int32_t c = a->chunk_elems ? a->chunk_elems : (int32_t)LUMA_CHUNK_ELEMS;
   if (c < LUMA_CHUNK_ELEMS_MIN || c > LUMA_CHUNK_ELEMS || (c & (c - 1)) != 0)
     return fail("luma_step: chunk_elems must be a power of two in [LUMA_CHUNK_ELEMS_MIN, LUMA_CHUNK_ELEMS]");
@@ -2411,7 +2464,11 @@ static int step_impl(const LumaStepArgs *a, void *stream, void *const *events) {
   src.chunk_shift = __builtin_ctz((unsigned)c);
   if (a->small_chunks < 0 || a->small_chunks > a->n_chunks)
     return fail("luma_step: small_chunks must be in [0, n_chunks]");
+  if (a->medium_chunks < 0 || a->medium_chunks > a->n_chunks - a->small_chunks)
+    return fail("luma_step: medium_chunks must be in [0, n_chunks - small_chunks]");
   src.small_from = a->n_chunks - a->small_chunks;
+  src.medium_from = src.small_from - a->medium_chunks;
+  src.chunk_base = 0;
   src.n_chunks = a->n_chunks;
   return launch_step(src, a->n_tensors, a->n_chunks, a->partials, a->base_seed, a->noise_mode,
                      a->flags, static_cast<hipStream_t>(stream), events);
@@ -2468,6 +2525,7 @@ int luma_step_tensor(const LumaTensor *tensor, const LumaGroup *group, float *pa
   if (!tensor->param || !tensor->grad || !tensor->q_m || !tensor->q_w || !tensor->slot ||
       !partials)
     return fail("luma_step_tensor: null pointer");
+  if ((uintptr_t)partials & 15u) return fail("luma_step_tensor: partials must be 16-byte aligned");
   if (noise_mode == LUMA_NOISE_INJECTED && (!tensor->u_m || !tensor->u_w))
     return fail("luma_step_tensor: injected noise needs u_m and u_w");
   // 4096 chunks fill the chip (16 workgroups per CU); a smaller tensor takes
@@ -2483,7 +2541,9 @@ int luma_step_tensor(const LumaTensor *tensor, const LumaGroup *group, float *pa
   src.one.first_chunk = 0;
   src.group = *group;
   src.chunk_shift = shift;
-  src.small_from = (int32_t)nch;   // one tensor: no small-tensor chunks
+  src.small_from = (int32_t)nch;   // one tensor: every chunk takes a workgroup
+  src.medium_from = (int32_t)nch;
+  src.chunk_base = 0;
   src.n_chunks = (int32_t)nch;
   if (scaling) src.scaling = *scaling;
   return launch_step(src, 1, (int32_t)nch, partials, base_seed, noise_mode, flags,

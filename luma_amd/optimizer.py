@@ -88,6 +88,9 @@ def shard_offset(t) -> int:
 
 
 _ARENA_ALIGN = 128   # int16 elements: every Q tensor starts on a 256-byte boundary
+# Smallest tensor given code summaries: pass 1 reads them only in whole
+# iterations of a workgroup (256 threads x 8 elements).
+_SUMMARY_MIN = 2048
 
 
 def state_arena(params, device):
@@ -125,6 +128,8 @@ class _Engine:
     those of the previous step launches with no host-to-device copy (and may
     be captured into a CUDA/HIP graph)."""
 
+    TABLE_CACHE = 4   # device tensor tables kept for re-use
+
     def __init__(self, device: torch.device):
         self.lib = L.load()
         self.host = L.load_host()
@@ -137,7 +142,12 @@ class _Engine:
         self.chunk_elems = 0         # fixed chunk length (a power of two), 0: chunk_for's choice
         self.small_tensors = True    # step tensors of <= SMALL_TENSOR elements a wavefront each
         self._small_chunks = 0       # trailing chunk records of such tensors (uploaded table)
+        self.medium_tensors = True   # step tensors of <= MEDIUM_TENSOR elements a one-wavefront
+                                     # workgroup each (the fast kernels)
+        self._medium_chunks = 0      # the records of such tensors, before the small ones
         self._d_tensors = None
+        self._table_cache = {}       # tensor-table bytes -> device copy (most recent last)
+        self._ptr_cache = {}         # pointer fingerprint -> (table, grads, params, device copy)
         self._d_chunks = None
         self._n_chunks = 0
         self._group_key = None
@@ -186,7 +196,7 @@ class _Engine:
         c = L.CHUNK_ELEMS
         while c > STEP_CHUNK_MIN and c * STEP_TARGET_CHUNKS > total:
             c //= 2
-        big = numels[numels > self._small_limit()]
+        big = numels[numels > self._wave_limit()]
         if len(big) >= STEP_TARGET_CHUNKS:
             while c < L.CHUNK_ELEMS and c < int(big.max()):
                 c *= 2
@@ -223,16 +233,23 @@ class _Engine:
         return tt
 
     def launch(self, tt: np.ndarray, groups: np.ndarray, base_seed: int, noise_mode: int,
-               flags: int = 0, scaling: Tuple[int, int] = (0, 0), same_table: bool = False):
+               flags: int = 0, scaling: Tuple[int, int] = (0, 0), same_table: bool = False,
+               moved: bool = False):
         """One step over the tensors of table tt (luma_step), uploading only the
         tables whose contents changed since the previous launch.  With
         ``same_table`` the caller vouches that tt is the array of the previous
-        launch, unchanged since: the comparison of its contents is skipped."""
+        launch, unchanged since: the comparison of its contents is skipped.
+        With ``moved`` it vouches that tt is that array with only its gradient
+        and parameter pointers rewritten: the device tables of earlier pointer
+        sets are looked up by those two columns alone."""
         capturing = torch.cuda.is_current_stream_capturing()
         n = len(tt)
-        setting = (self.chunk_elems, self._small_limit())
-        if not (same_table and self._tensor_src is not None and self._tensor_src[0] is tt
-                and self._tensor_src[1] == setting):
+        setting = (self.chunk_elems, self._small_limit(), self._medium_limit())
+        same_src = (self._tensor_src is not None and self._tensor_src[0] is tt
+                    and self._tensor_src[1] == setting)
+        if moved and same_src:
+            self._match_pointers(tt, capturing)
+        elif not (same_table and same_src):
             self._tensor_src = None     # stays unset if the upload fails
             self._match_table(tt, capturing)
             self._tensor_src = (tt, setting)
@@ -258,6 +275,7 @@ class _Engine:
             partials=self._partials.data_ptr(),
             base_seed=base_seed & _MASK64, noise_mode=noise_mode, flags=flags,
             chunk_elems=self._chunk, small_chunks=self._small_chunks,
+            medium_chunks=self._medium_chunks,
             scaling=L.Scaling(scaling[0] or None, scaling[1] or None))
         if self.profile_events is None:
             L.check(self.lib.luma_step(ctypes.byref(args), self._stream()), "luma_step")
@@ -267,31 +285,45 @@ class _Engine:
                     "luma_step_profiled")
 
     def _small_limit(self) -> int:
-        """Largest tensor stepped a wavefront each (0: none)."""
+        """Largest tensor stepped a wavefront each by the exact kernels (0: none)."""
         return int(L.SMALL_TENSOR) if self.small_tensors else 0
+
+    def _medium_limit(self) -> int:
+        """Largest tensor stepped by a one-wavefront workgroup (0: none)."""
+        return int(L.MEDIUM_TENSOR) if self.medium_tensors else 0
+
+    def _wave_limit(self) -> int:
+        """Largest tensor stepped by a single wavefront, either route."""
+        return max(self._small_limit(), self._medium_limit())
 
     def chunk_layout(self, numels: np.ndarray, c: int):
         """Chunk table layout of tensors of these sizes at chunk length c: the
-        first chunk of every tensor, the chunk records (tensor, index) and the
-        number of trailing records that belong to small tensors.  Tensors of at
-        most SMALL_TENSOR elements come last, stepped a wavefront per chunk
-        (luma.h, LumaStepArgs.small_chunks), largest first: the four
-        wavefronts of a workgroup then step tensors of about one size, and
-        none holds the workgroup long after the other three are done.  The
-        others keep their order, unless there are STEP_TARGET_CHUNKS of them
-        or more (chunk_for gives such a set one chunk per tensor): then the
-        largest come first, so the launch ends on its shortest workgroups.
+        first chunk of every tensor, the chunk records (tensor, index), and
+        the number of records of medium and of small tensors, which come last
+        in that order (luma.h, LumaStepArgs.medium_chunks / small_chunks).
+        Tensors of at most SMALL_TENSOR elements are stepped a wavefront per
+        chunk by the exact kernels, and those above it and of at most
+        MEDIUM_TENSOR elements (and one chunk) by a one-wavefront workgroup
+        of the fast kernels; each run is ordered largest first, so the four
+        wavefronts of a small-tensor workgroup step tensors of about one size
+        and every launch ends on its shortest work.  The others keep their
+        order, unless there are STEP_TARGET_CHUNKS of them or more (chunk_for
+        gives such a set one chunk per tensor): then the largest come first.
         Ties keep their order."""
         n = len(numels)
         nch = (numels + c - 1) // c
         small = numels <= self._small_limit()
-        big = np.nonzero(~small)[0]
+        medium = ~small & (numels <= min(self._medium_limit(), c))
+        big = np.nonzero(~small & ~medium)[0]
         if len(big) >= STEP_TARGET_CHUNKS:
             big = big[np.argsort(-numels[big], kind="stable")]
+        mid = np.nonzero(medium)[0]
+        mid = mid[np.argsort(-numels[mid], kind="stable")]
         little = np.nonzero(small)[0]
         little = little[np.argsort(-numels[little], kind="stable")]
-        order = np.concatenate([big, little])
+        order = np.concatenate([big, mid, little])
         n_small = int(nch[small].sum())
+        n_medium = int(nch[medium].sum())
         nch_o = nch[order]
         first_o = np.zeros(n, dtype=np.int64)
         np.cumsum(nch_o[:-1], out=first_o[1:])
@@ -301,7 +333,7 @@ class _Engine:
         ch = np.empty(n_chunks, dtype=L.CHUNK_DTYPE)
         ch["tensor"] = np.repeat(order.astype(np.int32), nch_o)
         ch["index"] = np.arange(n_chunks, dtype=np.int64) - np.repeat(first_o, nch_o)
-        return first, ch, n_small
+        return first, ch, n_small, n_medium
 
     def _match_table(self, tt: np.ndarray, capturing: bool):
         """Upload tt (and its chunk table) unless the device holds it already."""
@@ -310,16 +342,18 @@ class _Engine:
         numels = tt["numel"]
         c = self.chunk_for(numels)
         nkey = (numels.tobytes() + c.to_bytes(4, "little")
-                + self._small_limit().to_bytes(8, "little"))
+                + self._small_limit().to_bytes(8, "little")
+                + self._medium_limit().to_bytes(8, "little"))
         if nkey != self._numel_key:
             if capturing:
                 raise self._capture_error("the parameter or gradient set")
-            first, ch, n_small = self.chunk_layout(numels, c)
+            first, ch, n_small, n_medium = self.chunk_layout(numels, c)
             tt["first_chunk"] = first
             key = tt.tobytes()
             self._d_chunks = self._upload(ch)
             self._n_chunks = len(ch)
             self._small_chunks = n_small
+            self._medium_chunks = n_medium
             self._chunk = c
             self._numel_key = nkey
             self._first = first
@@ -327,10 +361,46 @@ class _Engine:
             tt["first_chunk"] = self._first
             key = tt.tobytes()
         if key != self._tensor_key:
+            # the last few uploaded tables stay on the device: a loop whose
+            # gradients alternate between buffers re-uses them, no upload
+            cached = self._table_cache.pop(key, None)
+            if cached is None:
+                if capturing:
+                    raise self._capture_error("the parameter or gradient set")
+                cached = self._upload(tt)
+            self._table_cache[key] = cached
+            while len(self._table_cache) > self.TABLE_CACHE:
+                self._table_cache.pop(next(iter(self._table_cache)))
+            self._d_tensors = cached
+            self._tensor_key = key
+
+    # odd multipliers of the pointer fingerprint (uint64 arithmetic wraps)
+    _FP_G = np.uint64(0x9E3779B97F4A7C15)
+    _FP_P = np.uint64(0xC2B2AE3D27D4EB4F)
+
+    def _match_pointers(self, tt: np.ndarray, capturing: bool):
+        """Device table for tt, which differs from the table last matched for
+        it in its gradient and parameter pointers only (a planned step whose
+        gradients moved, e.g. a loop that alternates gradient buffers): a
+        table uploaded for the same pointers is re-used (looked up by a
+        fingerprint of the two columns, then compared with them), so such a
+        loop uploads each table once."""
+        g, p = tt["grad"], tt["param"]
+        with np.errstate(over="ignore"):
+            fp = int((g * self._FP_G).sum(dtype=np.uint64) ^ (p * self._FP_P).sum(dtype=np.uint64))
+        hit = self._ptr_cache.pop(fp, None)
+        if hit is not None and not (hit[0] is tt and np.array_equal(hit[1], g)
+                                    and np.array_equal(hit[2], p)):
+            hit = None
+        if hit is None:
             if capturing:
                 raise self._capture_error("the parameter or gradient set")
-            self._d_tensors = self._upload(tt)
-            self._tensor_key = key
+            hit = (tt, g.copy(), p.copy(), self._upload(tt))
+        self._ptr_cache[fp] = hit
+        while len(self._ptr_cache) > self.TABLE_CACHE:
+            self._ptr_cache.pop(next(iter(self._ptr_cache)))
+        self._d_tensors = hit[3]
+        self._tensor_key = None   # (the bytes key of _match_table no longer applies)
 
     def set_scales(self, items):
         """items: list of (slot tensor, step, S_m, S_v, eps)."""
@@ -726,7 +796,8 @@ class LUMA(Optimizer):
             if r:
                 self._engine.launch(plan.tt, self._group_table(), self._base_seed,
                                     L.NOISE_PHILOX, self._flags,
-                                    self._scaling(self._engine.device), same_table=(r == 1))
+                                    self._scaling(self._engine.device), same_table=(r == 1),
+                                    moved=(r == 2))
                 plan.host.bump_steps(plan.states)
                 return loss
         self._plan = None
@@ -779,10 +850,14 @@ class LUMA(Optimizer):
         # code summaries: SUMMARY_WORDS words per chunk at this step's chunk length
         chunk = engine.chunk_for(np.fromiter((w[2].numel() for w in work), dtype=np.int64,
                                              count=len(work)))
+        # (a tensor below one whole 2048-element iteration, or stepped by a
+        # single wavefront, never reads a summary: it gets none)
+        least = max(_SUMMARY_MIN, engine._wave_limit() + 1)
         no_summ = [(self.state[w[1]], w[2]) for w in work
-                   if self.state[w[1]].get("_summary") is None
-                   or self.state[w[1]]["_summary"].numel() < -(-w[2].numel() // chunk)
-                   * L.SUMMARY_WORDS]
+                   if w[2].numel() >= least and (
+                       self.state[w[1]].get("_summary") is None
+                       or self.state[w[1]]["_summary"].numel() < -(-w[2].numel() // chunk)
+                       * L.SUMMARY_WORDS)]
         if no_summ and not capturing:   # (under capture, a short array is only used less)
             for (state, _), sm in zip(no_summ, summary_arena([p for _, p in no_summ],
                                                              engine.device, chunk)):
@@ -812,7 +887,8 @@ class LUMA(Optimizer):
             if grad.stride() != param.stride() or not _is_dense(grad):
                 grad = torch.empty_like(param, dtype=grad.dtype).copy_(grad)
             u_m, u_w = self._take_noise(p, param)
-            summ = state.get("_summary") if self._summaries else None
+            summ = (state.get("_summary") if self._summaries and param.numel() >= least
+                    else None)
             rows.append((param, grad, state["Q_m"], state["Q_w"], u_m, u_w, state["_slot"],
                          state["param_id"], code, gi, shard_offset(p), summ))
         tt = engine.table(rows)
@@ -821,7 +897,7 @@ class LUMA(Optimizer):
         # host count of step() calls; the kernels use the slot's device count
         for state in states:
             state["step"] += 1
-        if noise_mode == L.NOISE_PHILOX and _Plan.usable(work, rows):
+        if noise_mode == L.NOISE_PHILOX and engine.host is not None and _Plan.usable(work, rows):
             self._plan = _Plan(self.param_groups, work, rows, states, tt, engine.host)
             self._plan.chunk_setting = engine.chunk_elems
         self._noise = None

@@ -54,12 +54,15 @@ def test_plan_steps_like_a_rebuilt_table():
     matches = []
 
     def count(engine):
-        orig = engine._match_table
+        # table checks: a full comparison (_match_table) or, for a planned
+        # table whose pointers moved, the pointer-set lookup (_match_pointers)
+        for name in ("_match_table", "_match_pointers"):
+            orig = getattr(engine, name)
 
-        def wrapped(tt, capturing):
-            matches.append(len(tt))
-            return orig(tt, capturing)
-        engine._match_table = wrapped
+            def wrapped(tt, capturing, orig=orig):
+                matches.append(len(tt))
+                return orig(tt, capturing)
+            setattr(engine, name, wrapped)
 
     def set_grads(gs):
         for p, q, g in zip(a, b, gs):
@@ -86,10 +89,25 @@ def test_plan_steps_like_a_rebuilt_table():
     assert len(matches) == n0 and oa._plan is not None
     _same(a, b, oa, ob)
 
-    # new gradient tensors: the pointers are refreshed and the table uploaded
+    # new gradient tensors: the pointers are refreshed and the table looked
+    # up by its pointers (uploaded, as these pointers are new)
     set_grads(grads())
     _step(oa, ob)
     assert len(matches) == n0 + 1 and oa._plan is not None
+    _same(a, b, oa, ob)
+
+    # gradients alternating between two sets of buffers: each set's table is
+    # uploaded once and then re-used
+    sets = [grads(), grads()]
+    uploads = []
+    up = oa._engine._upload
+    oa._engine._upload = lambda arr: uploads.append(len(arr)) or up(arr)
+    for k in range(4):
+        for p, q, g in zip(a, b, sets[k % 2]):
+            p.grad, q.grad = g, g.clone()
+        _step(oa, ob)
+    oa._engine._upload = up
+    assert uploads == [len(SHAPES)] * 2 and oa._plan is not None
     _same(a, b, oa, ob)
 
     # bf16 gradients: the plan no longer applies, the table is rebuilt

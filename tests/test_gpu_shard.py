@@ -205,3 +205,53 @@ def test_dtensor_local_shard_world_size_one():
         assert sd["S_m"] == sp["S_m"] and sd["S_v"] == sp["S_v"] and sd["step"] == 3
     finally:
         dist.destroy_process_group()
+
+
+def test_dtensor_export_adamw_state_per_shard():
+    """export_adamw_state of a DTensor parameter (Shard(0) on a one-GPU mesh)
+    decodes its local shard (optimizer.py:189-250, tests/test_fsdp.py:187-215):
+    exp_avg / exp_avg_sq have the local shard's shape, equal the plain
+    tensor's export bit for bit, and equal the oracle's export of the same
+    shard (stepped with the oracle's own uniforms) within 1e-6."""
+    import torch.distributed as dist
+    from torch.distributed.device_mesh import init_device_mesh
+    from torch.distributed.tensor import Shard, distribute_tensor
+
+    dist.init_process_group("nccl", init_method=f"tcp://127.0.0.1:{_free_port()}", rank=0,
+                            world_size=1)
+    try:
+        mesh = init_device_mesh("cuda", (1,))
+        gen = torch.Generator().manual_seed(6)
+        w0 = torch.randn(80, 48, generator=gen) * 0.02
+        dp = torch.nn.Parameter(distribute_tensor(w0.cuda(), mesh, [Shard(0)]))
+        pp = torch.nn.Parameter(w0.cuda())
+        cpu = w0.clone()
+        od, op_ = LUMA([dp], **HYPER), LUMA([pp], **HYPER)
+        od._base_seed = op_._base_seed = BASE
+        oracle = O.OracleLUMA([dict(params=[cpu], **HYPER)], BASE, "cr")
+        for t in range(4):
+            g = torch.randn(80, 48, generator=gen) * 1e-3
+            cpu.grad = g
+            oracle.step()
+            u = tuple(x.reshape(80, 48).cuda() for x in oracle.last_draws[0])
+            dp.grad = distribute_tensor(g.cuda(), mesh, [Shard(0)])
+            pp.grad = g.cuda()
+            od.inject_noise({dp: u})
+            op_.inject_noise({pp: u})
+            od.step()
+            op_.step()
+        torch.cuda.synchronize()
+        ed, ep = od.export_adamw_state(), op_.export_adamw_state()
+        eo = oracle.export_adamw_state()
+        sd, sp, so = ed["state"][0], ep["state"][0], eo["state"][0]
+        local = od._unwrap_tensor(dp)
+        for key in ("exp_avg", "exp_avg_sq"):
+            assert sd[key].shape == local.shape
+            assert torch.equal(sd[key], sp[key]), key
+            ref = so[key].reshape(local.shape)
+            err = float((sd[key].cpu() - ref).abs().max()) / max(float(ref.abs().max()), 1e-30)
+            assert err <= 1e-6, (key, err)
+        assert float(sd["step"]) == float(so["step"]) == 4.0
+        assert ed["param_groups"] == ep["param_groups"]
+    finally:
+        dist.destroy_process_group()

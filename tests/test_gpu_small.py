@@ -1,4 +1,6 @@
-"""Small tensors stepped one wavefront each (LumaStepArgs.small_chunks).
+"""Small tensors stepped one wavefront each (LumaStepArgs.small_chunks), and
+medium tensors stepped by one-wavefront workgroups of the fast kernels
+(LumaStepArgs.medium_chunks).
 
 Tensors of at most LUMA_SMALL_TENSOR elements take the last chunk records
 and the wavefront kernels (exact path).  Their results must be the oracle's,
@@ -89,3 +91,44 @@ def test_small_route_matches_workgroup_route():
         assert sa[i]["S_m"] == sb[i]["S_m"] and sa[i]["S_v"] == sb[i]["S_v"], i
         d = float((p.detach() - q.detach()).abs().max())
         assert d <= 1e-6 * float(q.detach().abs().max()) + 1e-8, (i, d)
+
+
+# medium tensors: above LUMA_SMALL_TENSOR and up to LUMA_MEDIUM_TENSOR
+# elements, a one-wavefront workgroup each through the fast kernels
+MEDIUM = [513, 600, 1000, 2047, 2048, 2049, 3000, 4095, 4096, 4097, 1, 300, 70000, 9000]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_medium_tensors_match_oracle(dtype):
+    gen = torch.Generator(device=DEV).manual_seed(21)
+    params = [(torch.randn(n, device=DEV, generator=gen) * 0.02) for n in MEDIUM]
+    pair = SampledPair(params, range(len(MEDIUM)))
+    for t in range(1, 5):
+        g = torch.Generator(device=DEV).manual_seed(700 + t)
+        gd = [normal_grad(p.shape, 1e-3, g, DEV, dtype, outliers=1e-2, zeros=0.02)
+              for p in pair.params]
+        pair.step(gd, {i: x.cpu() for i, x in enumerate(gd)})
+        pair.check()
+        eng = pair.opt._engine
+        assert eng._medium_chunks == sum(1 for n in MEDIUM if L.SMALL_TENSOR < n <= L.MEDIUM_TENSOR)
+        assert eng._small_chunks == sum(1 for n in MEDIUM if n <= L.SMALL_TENSOR)
+
+
+def test_medium_route_for_every_tensor(monkeypatch):
+    """Step 2 routes every tensor of one chunk (here up to 16384 elements)
+    through one-wavefront workgroups, step 3 none, step 4 the default: every
+    step matches the oracle, and the code summaries that step 2 did not
+    write are not used by step 3."""
+    pair = SampledPair(_params(13), range(len(SIZES)))
+    _step(pair, 1)
+    monkeypatch.setattr(L, "MEDIUM_TENSOR", 1 << 20)
+    _step(pair, 2)
+    eng = pair.opt._engine
+    assert eng._medium_chunks == sum(1 for n in SIZES if L.SMALL_TENSOR < n <= eng._chunk)
+    monkeypatch.setattr(L, "MEDIUM_TENSOR", 4096)
+    eng.medium_tensors = False
+    _step(pair, 3)
+    assert eng._medium_chunks == 0
+    eng.medium_tensors = True
+    _step(pair, 4)
+    assert eng._medium_chunks > 0

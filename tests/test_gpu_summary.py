@@ -76,8 +76,10 @@ def _check_bounds(opt, params, t):
         slot = st["_slot"]
         summ_step = int(slot[8:16].view(torch.int64).item())
         summ_shift = int(slot[328:332].view(torch.int32).item())
-        if p.numel() <= L.SMALL_TENSOR:
-            # stepped a wavefront each: no summaries, and none claimed
+        if p.numel() <= max(L.SMALL_TENSOR, L.MEDIUM_TENSOR) or p.numel() < 2048:
+            # stepped by a single wavefront (either route), or below one
+            # whole workgroup iteration: no summaries (none allocated), and
+            # none claimed
             assert summ_step == 0, summ_step
             continue
         assert summ_step == st["step"], (summ_step, st["step"])

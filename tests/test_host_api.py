@@ -4,6 +4,7 @@ import ctypes
 import os
 import re
 
+import numpy as np
 import pytest
 import torch
 import torch.nn as nn
@@ -16,12 +17,15 @@ from luma_amd.optimizer import make_step_seed
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def _engine_stub(chunk_elems=0, small_tensors=True):
+def _engine_stub(chunk_elems=0, small_tensors=True, medium_tensors=False):
     """The attributes _Engine.chunk_for and _Engine.chunk_layout read."""
     import types
     from luma_amd.optimizer import _Engine
-    eng = types.SimpleNamespace(chunk_elems=chunk_elems, small_tensors=small_tensors)
+    eng = types.SimpleNamespace(chunk_elems=chunk_elems, small_tensors=small_tensors,
+                                medium_tensors=medium_tensors)
     eng._small_limit = lambda: _Engine._small_limit(eng)
+    eng._medium_limit = lambda: _Engine._medium_limit(eng)
+    eng._wave_limit = lambda: _Engine._wave_limit(eng)
     return eng
 
 
@@ -180,9 +184,35 @@ def test_step_rejects_bad_chunk_length():
     for bad in (1000, 1024, 262144, 3 * 4096):
         args = L.StepArgs(tensors=16, n_tensors=1, n_chunks=1, chunks=16, groups=16, partials=16,
                           base_seed=0, noise_mode=L.NOISE_PHILOX, flags=0, chunk_elems=bad,
-                          reserved=0, scaling=L.Scaling(None, None))
+                          small_chunks=0, medium_chunks=0, scaling=L.Scaling(None, None))
         assert lib.luma_step(ctypes.byref(args), None) != 0
         assert b"chunk_elems" in lib.luma_last_error()
+
+
+def test_step_rejects_bad_small_chunks():
+    """luma_step validates small_chunks (0 .. n_chunks) before any launch."""
+    lib = L.load()
+    for bad in (-1, 3):
+        args = L.StepArgs(tensors=16, n_tensors=1, n_chunks=2, chunks=16, groups=16, partials=16,
+                          base_seed=0, noise_mode=L.NOISE_PHILOX, flags=0, chunk_elems=0,
+                          small_chunks=bad, scaling=L.Scaling(None, None))
+        assert lib.luma_step(ctypes.byref(args), None) != 0
+        assert b"small_chunks" in lib.luma_last_error()
+    for small, bad in ((0, -1), (0, 3), (1, 2)):
+        args = L.StepArgs(tensors=16, n_tensors=1, n_chunks=2, chunks=16, groups=16, partials=16,
+                          base_seed=0, noise_mode=L.NOISE_PHILOX, flags=0, chunk_elems=0,
+                          small_chunks=small, medium_chunks=bad, scaling=L.Scaling(None, None))
+        assert lib.luma_step(ctypes.byref(args), None) != 0
+        assert b"medium_chunks" in lib.luma_last_error()
+
+
+def test_step_args_fields():
+    """The ctypes binding has exactly the header's LumaStepArgs fields (a
+    misspelt keyword would otherwise become a plain Python attribute)."""
+    names = [f[0] for f in L.StepArgs._fields_]
+    assert names == ["tensors", "n_tensors", "n_chunks", "chunks", "groups", "partials",
+                     "base_seed", "noise_mode", "flags", "chunk_elems", "small_chunks",
+                     "medium_chunks", "reserved", "scaling"]
 
 
 def test_package_exports():
@@ -219,7 +249,7 @@ def test_chunk_layout_small_tensors_last():
     from luma_amd.optimizer import _Engine
     numels = np.array([5000, 3, 512, 513, 40000, 1, 20000], dtype=np.int64)
     eng = _engine_stub(small_tensors=True)
-    first, ch, n_small = _Engine.chunk_layout(eng, numels, 16384)
+    first, ch, n_small, n_med = _Engine.chunk_layout(eng, numels, 16384)
     assert n_small == 3
     assert ch["tensor"].tolist() == [0, 3, 4, 4, 4, 6, 6, 2, 1, 5]
     assert ch["index"].tolist() == [0, 0, 0, 1, 2, 0, 1, 0, 0, 0]
@@ -227,7 +257,7 @@ def test_chunk_layout_small_tensors_last():
     for t in range(len(numels)):
         assert ch["tensor"][first[t]] == t and ch["index"][first[t]] == 0
     eng.small_tensors = False
-    first, ch, n_small = _Engine.chunk_layout(eng, numels, 16384)
+    first, ch, n_small, n_med = _Engine.chunk_layout(eng, numels, 16384)
     assert n_small == 0
     assert ch["tensor"].tolist() == [0, 1, 2, 3, 4, 4, 4, 5, 6, 6]
     assert first.tolist() == [0, 1, 2, 3, 4, 7, 8]
@@ -243,18 +273,73 @@ def test_chunk_layout_many_tensors_largest_first(monkeypatch):
     eng = _engine_stub()
     monkeypatch.setattr(O, "STEP_TARGET_CHUNKS", 5)
     assert O._Engine.chunk_for(eng, numels) == 65536
-    first, ch, n_small = O._Engine.chunk_layout(eng, numels, 65536)
+    first, ch, n_small, n_med = O._Engine.chunk_layout(eng, numels, 65536)
     assert n_small == 3
     assert ch["tensor"].tolist() == [4, 6, 0, 7, 3, 2, 1, 5]
     assert ch["index"].tolist() == [0] * 8
     for t in range(len(numels)):
         assert ch["tensor"][first[t]] == t
     # chunks of 16384: the 40000-element tensor's three records stay together
-    first, ch, n_small = O._Engine.chunk_layout(eng, numels, 16384)
+    first, ch, n_small, n_med = O._Engine.chunk_layout(eng, numels, 16384)
     assert ch["tensor"].tolist() == [4, 4, 4, 6, 6, 0, 7, 3, 2, 1, 5]
     assert ch["index"].tolist() == [0, 1, 2, 0, 1, 0, 0, 0, 0, 0, 0]
     assert first.tolist() == [5, 9, 8, 7, 0, 10, 3, 6]
     # one tensor fewer above the limit: parameter order
     monkeypatch.setattr(O, "STEP_TARGET_CHUNKS", 6)
-    first, ch, n_small = O._Engine.chunk_layout(eng, numels, 65536)
+    first, ch, n_small, n_med = O._Engine.chunk_layout(eng, numels, 65536)
     assert ch["tensor"].tolist() == [0, 3, 4, 6, 7, 2, 1, 5]
+
+
+def test_chunk_layout_medium_tensors():
+    """Tensors above SMALL_TENSOR and of at most MEDIUM_TENSOR elements (and
+    one chunk) take the records before the small ones, largest first; the
+    workgroup tensors keep their order and come first."""
+    import numpy as np
+    from luma_amd.optimizer import _Engine
+    numels = np.array([5000, 3, 512, 513, 40000, 1, 20000, 4096, 2000], dtype=np.int64)
+    eng = _engine_stub(medium_tensors=True)
+    first, ch, n_small, n_med = _Engine.chunk_layout(eng, numels, 16384)
+    assert (n_med, n_small) == (3, 3)
+    assert ch["tensor"].tolist() == [0, 4, 4, 4, 6, 6, 7, 8, 3, 2, 1, 5]
+    assert ch["index"].tolist() == [0, 0, 1, 2, 0, 1, 0, 0, 0, 0, 0, 0]
+    for t in range(len(numels)):
+        assert ch["tensor"][first[t]] == t and ch["index"][first[t]] == 0
+    # a chunk shorter than the medium limit: only tensors of one chunk qualify
+    first, ch, n_small, n_med = _Engine.chunk_layout(eng, numels, 2048)
+    assert (n_med, n_small) == (2, 3)
+    assert ch["tensor"].tolist()[-5:] == [8, 3, 2, 1, 5]
+    # 4096 or more tensors above the medium limit decide the one-chunk-per-tensor rule
+    assert _Engine.chunk_for(eng, np.array([3000] * 5000 + [40000], dtype=np.int64)) == 16384
+    assert _Engine.chunk_for(eng, np.array([5000] * 4096 + [40000], dtype=np.int64)) == 65536
+
+
+def test_moved_pointer_tables_are_reused():
+    """A planned step whose gradients alternate between buffers uploads each
+    pointer set's table once (_Engine._match_pointers), and a fingerprint
+    collision or another table object never returns a wrong table."""
+    from luma_amd.optimizer import _Engine
+    eng = _Engine.__new__(_Engine)
+    eng._ptr_cache = {}
+    eng._tensor_key = b""
+    uploads = []
+    eng._upload = lambda arr: uploads.append(arr.copy()) or len(uploads)
+    tt = np.zeros(5, dtype=L.TENSOR_DTYPE)
+    tt["param"] = np.arange(5) * 4096 + (1 << 40)
+    sets = [np.arange(5, dtype=np.uint64) * 512 + (k + 1) * (1 << 36) for k in range(2)]
+    for i in range(6):
+        tt["grad"] = sets[i % 2]
+        eng._match_pointers(tt, capturing=False)
+        assert eng._d_tensors == 1 + (i % 2)          # one upload per pointer set
+        assert np.array_equal(uploads[eng._d_tensors - 1]["grad"], sets[i % 2])
+    assert len(uploads) == 2 and eng._tensor_key is None
+    # the same pointers in another table object: not re-used
+    tt2 = tt.copy()
+    eng._match_pointers(tt2, capturing=False)
+    assert len(uploads) == 3
+    # a cached entry whose columns differ (a forced collision): uploaded afresh
+    fp = list(eng._ptr_cache)[-1]                      # tt2's entry
+    ent = eng._ptr_cache[fp]
+    assert ent[0] is tt2
+    eng._ptr_cache = {fp: (ent[0], ent[1] + 1, ent[2], ent[3])}
+    with pytest.raises(RuntimeError):
+        eng._match_pointers(ent[0], capturing=True)   # would need an upload under capture

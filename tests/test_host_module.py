@@ -93,3 +93,43 @@ def test_refresh_rejects_host_tensors():
     ps[0].grad = torch.ones(4)
     tt = np.zeros(1, dtype=L.TENSOR_DTYPE)
     assert _refresh([{"params": ps}], ps, [1], [0], [L.GRAD_F32], tt) == 0
+
+
+def test_module_records_its_torch():
+    """The module was compiled against this torch (load_host refuses another)."""
+    assert H is not None and H.torch_version == torch.__version__
+
+
+class _Recording(torch.Tensor):
+    """A wrapper subclass with a custom device policy: asking its impl for
+    is_cuda() or device() goes through __torch_dispatch__ (Python)."""
+    calls = 0
+
+    @staticmethod
+    def __new__(cls, elem):
+        return torch.Tensor._make_wrapper_subclass(cls, elem.shape, dtype=elem.dtype,
+                                                   device=elem.device, dispatch_device=True)
+
+    @classmethod
+    def __torch_dispatch__(cls, func, types, args=(), kwargs=None):
+        cls.calls += 1
+        if func is torch.ops.prim.device.default:   # the .grad setter asks for it
+            return torch.device("cpu")
+        raise RuntimeError(f"unexpected {func}")
+
+
+def test_refresh_rejects_a_subclass_gradient_without_python():
+    """With 8192 or more parameters the check runs on worker threads while the
+    caller holds the GIL; a gradient subclass with a custom device policy
+    must be rejected from its dispatch keys, before anything that would call
+    into Python."""
+    n = 3 * 4096
+    ps = [torch.zeros(2, requires_grad=True) for _ in range(n)]
+    for p in ps:
+        p.grad = torch.zeros(2)
+    tt = np.zeros(n, dtype=L.TENSOR_DTYPE)
+    groups = [{"params": ps}]
+    ps[-5].grad = _Recording(torch.zeros(2))
+    _Recording.calls = 0
+    assert _refresh(groups, ps, [1] * n, list(range(n)), [L.GRAD_F32] * n, tt) == 0
+    assert _Recording.calls == 0
