@@ -78,8 +78,8 @@ extern "C" {
 
 /*
  * Tensors above LUMA_SMALL_TENSOR and of at most this many elements are best
- * stepped by a workgroup of one wavefront each (LumaStepArgs.medium_chunks):
- * a workgroup of four would leave most of its wavefronts idle on them.
+ * stepped one wavefront each (LumaStepArgs.medium_chunks): a whole
+ * workgroup would leave most of its wavefronts idle on them.
  */
 #define LUMA_MEDIUM_TENSOR 4096
 
@@ -203,12 +203,12 @@ typedef struct LumaStepArgs {
                                 most LUMA_SMALL_TENSOR elements (any tensor is stepped
                                 correctly).  0: every chunk takes a workgroup */
   int32_t medium_chunks;     /* the medium_chunks records just before the small ones
-                                are stepped by a workgroup of one wavefront each (the
-                                same fast kernels as the others, 8 elements per lane and
-                                iteration); meant for tensors of at most
-                                LUMA_MEDIUM_TENSOR elements, one chunk each (any chunk is
-                                stepped correctly).  Such tensors keep no code summaries.
-                                0: none */
+                                are stepped one wavefront each, four per workgroup, in
+                                the same launches and by the same fast kernels as the
+                                others (8 elements per lane and iteration); meant for
+                                tensors of at most LUMA_MEDIUM_TENSOR elements, one
+                                chunk each (any chunk is stepped correctly).  Such
+                                tensors keep no code summaries.  0: none */
   int32_t reserved;          /* 0 */
   LumaScaling scaling;       /* both NULL: unscaled gradients, always step */
 } LumaStepArgs;
@@ -243,9 +243,8 @@ int64_t luma_summary_words(int64_t numel, int32_t chunk_elems);
  * step count + 1, step scalars), pass 2 (re-decode + EMA + AdamW update +
  * LogSR re-quantisation).  A tensor whose slot holds step count 0 takes the
  * init step.  Three kernel launches on `stream` (a hipStream_t), plus one
- * per pass for the medium tensors (medium_chunks > 0) and one per pass for
- * the small tensors (small_chunks > 0), which follow the workgroup kernels;
- * no host synchronisation.  No device table is written, so the sequence may
+ * per pass for the small tensors (small_chunks > 0), which follow the
+ * workgroup kernels; no host synchronisation.  No device table is written, so the sequence may
  * be captured into a HIP graph and replayed.
  */
 int luma_step(const LumaStepArgs *args, void *stream);

@@ -40,6 +40,8 @@ namespace luma {
 
 constexpr int kThreads = 256;     // 4 wave64 per workgroup
 constexpr int kVec = 8;           // consecutive elements per thread per iteration
+constexpr int kItShift = 11;      // log2(kThreads * kVec): elements per workgroup iteration
+static_assert((1 << kItShift) == kThreads * kVec, "kItShift");
 constexpr int64_t kChunk = LUMA_CHUNK_ELEMS;
 static_assert(kChunk % (kThreads * kVec) == 0, "chunk must be a whole number of iterations");
 static_assert(kChunk <= (1 << 20), "chunk offsets fit the 32-bit word of a pass-2 queue entry");
@@ -80,11 +82,11 @@ static_assert(sizeof(Tensor) == sizeof(LumaTensor), "tensor layout");
 // Where a launch finds its tensors: the device tables of luma_step, or (when
 // `tensors` is null) the single tensor and group passed by value by
 // luma_step_tensor, whose chunks are then the workgroups in order.  The
-// chunk records come in three runs: [0, medium_from) take a workgroup of
-// kThreads each, [medium_from, small_from) a workgroup of one wavefront
-// each (medium tensors, through the same kernels), [small_from, n_chunks)
-// the wavefront-per-tensor exact kernels (small tensors).  A launch over
-// one run starts at record chunk_base.
+// chunk records come in three runs: [0, medium_from) take a workgroup each,
+// [medium_from, small_from) a wavefront each (medium tensors: the pass
+// kernels' workgroups from medium_from on step four such records, one per
+// wavefront, through the same code), [small_from, n_chunks) the
+// wavefront-per-tensor exact kernels (small tensors).
 struct StepSrc {
   const Tensor *tensors;
   const LumaChunk *chunks;
@@ -97,7 +99,19 @@ struct StepSrc {
   int32_t small_from;    // chunks from here on: small tensors, one wavefront each
   int32_t n_chunks;
   int32_t medium_from;   // chunks from here on (to small_from): medium tensors
-  int32_t chunk_base;    // record of this launch's workgroup 0
+  int32_t reserved;
+};
+
+// How a chunk's elements are shared out: among nt threads (kThreads, a whole
+// workgroup; or 64, one wavefront of a medium record), tid this thread's
+// index among them.  An iteration covers nt * kVec consecutive elements.
+// The thread index is recomputed from threadIdx.x where it is used rather
+// than held: a register live across a whole pass body costs spills.
+struct Share {
+  int nt;
+  __device__ __forceinline__ uint32_t tid() const {
+    return nt == kThreads ? threadIdx.x : threadIdx.x & 63u;
+  }
 };
 
 // Elements [beg, end) of chunk ci of tensor T.
@@ -145,19 +159,41 @@ __device__ __forceinline__ float unscale_rt(float g, float inv, int dt) {
   return unscale<LUMA_GRAD_BF16>(g, inv);
 }
 
-// The chunk of this workgroup: its tensor, group and chunk index.
-__device__ __forceinline__ void chunk_job(const StepSrc &src, Tensor &T, LumaGroup &g,
-                                          int64_t &index) {
+// The chunk of this workgroup, or from medium_from on of this wavefront:
+// its record, tensor, group, chunk index and thread share.  False: the
+// wavefront has no record (the last workgroup of the medium run).
+__device__ __forceinline__ bool chunk_job(const StepSrc &src, Tensor &T, LumaGroup &g,
+                                          int64_t &index, int64_t &rec, Share &sh) {
   if (src.tensors) {
-    const LumaChunk c = src.chunks[src.chunk_base + blockIdx.x];
+    if ((int32_t)blockIdx.x < src.medium_from) {
+      rec = blockIdx.x;
+      sh = Share{kThreads};
+    } else {
+      // wave-uniform (readfirstlane): the record and the tensor it names
+      // then load through the scalar cache into scalar registers
+      rec = __builtin_amdgcn_readfirstlane(
+          src.medium_from + (int32_t)(blockIdx.x - (uint32_t)src.medium_from) * (kThreads / 64) +
+          (int32_t)(threadIdx.x >> 6));
+      if (rec >= src.small_from) return false;
+      sh = Share{64};
+    }
+    const LumaChunk c = src.chunks[rec];
     T = src.tensors[c.tensor];
     g = src.groups[T.group];
     index = c.index;
   } else {
     T = src.one;
     g = src.group;
-    index = blockIdx.x;
+    index = rec = blockIdx.x;
+    sh = Share{kThreads};
   }
+  return true;
+}
+
+// Workgroups of a pass-kernel launch: one per workgroup record, one per
+// four medium records.
+__device__ __host__ __forceinline__ int32_t pass_blocks(int32_t medium_from, int32_t small_from) {
+  return medium_from + (small_from - medium_from + kThreads / 64 - 1) / (kThreads / 64);
 }
 
 // The tensor of this workgroup (one workgroup per tensor).
@@ -374,6 +410,20 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(StepSrc src,
   finalize_tensor(src, T, grp, partials);
 }
 
+// The record of a chunk whose threads hold (am, im), (av, iv): the share's
+// argmax (a workgroup's, with barriers, or a wavefront's), put by its
+// thread 0.
+__device__ __forceinline__ void put_chunk(float *partials, int64_t rec, const Share &sh, float am,
+                                          float av, uint32_t im, uint32_t iv) {
+  if (sh.nt == kThreads) {
+    block_argmax2(am, im, av, iv);
+  } else {
+    wave_argmax(am, im);
+    wave_argmax(av, iv);
+  }
+  if (sh.tid() == 0) put_partial(partials, rec, am, av, im, iv);
+}
+
 // m', v' of element i of tensor T (exact path).
 __device__ __forceinline__ void element_ema(const Tensor &T, const Hyper &h, const Grid *old,
                                             int64_t i, bool scaled, float inv, float &mn,
@@ -393,8 +443,9 @@ __global__ __launch_bounds__(kThreads) void pass1_exact_kernel(StepSrc src,
   if (skip_step(src)) return;
   Tensor T;
   LumaGroup grp;
-  int64_t ci;
-  chunk_job(src, T, grp, ci);
+  int64_t ci, rec;
+  Share sh;
+  if (!chunk_job(src, T, grp, ci, rec, sh)) return;   // (wave mode: no barriers below)
   const Hyper h = group_hyper(grp);
   const bool scaled = src.scaling.grad_scale != nullptr;
   const float inv = inv_scale(src);
@@ -406,7 +457,7 @@ __global__ __launch_bounds__(kThreads) void pass1_exact_kernel(StepSrc src,
 
   float am = 0.0f, av = 0.0f;
   uint32_t im = kNoArg, iv = kNoArg;
-  for (int64_t e0 = beg + (int64_t)threadIdx.x * kVec; e0 < end; e0 += (int64_t)blockDim.x * kVec) {
+  for (int64_t e0 = beg + (int64_t)sh.tid() * kVec; e0 < end; e0 += (int64_t)sh.nt * kVec) {
     for (int j = 0; j < kVec; ++j) {
       const int64_t i = e0 + j;
       if (i >= end) break;
@@ -422,8 +473,7 @@ __global__ __launch_bounds__(kThreads) void pass1_exact_kernel(StepSrc src,
       }
     }
   }
-  block_argmax2(am, im, av, iv);
-  if (threadIdx.x == 0) put_partial(partials, src.chunk_base + blockIdx.x, am, av, im, iv);
+  put_chunk(partials, rec, sh, am, av, im, iv);
 }
 
 // ---------------------------------------------------------------------------
@@ -524,8 +574,9 @@ __global__ __launch_bounds__(kThreads) void pass2_exact_kernel(StepSrc src, uint
   if (skip_step(src)) return;
   Tensor T;
   LumaGroup grp;
-  int64_t ci;
-  chunk_job(src, T, grp, ci);
+  int64_t ci, rec;
+  Share sh;
+  if (!chunk_job(src, T, grp, ci, rec, sh)) return;
   const bool scaled = src.scaling.grad_scale != nullptr;
   const float inv = inv_scale(src);
   const Slot &S = *(const Slot *)T.slot;
@@ -540,7 +591,7 @@ __global__ __launch_bounds__(kThreads) void pass2_exact_kernel(StepSrc src, uint
   const PhiloxBase pb = philox_base(T.elem_offset);
   const bool inj = injected(T, noise_mode);
 
-  for (int64_t e0 = beg + (int64_t)threadIdx.x * kVec; e0 < end; e0 += (int64_t)blockDim.x * kVec)
+  for (int64_t e0 = beg + (int64_t)sh.tid() * kVec; e0 < end; e0 += (int64_t)sh.nt * kVec)
     exact_group(T, h, old, G, e0, end, scaled, inv, inj, pb, k0, k1);
 }
 
@@ -1089,10 +1140,11 @@ __device__ __forceinline__ void unpack_grads(const Raw8 &r, Group8 &G) {
 // iteration first bounds its block from the summary and the gradients, and
 // loads the block's codes only when some lane's bound reaches the
 // thresholds: most blocks cost their gradients alone.
-template <int GD, bool SMALL, bool SCALED, bool SUMM>
+template <int GD, bool SMALL, bool SCALED, bool SUMM, int NT>
 __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOBAL Grid *old,
                                 float inv, int64_t ci, int64_t beg, int64_t end, float &exm,
-                                float &exv, uint32_t &exi_m, uint32_t &exi_v, uint32_t *queue) {
+                                float &exv, uint32_t &exi_m, uint32_t &exi_v, uint32_t *queue,
+                                Share sh) {
   const Bounds B = make_bounds((const Grid *)old, nullptr, h.beta1, h.beta2);
   const DecodeK D = decode_consts(old, h.eps);
   P1Const K;
@@ -1199,8 +1251,9 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   // a wave stops once all its groups lie past the end.
   // Threads per chunk: kThreads, or one wavefront for a medium tensor; an
   // iteration covers nt * kVec consecutive elements.
-  const int nt = (int)blockDim.x;
-  const int it_shift = __builtin_ctz((unsigned)nt) + 3;
+  constexpr int nt = NT;
+  constexpr int it_shift = NT == kThreads ? kItShift : kItShift - 2;  // 64 = kThreads / 4
+  static_assert(NT == kThreads || NT == 64, "a workgroup or one wavefront per chunk");
   const int64_t kStride = (int64_t)1 << it_shift;
   const int n_it = (int)((end - beg + kStride - 1) >> it_shift);
   // Iterations in which every lane's group is whole run in a loop of their
@@ -1215,7 +1268,7 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     // same thread of the same chunk) and, once, the decode of its code
     // bound; each iteration then bounds with the lane's largest |g| alone.
     static_assert(LUMA_SUMMARY_WORDS == kThreads, "one summary word per thread of a chunk");
-    const uint32_t sw = T.summary[ci * LUMA_SUMMARY_WORDS + threadIdx.x];
+    const uint32_t sw = T.summary[ci * LUMA_SUMMARY_WORDS + sh.tid()];
     const FastEma d = fast_ema<SMALL ? kRegSmall : kRegGeneral, false>((int)(sw & 0xFFFFu), (int)(kCodeFloat | (sw >> 16)),
                                              0.0f, K.dm, K.ndw, K.nbias, K.iwmin, K.eps, K.b1,
                                              K.omb1, K.b2, K.omb2, K.sign);
@@ -1224,7 +1277,7 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     // p1_reach); only when it reaches a threshold in some lane are the
     // wave's codes read and decoded.
     auto visit = [&](const Raw8 &cur, int j) {
-      const int64_t e0 = beg + ((int64_t)j * nt + threadIdx.x) * kVec;
+      const int64_t e0 = beg + ((int64_t)j * nt + sh.tid()) * kVec;
       {
         const float g = raw_gmax<GD, SCALED>(cur, K.inv);
         const float mn = fmaf(K.b1, d.am, K.omb1 * g);
@@ -1255,7 +1308,7 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     // single buffer carried across iterations) would make every iteration
     // wait for the load just issued.
     auto group_at = [&](int j) {
-      return beg + ((int64_t)(j < n_whole ? j : n_whole - 1) * nt + threadIdx.x) * kVec;
+      return beg + ((int64_t)(j < n_whole ? j : n_whole - 1) * nt + sh.tid()) * kVec;
     };
     Raw8 ra, rb;
     load_grads<GD>(T, group_at(0), ra);
@@ -1270,10 +1323,10 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     it = n_whole;
   } else if (n_whole > 0) {
     Raw8 raw;
-    load_raw<GD>(T, beg + (int64_t)threadIdx.x * kVec, raw);
+    load_raw<GD>(T, beg + (int64_t)sh.tid() * kVec, raw);
     seed_thresholds();
     for (; it < n_whole; ++it) {
-      const int64_t e0 = beg + ((int64_t)it * nt + threadIdx.x) * kVec;
+      const int64_t e0 = beg + ((int64_t)it * nt + sh.tid()) * kVec;
       const int64_t en = end - e0 - kStride >= kVec ? e0 + kStride : e0;
       uint32_t am[kVec], av[kVec];
       p1_iter<GD, SMALL, SCALED, true, true>(T, K, e0, kVec, raw, en, Tm, Tv, am, av);
@@ -1283,8 +1336,8 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   if (n_whole == 0) seed_thresholds();
   for (; it < n_it; ++it) {
     // a wave whose groups all lie past the end is done (small tensors)
-    if (beg + ((int64_t)it * nt + (threadIdx.x & ~63u)) * kVec >= end) break;
-    const int64_t e0 = beg + ((int64_t)it * nt + threadIdx.x) * kVec;
+    if (beg + ((int64_t)it * nt + (sh.tid() & ~63u)) * kVec >= end) break;
+    const int64_t e0 = beg + ((int64_t)it * nt + sh.tid()) * kVec;
     const int64_t rem = end - e0;
     const int n = rem <= 0 ? 0 : (rem < kVec ? (int)rem : kVec);
     uint32_t am[kVec], av[kVec];
@@ -1310,8 +1363,8 @@ struct InitMax {
 // copy of the record stays in registers.
 template <int GD>
 __device__ __noinline__ InitMax pass1_init_scan(const LUMA_GLOBAL void *grad, int64_t beg,
-                                                int64_t end, bool vec_ok) {
-  const int64_t kStride = (int64_t)blockDim.x * kVec;
+                                                int64_t end, bool vec_ok, Share sh) {
+  const int64_t kStride = (int64_t)sh.nt * kVec;
   Tensor T{};
   T.grad = grad;
   InitMax r{0u, kNoArg};
@@ -1322,7 +1375,7 @@ __device__ __noinline__ InitMax pass1_init_scan(const LUMA_GLOBAL void *grad, in
       r.gi = (uint32_t)(i - beg);
     }
   };
-  for (int64_t e0 = beg + (int64_t)threadIdx.x * kVec; e0 < end; e0 += kStride) {
+  for (int64_t e0 = beg + (int64_t)sh.tid() * kVec; e0 < end; e0 += kStride) {
     if (vec_ok && end - e0 >= kVec) {
       Raw8 rw;
       load_grads<GD>(T, e0, rw);
@@ -1337,35 +1390,39 @@ __device__ __noinline__ InitMax pass1_init_scan(const LUMA_GLOBAL void *grad, in
   return r;
 }
 
-template <int GD, bool SUMM>
+template <int GD, bool SUMM, int NT>
 __device__ __forceinline__ void pass1_dispatch_s(const Tensor &T, const Hyper &h,
                                                  const LUMA_GLOBAL Grid *old, float inv,
                                                  int64_t ci, int64_t beg, int64_t end, bool small,
                                                  bool scaled, float &exm, float &exv,
-                                                 uint32_t &im, uint32_t &iv, uint32_t *q) {
+                                                 uint32_t &im, uint32_t &iv, uint32_t *q, Share sh) {
   if (scaled) {
     if (small)
-      pass1_fast_body<GD, true, true, SUMM>(T, h, old, inv, ci, beg, end, exm, exv, im, iv, q);
+      pass1_fast_body<GD, true, true, SUMM, NT>(T, h, old, inv, ci, beg, end, exm, exv, im, iv, q, sh);
     else
-      pass1_fast_body<GD, false, true, SUMM>(T, h, old, inv, ci, beg, end, exm, exv, im, iv, q);
+      pass1_fast_body<GD, false, true, SUMM, NT>(T, h, old, inv, ci, beg, end, exm, exv, im, iv, q, sh);
   } else {
     if (small)
-      pass1_fast_body<GD, true, false, SUMM>(T, h, old, inv, ci, beg, end, exm, exv, im, iv, q);
+      pass1_fast_body<GD, true, false, SUMM, NT>(T, h, old, inv, ci, beg, end, exm, exv, im, iv, q, sh);
     else
-      pass1_fast_body<GD, false, false, SUMM>(T, h, old, inv, ci, beg, end, exm, exv, im, iv, q);
+      pass1_fast_body<GD, false, false, SUMM, NT>(T, h, old, inv, ci, beg, end, exm, exv, im, iv, q, sh);
   }
 }
 
+// Summaries are kept for workgroup chunks only, so the wavefront form has
+// no summary variant.
 template <int GD>
 __device__ __forceinline__ void pass1_dispatch(const Tensor &T, const Hyper &h,
                                                const LUMA_GLOBAL Grid *old, float inv, int64_t ci,
                                                int64_t beg, int64_t end, bool small, bool scaled,
                                                bool summ, float &exm, float &exv, uint32_t &im,
-                                               uint32_t &iv, uint32_t *q) {
-  if (summ)
-    pass1_dispatch_s<GD, true>(T, h, old, inv, ci, beg, end, small, scaled, exm, exv, im, iv, q);
+                                               uint32_t &iv, uint32_t *q, Share sh) {
+  if (sh.nt != kThreads)
+    pass1_dispatch_s<GD, false, 64>(T, h, old, inv, ci, beg, end, small, scaled, exm, exv, im, iv, q, sh);
+  else if (summ)
+    pass1_dispatch_s<GD, true, kThreads>(T, h, old, inv, ci, beg, end, small, scaled, exm, exv, im, iv, q, sh);
   else
-    pass1_dispatch_s<GD, false>(T, h, old, inv, ci, beg, end, small, scaled, exm, exv, im, iv, q);
+    pass1_dispatch_s<GD, false, kThreads>(T, h, old, inv, ci, beg, end, small, scaled, exm, exv, im, iv, q, sh);
 }
 
 // Whether pass 1 may use chunk ci's code summaries: the previous step's
@@ -1373,8 +1430,9 @@ __device__ __forceinline__ void pass1_dispatch(const Tensor &T, const Hyper &h,
 // fit in the array, its grid is finite, and the tensor's streams are 16-byte
 // aligned (the whole-group loop).
 __device__ __forceinline__ bool summaries_valid(const Tensor &T, const LUMA_GLOBAL Grid *old,
-                                                int64_t prev, int64_t ci, int32_t shift) {
-  return blockDim.x == kThreads && T.summary != nullptr &&
+                                                int64_t prev, int64_t ci, int32_t shift,
+                                                const Share &sh) {
+  return sh.nt == kThreads && T.summary != nullptr &&
          (ci + 1) * LUMA_SUMMARY_WORDS <= T.summary_words &&
          old != nullptr && T.slot->summ_step == prev && T.slot->summ_shift == shift &&
          __builtin_isfinite(old->dm) && __builtin_isfinite(old->dw) &&
@@ -1386,8 +1444,9 @@ __global__ __launch_bounds__(kThreads, 4) void pass1_fast_kernel(StepSrc src,
   if (skip_step(src)) return;
   Tensor T;
   LumaGroup grp;
-  int64_t ci;
-  chunk_job(src, T, grp, ci);
+  int64_t ci, rec;
+  Share sh;
+  if (!chunk_job(src, T, grp, ci, rec, sh)) return;   // (wave mode: no barriers below)
   const Hyper h = group_hyper(grp);
   // this step is t = step + 1; its decode reads the grid of step t - 1
   const int64_t prev = T.slot->step;
@@ -1399,15 +1458,15 @@ __global__ __launch_bounds__(kThreads, 4) void pass1_fast_kernel(StepSrc src,
   const float inv = inv_scale(src);
   __shared__ uint32_t qbuf[kThreads / 64][kQueueCap];
   uint32_t *q = qbuf[threadIdx.x >> 6];
-  const bool summ = summaries_valid(T, old, prev, ci, src.chunk_shift);
+  const bool summ = summaries_valid(T, old, prev, ci, src.chunk_shift, sh);
   float exm = 0.0f, exv = 0.0f;
   uint32_t exi_m = kNoArg, exi_v = kNoArg;
   if (old == nullptr) {
     const bool vec_ok = tensor_vec_ok(T);
     const InitMax r =
-        T.grad_dtype == LUMA_GRAD_BF16  ? pass1_init_scan<LUMA_GRAD_BF16>(T.grad, beg, end, vec_ok)
-        : T.grad_dtype == LUMA_GRAD_F16 ? pass1_init_scan<LUMA_GRAD_F16>(T.grad, beg, end, vec_ok)
-                                        : pass1_init_scan<LUMA_GRAD_F32>(T.grad, beg, end, vec_ok);
+        T.grad_dtype == LUMA_GRAD_BF16  ? pass1_init_scan<LUMA_GRAD_BF16>(T.grad, beg, end, vec_ok, sh)
+        : T.grad_dtype == LUMA_GRAD_F16 ? pass1_init_scan<LUMA_GRAD_F16>(T.grad, beg, end, vec_ok, sh)
+                                        : pass1_init_scan<LUMA_GRAD_F32>(T.grad, beg, end, vec_ok, sh);
     // unscaling is monotone in |g|: only the largest is unscaled
     float g = __uint_as_float(r.gb);
     if (scaled) g = unscale_rt(g, inv, T.grad_dtype);
@@ -1418,15 +1477,14 @@ __global__ __launch_bounds__(kThreads, 4) void pass1_fast_kernel(StepSrc src,
     exi_m = exi_v = r.gi;
   } else if (T.grad_dtype == LUMA_GRAD_BF16)
     pass1_dispatch<LUMA_GRAD_BF16>(T, h, old, inv, ci, beg, end, small, scaled, summ, exm, exv,
-                                   exi_m, exi_v, q);
+                                   exi_m, exi_v, q, sh);
   else if (T.grad_dtype == LUMA_GRAD_F16)
     pass1_dispatch<LUMA_GRAD_F16>(T, h, old, inv, ci, beg, end, small, scaled, summ, exm, exv,
-                                  exi_m, exi_v, q);
+                                  exi_m, exi_v, q, sh);
   else
     pass1_dispatch<LUMA_GRAD_F32>(T, h, old, inv, ci, beg, end, small, scaled, summ, exm, exv,
-                                  exi_m, exi_v, q);
-  block_argmax2(exm, exi_m, exv, exi_v);
-  if (threadIdx.x == 0) put_partial(partials, src.chunk_base + blockIdx.x, exm, exv, exi_m, exi_v);
+                                  exi_m, exi_v, q, sh);
+  put_chunk(partials, rec, sh, exm, exv, exi_m, exi_v);
 }
 
 // Inclusive prefix sum over the 64 lanes of a wave (all lanes active): three
@@ -1784,7 +1842,8 @@ __device__ __forceinline__ uint32_t p2_iter(const Tensor &T, const P2Const &C, i
 template <int GD, bool INJ, int REG, bool SCALED, int KTAG>
 __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOBAL Grid *old,
                                 const LUMA_GLOBAL Grid *nw, float inv, int64_t ci, int64_t beg,
-                                int64_t end, uint32_t k0, uint32_t k1, uint4 *queue) {
+                                int64_t end, uint32_t k0, uint32_t k1, uint4 *queue,
+                                Share sh) {
   const Bounds B = make_bounds((const Grid *)old, (const Grid *)nw, h.beta1, h.beta2);
   P2Const C;
   C.D = decode_consts(old, h.eps);
@@ -1879,7 +1938,7 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   };
   // Threads per chunk: kThreads, or one wavefront for a medium tensor; an
   // iteration covers nt * kVec = 1 << it_shift consecutive elements.
-  const int nt = (int)blockDim.x;
+  const int nt = sh.nt;
   const int it_shift = __builtin_ctz((unsigned)nt) + 3;
   // Staging: whole-group iterations [staged_lo, staged_hi) keep their
   // preconditioner codes in stage[(it % kStage) * 64 + lane] until written
@@ -2009,7 +2068,7 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   auto write_back = [&](int j) {
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     const uint4 v = stage[(j % kStage) * 64 + lane];
-    const int64_t e = beg + ((int64_t)j * nt + threadIdx.x) * kVec;
+    const int64_t e = beg + ((int64_t)j * nt + sh.tid()) * kVec;
     vu4 w;
     w.x = v.x; w.y = v.y; w.z = v.z; w.w = v.w;
     store_stream(w, (LUMA_GLOBAL vu4 *)(T.q_w + e));
@@ -2029,7 +2088,7 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   // flight would make the copy wait for them); past the last whole group the
   // loads repeat the last group, and are not used.
   auto group_at = [&](int j) {
-    return beg + ((int64_t)(j < n_whole ? j : n_whole - 1) * nt + threadIdx.x) * kVec;
+    return beg + ((int64_t)(j < n_whole ? j : n_whole - 1) * nt + sh.tid()) * kVec;
   };
   auto whole_iter = [&](const P2Raw &R, int j) {
     const int64_t e0 = group_at(j);
@@ -2066,8 +2125,8 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   staged_lo = staged_hi = 0;
   for (; it < n_it; ++it) {
     // a wave whose groups all lie past the end is done (small tensors)
-    if (beg + ((int64_t)it * nt + (threadIdx.x & ~63u)) * kVec >= end) break;
-    const int64_t e0 = beg + ((int64_t)it * nt + threadIdx.x) * kVec;
+    if (beg + ((int64_t)it * nt + (sh.tid() & ~63u)) * kVec >= end) break;
+    const int64_t e0 = beg + ((int64_t)it * nt + sh.tid()) * kVec;
     const int64_t rem = end - e0;
     const int n = rem <= 0 ? 0 : (rem < kVec ? (int)rem : kVec);
     Group8 Q;
@@ -2091,7 +2150,7 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     const int mn = min((int)(int16_t)(acc.mn & 0xFFFFu), (int)(int16_t)(acc.mn >> 16));
     const uint32_t qa = (uint32_t)max(mx, -mn), qw = min(acc.wn & 0xFFFFu, acc.wn >> 16);
     const uint32_t a = min(qa + marg_m, 32767u), w = qw > marg_w ? qw - marg_w : 0u;
-    T.summary[ci * LUMA_SUMMARY_WORDS + threadIdx.x] = a | (w << 16);
+    T.summary[ci * LUMA_SUMMARY_WORDS + sh.tid()] = a | (w << 16);
   }
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   if (lane < qlen_m) run_m(queue_m[(head_m + lane) & (kQueueCapM - 1)]);
@@ -2103,14 +2162,14 @@ __device__ __forceinline__ void pass2_dispatch_r(const Tensor &T, const Hyper &h
                                                  const LUMA_GLOBAL Grid *old,
                                                  const LUMA_GLOBAL Grid *nw, float inv, int64_t ci,
                                                  int64_t beg, int64_t end, uint32_t k0,
-                                                 uint32_t k1, int reg, uint4 *q) {
+                                                 uint32_t k1, int reg, uint4 *q, Share sh) {
   if (reg == kRegSmall)
-    pass2_fast_body<GD, INJ, kRegSmall, SCALED, INJ_OK>(T, h, old, nw, inv, ci, beg, end, k0, k1, q);
+    pass2_fast_body<GD, INJ, kRegSmall, SCALED, INJ_OK>(T, h, old, nw, inv, ci, beg, end, k0, k1, q, sh);
   else if (reg == kRegMedium)
-    pass2_fast_body<GD, INJ, kRegMedium, SCALED, INJ_OK>(T, h, old, nw, inv, ci, beg, end, k0, k1, q);
+    pass2_fast_body<GD, INJ, kRegMedium, SCALED, INJ_OK>(T, h, old, nw, inv, ci, beg, end, k0, k1, q, sh);
   else
     pass2_fast_body<GD, INJ, kRegGeneral, SCALED, INJ_OK>(T, h, old, nw, inv, ci, beg, end, k0, k1,
-                                                          q);
+                                                          q, sh);
 }
 
 template <int GD, bool SCALED, bool INJ_OK>
@@ -2118,11 +2177,12 @@ __device__ __forceinline__ void pass2_dispatch_s(const Tensor &T, const Hyper &h
                                                  const LUMA_GLOBAL Grid *old,
                                                  const LUMA_GLOBAL Grid *nw, float inv, int64_t ci,
                                                  int64_t beg, int64_t end, uint32_t k0,
-                                                 uint32_t k1, bool inj, int reg, uint4 *q) {
+                                                 uint32_t k1, bool inj, int reg, uint4 *q,
+                                                 Share sh) {
   if (INJ_OK && inj)
-    pass2_dispatch_r<GD, SCALED, INJ_OK, true>(T, h, old, nw, inv, ci, beg, end, k0, k1, reg, q);
+    pass2_dispatch_r<GD, SCALED, INJ_OK, true>(T, h, old, nw, inv, ci, beg, end, k0, k1, reg, q, sh);
   else
-    pass2_dispatch_r<GD, SCALED, INJ_OK, false>(T, h, old, nw, inv, ci, beg, end, k0, k1, reg, q);
+    pass2_dispatch_r<GD, SCALED, INJ_OK, false>(T, h, old, nw, inv, ci, beg, end, k0, k1, reg, q, sh);
 }
 
 template <int GD, bool INJ_OK>
@@ -2130,11 +2190,11 @@ __device__ __forceinline__ void pass2_dispatch(const Tensor &T, const Hyper &h,
                                                const LUMA_GLOBAL Grid *old,
                                                const LUMA_GLOBAL Grid *nw, float inv, bool scaled,
                                                int64_t ci, int64_t beg, int64_t end, uint32_t k0,
-                                               uint32_t k1, bool inj, int reg, uint4 *q) {
+                                               uint32_t k1, bool inj, int reg, uint4 *q, Share sh) {
   if (scaled)
-    pass2_dispatch_s<GD, true, INJ_OK>(T, h, old, nw, inv, ci, beg, end, k0, k1, inj, reg, q);
+    pass2_dispatch_s<GD, true, INJ_OK>(T, h, old, nw, inv, ci, beg, end, k0, k1, inj, reg, q, sh);
   else
-    pass2_dispatch_s<GD, false, INJ_OK>(T, h, old, nw, inv, ci, beg, end, k0, k1, inj, reg, q);
+    pass2_dispatch_s<GD, false, INJ_OK>(T, h, old, nw, inv, ci, beg, end, k0, k1, inj, reg, q, sh);
 }
 
 // INJ_OK: a launch with injected uniforms.  Philox launches use the kernel
@@ -2148,8 +2208,9 @@ __global__ __launch_bounds__(kThreads) void pass2_fast_kernel(StepSrc src, uint6
   if (skip_step(src)) return;
   Tensor T;
   LumaGroup grp;
-  int64_t ci;
-  chunk_job(src, T, grp, ci);
+  int64_t ci, rec;
+  Share sh;
+  if (!chunk_job(src, T, grp, ci, rec, sh)) return;   // (no barriers below)
   const LUMA_GLOBAL Slot *S = T.slot;
   const int64_t t = S->step;   // advanced by finalize
   const Hyper h = S->hyp;
@@ -2165,19 +2226,18 @@ __global__ __launch_bounds__(kThreads) void pass2_fast_kernel(StepSrc src, uint6
   const int reg = momentum_regime(x_top, nw->sm);
   const bool scaled = src.scaling.grad_scale != nullptr;
   const float inv = inv_scale(src);
-  // each wavefront's queues and staging ring: launched with blockDim.x / 64
-  // blocks of kWaveLds entries of dynamic LDS
-  extern __shared__ uint4 p2_lds[];
-  uint4 *q = p2_lds + (threadIdx.x >> 6) * kWaveLds;
+  // each wavefront's queues and staging ring
+  __shared__ uint4 qbuf[kThreads / 64][kWaveLds];
+  uint4 *q = qbuf[threadIdx.x >> 6];
   if (T.grad_dtype == LUMA_GRAD_BF16)
     pass2_dispatch<LUMA_GRAD_BF16, INJ_OK>(T, h, old, nw, inv, scaled, ci, beg, end, k0, k1, inj,
-                                           reg, q);
+                                           reg, q, sh);
   else if (T.grad_dtype == LUMA_GRAD_F16)
     pass2_dispatch<LUMA_GRAD_F16, INJ_OK>(T, h, old, nw, inv, scaled, ci, beg, end, k0, k1, inj,
-                                          reg, q);
+                                          reg, q, sh);
   else
     pass2_dispatch<LUMA_GRAD_F32, INJ_OK>(T, h, old, nw, inv, scaled, ci, beg, end, k0, k1, inj,
-                                          reg, q);
+                                          reg, q, sh);
 }
 
 // ---------------------------------------------------------------------------
@@ -2398,30 +2458,18 @@ static int launch_step(StepSrc src, int32_t n_tensors, int32_t n_chunks, float *
   };
   if (int r = mark(0)) return r;
   const bool exact = (flags & LUMA_FLAG_EXACT_ONLY) != 0;
-  // chunks [0, medium_from): a workgroup of kThreads each; [medium_from,
-  // small_from): a workgroup of one wavefront each (same kernels);
+  // chunks [0, medium_from): a workgroup each; [medium_from, small_from): a
+  // wavefront each, four per workgroup, in the same launches;
   // [small_from, n_chunks): small tensors, a wavefront each
-  const int32_t n_big = src.medium_from;
-  const int32_t n_med = src.small_from - src.medium_from;
+  const int32_t blocks = pass_blocks(src.medium_from, src.small_from);
   const int32_t small_blocks = (n_chunks - src.small_from + kThreads / 64 - 1) / (kThreads / 64);
-  StepSrc med = src;
-  med.chunk_base = src.medium_from;
-  // the runs of pass 1 or pass 2: kernel k over [0, n_big) and [medium_from, small_from)
-  auto runs = [&](auto kernel, size_t lds_per_wave, auto... args) -> int {
-    if (n_big > 0) {
-      hipLaunchKernelGGL(kernel, dim3(n_big), dim3(kThreads), lds_per_wave * (kThreads / 64), s,
-                         src, args...);
-      if (int r = check_launch("luma_step: launch")) return r;
-    }
-    if (n_med > 0) {
-      hipLaunchKernelGGL(kernel, dim3(n_med), dim3(64), lds_per_wave, s, med, args...);
-      if (int r = check_launch("luma_step: launch (medium tensors)")) return r;
-    }
-    return 0;
-  };
-  constexpr size_t kP2Lds = sizeof(uint4) * kWaveLds;
-  if (int r = exact ? runs(pass1_exact_kernel, 0, partials) : runs(pass1_fast_kernel, 0, partials))
-    return r;
+  if (blocks > 0) {
+    if (exact)
+      hipLaunchKernelGGL(pass1_exact_kernel, dim3(blocks), dim3(kThreads), 0, s, src, partials);
+    else
+      hipLaunchKernelGGL(pass1_fast_kernel, dim3(blocks), dim3(kThreads), 0, s, src, partials);
+    if (int r = check_launch("luma_step: pass 1 launch")) return r;
+  }
   if (small_blocks > 0) {
     hipLaunchKernelGGL(pass1_small_kernel, dim3(small_blocks), dim3(kThreads), 0, s, src, partials);
     if (int r = check_launch("luma_step: pass 1 (small tensors) launch")) return r;
@@ -2431,14 +2479,18 @@ static int launch_step(StepSrc src, int32_t n_tensors, int32_t n_chunks, float *
                      dim3(kThreads), 0, s, src, (const float *)partials, n_tensors);
   if (int r = check_launch("luma_step: finalize launch")) return r;
   if (int r = mark(2)) return r;
-  int r2;
-  if (exact)
-    r2 = runs(pass2_exact_kernel, 0, base_seed, (int)noise_mode);
-  else if (noise_mode == LUMA_NOISE_INJECTED)
-    r2 = runs(pass2_fast_kernel<true>, kP2Lds, base_seed, (int)noise_mode);
-  else
-    r2 = runs(pass2_fast_kernel<false>, kP2Lds, base_seed, (int)noise_mode);
-  if (r2) return r2;
+  if (blocks > 0) {
+    if (exact)
+      hipLaunchKernelGGL(pass2_exact_kernel, dim3(blocks), dim3(kThreads), 0, s, src, base_seed,
+                         (int)noise_mode);
+    else if (noise_mode == LUMA_NOISE_INJECTED)
+      hipLaunchKernelGGL(pass2_fast_kernel<true>, dim3(blocks), dim3(kThreads), 0, s, src,
+                         base_seed, (int)noise_mode);
+    else
+      hipLaunchKernelGGL(pass2_fast_kernel<false>, dim3(blocks), dim3(kThreads), 0, s, src,
+                         base_seed, (int)noise_mode);
+    if (int r = check_launch("luma_step: pass 2 launch")) return r;
+  }
   if (small_blocks > 0) {
     hipLaunchKernelGGL(pass2_small_kernel, dim3(small_blocks), dim3(kThreads), 0, s, src,
                        base_seed, (int)noise_mode);
@@ -2468,7 +2520,6 @@ static int step_impl(const LumaStepArgs *a, void *stream, void *const *events) {
     return fail("luma_step: medium_chunks must be in [0, n_chunks - small_chunks]");
   src.small_from = a->n_chunks - a->small_chunks;
   src.medium_from = src.small_from - a->medium_chunks;
-  src.chunk_base = 0;
   src.n_chunks = a->n_chunks;
   return launch_step(src, a->n_tensors, a->n_chunks, a->partials, a->base_seed, a->noise_mode,
                      a->flags, static_cast<hipStream_t>(stream), events);
@@ -2543,7 +2594,6 @@ int luma_step_tensor(const LumaTensor *tensor, const LumaGroup *group, float *pa
   src.chunk_shift = shift;
   src.small_from = (int32_t)nch;   // one tensor: every chunk takes a workgroup
   src.medium_from = (int32_t)nch;
-  src.chunk_base = 0;
   src.n_chunks = (int32_t)nch;
   if (scaling) src.scaling = *scaling;
   return launch_step(src, 1, (int32_t)nch, partials, base_seed, noise_mode, flags,
