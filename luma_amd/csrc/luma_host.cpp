@@ -10,17 +10,23 @@
 // in host memory, so the walk is bound by memory latency: it runs in stages
 // over arrays (parameter object -> TensorImpl -> autograd meta -> gradient
 // TensorImpl -> data pointers) with software prefetch a few tensors ahead,
-// and large sets are split over a few threads.  The worker threads only read
-// C++ objects while the calling thread holds the GIL, so nothing they read
-// can change under them.  The module computes nothing of the step itself:
-// the step runs in libluma_hip.so.
+// and large sets are split over a few threads of a pool that lives as long as
+// the process (made on first use, made again in a forked child).  The worker
+// threads only read C++ objects while the calling thread holds the GIL, so
+// nothing they read can change under them.  The module computes nothing of
+// the step itself: the step runs in libluma_hip.so.
 #include <ATen/core/Tensor.h>
 #include <pybind11/numpy.h>
 #include <pybind11/pybind11.h>
 #include <torch/csrc/autograd/python_variable.h>
 
+#include <unistd.h>
+
 #include <algorithm>
+#include <condition_variable>
 #include <cstdint>
+#include <functional>
+#include <mutex>
 #include <thread>
 #include <vector>
 
@@ -39,8 +45,80 @@ int grad_code(at::ScalarType t) {
 }
 
 constexpr int64_t kAhead = 8;             // prefetch distance, in tensors
-constexpr int64_t kPerThread = 4096;      // parameters per worker thread
-constexpr int kMaxThreads = 8;
+constexpr int64_t kPerThread = 2048;      // parameters per thread, at least
+constexpr int kMaxThreads = 8;            // the calling thread and up to 7 workers
+
+// Workers that run part t of a job for t = 1 .. parts-1 while the calling
+// thread runs part 0.  One job at a time (the callers hold the GIL).
+class Pool {
+ public:
+  // The pool of this process; empty (run() then does every part on the
+  // calling thread) when no thread could be started.
+  static Pool &get() {
+    static Pool *pool = nullptr;
+    static pid_t owner = 0;
+    if (!pool || owner != getpid()) {
+      // a forked child inherits the memory but not the threads: it makes
+      // its own pool (the parent's stays unused in the child)
+      pool = new Pool(kMaxThreads - 1);
+      owner = getpid();
+    }
+    return *pool;
+  }
+
+  void run(int parts, const std::function<void(int)> &fn) {
+    const int use = std::min<int>(parts - 1, (int)threads_.size());
+    {
+      std::lock_guard<std::mutex> lock(mu_);
+      fn_ = &fn;
+      use_ = use;
+      pending_ = use;
+      ++gen_;
+    }
+    if (use > 0) wake_.notify_all();
+    for (int t = use + 1; t < parts; ++t) fn(t);   // parts no worker took
+    fn(0);
+    std::unique_lock<std::mutex> lock(mu_);
+    done_.wait(lock, [&] { return pending_ == 0; });
+    fn_ = nullptr;
+  }
+
+ private:
+  explicit Pool(int n) {
+    for (int i = 0; i < n; ++i) {
+      try {
+        threads_.emplace_back([this, i] { loop(i + 1); });
+      } catch (...) {
+        break;
+      }
+    }
+    for (std::thread &t : threads_) t.detach();
+  }
+
+  void loop(int part) {
+    uint64_t seen = 0;
+    for (;;) {
+      const std::function<void(int)> *fn;
+      {
+        std::unique_lock<std::mutex> lock(mu_);
+        wake_.wait(lock, [&] { return gen_ != seen; });
+        seen = gen_;
+        if (part > use_) continue;
+        fn = fn_;
+      }
+      (*fn)(part);
+      std::lock_guard<std::mutex> lock(mu_);
+      if (--pending_ == 0) done_.notify_one();
+    }
+  }
+
+  std::vector<std::thread> threads_;
+  std::mutex mu_;
+  std::condition_variable wake_, done_;
+  const std::function<void(int)> *fn_ = nullptr;
+  int use_ = 0, pending_ = 0;
+  uint64_t gen_ = 0;
+};
 
 inline void prefetch(const void *p) { __builtin_prefetch(p, 0, 3); }
 
@@ -205,22 +283,16 @@ int refresh(py::list groups, py::list planned, carray<uint8_t> has_grad,
                reinterpret_cast<char *>(table), row_bytes, grad_off, param_off, device};
   const int T = (int)std::min<int64_t>(kMaxThreads, std::max<int64_t>(1, n_params / kPerThread));
   std::vector<int> res(T, 1);
-  std::vector<std::thread> workers;
-  for (int t = 0; t < T; ++t) {
+  const std::function<void(int)> part = [&](int t) {
     const int64_t a = n_params * t / T, b = n_params * (t + 1) / T;
     const int64_t ra = std::lower_bound(rp, rp + n_rows, a) - rp;
     const int64_t rb = std::lower_bound(rp, rp + n_rows, b) - rp;
-    bool spawned = false;
-    if (t + 1 < T) {
-      try {
-        workers.emplace_back([&P, &res, t, a, b, ra, rb] { res[t] = check_range(P, a, b, ra, rb); });
-        spawned = true;
-      } catch (...) {
-      }
-    }
-    if (!spawned) res[t] = check_range(P, a, b, ra, rb);
-  }
-  for (std::thread &w : workers) w.join();
+    res[t] = check_range(P, a, b, ra, rb);
+  };
+  if (T == 1)
+    part(0);
+  else
+    Pool::get().run(T, part);
   int out = 1;
   for (int r : res) {
     if (r == 0) return 0;
@@ -231,13 +303,26 @@ int refresh(py::list groups, py::list planned, carray<uint8_t> has_grad,
 
 // state["step"] += 1 for every state dict of the list.  The dicts of one
 // plan usually hold the same count object, so the sum is formed once per
-// distinct object.
+// distinct object.  The dicts lie scattered in memory: each one, and then its
+// key table, is prefetched a few dicts ahead.
 void bump_steps(py::list states) {
   static PyObject *key = PyUnicode_InternFromString("step");
   py::object last_v, last_nv;
   py::object one = py::int_(1);
-  for (py::handle h : states) {
-    PyObject *d = h.ptr();
+  for (Py_ssize_t i = 0; i < PyList_GET_SIZE(states.ptr()); ++i) {
+    // (the size is read again each time: a count object's __add__ could
+    // change the list)
+    const Py_ssize_t n = PyList_GET_SIZE(states.ptr());
+    if (i + 2 * kAhead < n) prefetch(PyList_GET_ITEM(states.ptr(), i + 2 * kAhead));
+    if (i + kAhead < n) {
+      PyObject *a = PyList_GET_ITEM(states.ptr(), i + kAhead);
+      if (PyDict_CheckExact(a)) {
+        const char *keys = reinterpret_cast<const char *>(((PyDictObject *)a)->ma_keys);
+        prefetch(keys);
+        prefetch(keys + 64);
+      }
+    }
+    PyObject *d = PyList_GET_ITEM(states.ptr(), i);
     if (!PyDict_Check(d)) throw py::type_error("bump_steps: a state is not a dict");
     PyObject *v = PyDict_GetItemWithError(d, key);
     if (!v) {

@@ -323,91 +323,137 @@ __device__ __forceinline__ void block_argmax2(float &a, uint32_t &ia, float &b, 
 // S' = max(max, floor) with Python's max() semantics (a NaN maximum stays NaN).
 __device__ __forceinline__ double py_max(double a, double floor_) { return floor_ > a ? floor_ : a; }
 
-// The per-tensor stage of a step, one wavefront per tensor after pass 1:
-// reduce the tensor's chunk records to S_m', S_v' (functional.py:282-284;
-// init 217-219), derive the new grid in float64 (functional.py:74-92),
-// advance the step count, derive the step's scalars (functional.py:209-213,
-// 262-264), and keep the maxima's elements as the next step's seeds.
-__device__ __forceinline__ void finalize_tensor(const StepSrc &src, const Tensor &T,
-                                                const LumaGroup &grp, const float *partials) {
+// The per-tensor stage of a step, after pass 1: reduce the tensor's chunk
+// records to S_m', S_v' (functional.py:282-284; init 217-219), derive the
+// new grid in float64 (functional.py:74-92), advance the step count, derive
+// the step's scalars (functional.py:209-213, 262-264), and keep the maxima's
+// elements as the next step's seeds.
+//
+// The tail, by one lane: from the tensor's maxima and the elements holding
+// them (-1: none), everything after the reduction.
+__device__ __forceinline__ void finalize_tail(const StepSrc &src, const Tensor &T,
+                                              const LumaGroup &grp, int64_t prev, float am,
+                                              float av, int64_t seed_m, int64_t seed_v) {
+  const double s_m = py_max((double)am, 1e-9);  // SCALE_FLOOR_M (config.py:25)
+  const double s_v = py_max((double)av, 0.0);
+  LUMA_GLOBAL Slot &s = *T.slot;
+  const int64_t t = prev + 1;
+  const int par = (int)(t & 1);
+  const Hyper h = step_hyper(grp, t);
+  s.s_m[par] = s_m;
+  s.s_v[par] = s_v;
+  Grid g;
+  make_grid(s_m, s_v, grp.eps, g);
+  make_fast(g, h.eps);
+  s.grid[par] = g;
+  s.hyp = h;
+  s.step = t;
+  // (only the kThreads-workgroup route writes summaries)
+  s.summ_step = (src.summaries && T.summary && T.first_chunk < src.medium_from) ? t : 0;
+  s.summ_shift = src.chunk_shift;
+  s.seed_m = seed_m;
+  s.seed_v = seed_v;
+}
+
+// The element a chunk record's offset word names (-1: none).
+__device__ __forceinline__ int64_t seed_at(uint32_t chunk, uint32_t off, int32_t shift) {
+  return (chunk == kNoArg || off == kNoArg) ? -1 : ((int64_t)chunk << shift) + off;
+}
+
+// One wavefront for tensor T (wave-uniform): each lane folds every 64th of
+// the tensor's records, 16 loads in flight (a tensor of a few thousand
+// chunks reads them in a few round trips), keeping the offset word of its
+// best record, which the winning lane then hands out.
+__device__ __forceinline__ void finalize_wave(const StepSrc &src, const Tensor &T,
+                                              const LumaGroup &grp, const float *partials) {
+  const int64_t prev = T.slot->step;   // (loaded while the records stream in)
   const uint32_t lane = lane_id();
   const int nch = (int)(((T.numel - 1) >> src.chunk_shift) + 1);
   float am = 0.0f, av = 0.0f;
   uint32_t cm = kNoArg, cv = kNoArg;   // chunk (within the tensor) of each maximum
-  // each lane reads its records 16 bytes at a time, four loads in flight
-  // (the loop is latency-bound: a tensor of a few thousand chunks reads
-  // them in a few round trips instead of one per 64 records)
+  uint32_t om = kNoArg, ov = kNoArg;   // its offset word
   const vf4 *rec = (const vf4 *)(partials + kPartialWords * (int64_t)T.first_chunk);
   auto fold = [&](const vf4 &r, int i) {
     if (beats(r.x, am)) {
       am = r.x;
       cm = (uint32_t)i;
+      om = __float_as_uint(r.z);
     }
     if (beats(r.y, av)) {
       av = r.y;
       cv = (uint32_t)i;
+      ov = __float_as_uint(r.w);
     }
   };
+  constexpr int kInFlight = 16;
   int i = (int)lane;
-  for (; i + 3 * 64 < nch; i += 4 * 64) {
-    const vf4 r0 = rec[i], r1 = rec[i + 64], r2 = rec[i + 128], r3 = rec[i + 192];
-    fold(r0, i);
-    fold(r1, i + 64);
-    fold(r2, i + 128);
-    fold(r3, i + 192);
+  for (; i + (kInFlight - 1) * 64 < nch; i += kInFlight * 64) {
+    vf4 r[kInFlight];
+#pragma unroll
+    for (int k = 0; k < kInFlight; ++k) r[k] = rec[i + 64 * k];
+#pragma unroll
+    for (int k = 0; k < kInFlight; ++k) fold(r[k], i + 64 * k);
   }
   for (; i < nch; i += 64) fold(rec[i], i);
+  // the lane that read chunk c is c % 64; wave_argmax keeps the smallest
+  // chunk among equal maxima, which is that lane's own first best
   wave_argmax(am, cm);
   wave_argmax(av, cv);
-  if (lane == 0) {
-    // the seeds: chunk * C + the offset pass 1 recorded in that chunk
-    auto seed = [&](uint32_t c, int word) -> int64_t {
-      if (c == kNoArg) return -1;
-      const uint32_t off =
-          __float_as_uint(partials[kPartialWords * ((int64_t)T.first_chunk + c) + word]);
-      return off == kNoArg ? -1 : ((int64_t)c << src.chunk_shift) + off;
-    };
-    const int64_t seed_m = seed(cm, 2), seed_v = seed(cv, 3);
-    const double s_m = py_max((double)am, 1e-9);  // SCALE_FLOOR_M (config.py:25)
-    const double s_v = py_max((double)av, 0.0);
-    LUMA_GLOBAL Slot &s = *T.slot;
-    const int64_t t = s.step + 1;
-    const int par = (int)(t & 1);
-    const Hyper h = step_hyper(grp, t);
-    s.s_m[par] = s_m;
-    s.s_v[par] = s_v;
-    Grid g;
-    make_grid(s_m, s_v, grp.eps, g);
-    make_fast(g, h.eps);
-    s.grid[par] = g;
-    s.hyp = h;
-    s.step = t;
-    // (only the kThreads-workgroup route writes summaries)
-    s.summ_step = (src.summaries && T.summary && T.first_chunk < src.medium_from) ? t : 0;
-    s.summ_shift = src.chunk_shift;
-    s.seed_m = seed_m;
-    s.seed_v = seed_v;
-  }
+  om = (uint32_t)__shfl((int)om, (int)(cm & 63u), 64);
+  ov = (uint32_t)__shfl((int)ov, (int)(cv & 63u), 64);
+  if (lane == 0)
+    finalize_tail(src, T, grp, prev, am, av, seed_at(cm, om, src.chunk_shift),
+                  seed_at(cv, ov, src.chunk_shift));
 }
 
-// One wavefront per tensor, four per workgroup (fewer workgroups to
-// dispatch when there are thousands of small tensors).
+// Waves [0, n_tensors): one tensor each, except the tensors whose records
+// start in the medium and small runs; those (one record each, as a rule)
+// take a lane each in the waves after, 64 records per wave, so that the
+// float64 tail of 64 small tensors runs side by side.
+__device__ __host__ inline int32_t finalize_waves(const StepSrc &src, int32_t n_tensors) {
+  return n_tensors + (src.tensors ? (src.n_chunks - src.medium_from + 63) / 64 : 0);
+}
+
 __global__ __launch_bounds__(kThreads) void finalize_kernel(StepSrc src,
                                                             const float *__restrict__ partials,
                                                             int32_t n_tensors) {
   if (skip_step(src)) return;
-  const int64_t ti = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
-  if (ti >= n_tensors) return;   // no barriers below
-  Tensor T;
-  LumaGroup grp;
-  if (src.tensors) {
-    T = src.tensors[ti];
-    grp = src.groups[T.group];
-  } else {
-    T = src.one;
-    grp = src.group;
+  const int32_t w = __builtin_amdgcn_readfirstlane((int32_t)blockIdx.x * (kThreads / 64) +
+                                                   (int32_t)(threadIdx.x >> 6));
+  if (w < n_tensors) {
+    if (!src.tensors) {
+      finalize_wave(src, src.one, src.group, partials);
+      return;
+    }
+    const Tensor T = src.tensors[w];
+    if (T.first_chunk >= src.medium_from) return;   // a lane's (below)
+    finalize_wave(src, T, src.groups[T.group], partials);
+    return;
   }
-  finalize_tensor(src, T, grp, partials);
+  if (!src.tensors) return;
+  const int64_t r = (int64_t)src.medium_from + (int64_t)(w - n_tensors) * 64 + lane_id();
+  if (r >= src.n_chunks) return;   // (no wave operations below)
+  const Tensor T = src.tensors[src.chunks[r].tensor];
+  if (T.first_chunk != r) return;   // not the tensor's first record
+  const int64_t prev = T.slot->step;
+  const int nch = (int)(((T.numel - 1) >> src.chunk_shift) + 1);
+  float am = 0.0f, av = 0.0f;
+  uint32_t cm = kNoArg, cv = kNoArg, om = kNoArg, ov = kNoArg;
+  for (int c = 0; c < nch; ++c) {
+    const vf4 x = ((const vf4 *)partials)[r + c];
+    if (beats(x.x, am)) {
+      am = x.x;
+      cm = (uint32_t)c;
+      om = __float_as_uint(x.z);
+    }
+    if (beats(x.y, av)) {
+      av = x.y;
+      cv = (uint32_t)c;
+      ov = __float_as_uint(x.w);
+    }
+  }
+  finalize_tail(src, T, src.groups[T.group], prev, am, av, seed_at(cm, om, src.chunk_shift),
+                seed_at(cv, ov, src.chunk_shift));
 }
 
 // The record of a chunk whose threads hold (am, im), (av, iv): the share's
@@ -2475,7 +2521,8 @@ static int launch_step(StepSrc src, int32_t n_tensors, int32_t n_chunks, float *
     if (int r = check_launch("luma_step: pass 1 (small tensors) launch")) return r;
   }
   if (int r = mark(1)) return r;
-  hipLaunchKernelGGL(finalize_kernel, dim3((n_tensors + kThreads / 64 - 1) / (kThreads / 64)),
+  const int32_t fin_waves = finalize_waves(src, n_tensors);
+  hipLaunchKernelGGL(finalize_kernel, dim3((fin_waves + kThreads / 64 - 1) / (kThreads / 64)),
                      dim3(kThreads), 0, s, src, (const float *)partials, n_tensors);
   if (int r = check_launch("luma_step: finalize launch")) return r;
   if (int r = mark(2)) return r;

@@ -119,7 +119,7 @@ class _Recording(torch.Tensor):
 
 
 def test_refresh_rejects_a_subclass_gradient_without_python():
-    """With 8192 or more parameters the check runs on worker threads while the
+    """With 4096 or more parameters the check runs on worker threads while the
     caller holds the GIL; a gradient subclass with a custom device policy
     must be rejected from its dispatch keys, before anything that would call
     into Python."""
@@ -133,3 +133,29 @@ def test_refresh_rejects_a_subclass_gradient_without_python():
     _Recording.calls = 0
     assert _refresh(groups, ps, [1] * n, list(range(n)), [L.GRAD_F32] * n, tt) == 0
     assert _Recording.calls == 0
+
+
+def test_refresh_pool_after_fork():
+    """The check's worker threads belong to the process that made them: a
+    forked child (a DataLoader worker, say) that steps makes its own."""
+    import multiprocessing as mp
+    n = 4 * 2048
+    ps = [torch.zeros(2, requires_grad=True) for _ in range(n)]
+    for p in ps:
+        p.grad = torch.zeros(2)
+    tt = np.zeros(n, dtype=L.TENSOR_DTYPE)
+    groups = [{"params": ps}]
+    args = (groups, ps, [1] * n, list(range(n)), [L.GRAD_F32] * n, tt)
+    for _ in range(3):   # the parent's pool, used more than once
+        assert _refresh(*args) == 0
+    ctx = mp.get_context("fork")
+    q = ctx.Queue()
+    child = ctx.Process(target=lambda: q.put([_refresh(*args) for _ in range(3)]))
+    child.start()
+    child.join(60)
+    alive = child.is_alive()
+    if alive:
+        child.kill()
+    assert not alive and child.exitcode == 0
+    assert q.get(timeout=5) == [0, 0, 0]
+    assert _refresh(*args) == 0
