@@ -8,7 +8,7 @@ SCALE_FLOOR_M: float = 1e-9       # minimum momentum scale S_m
 # Triton launch parameters; these are the gfx950 equivalents).
 CHUNK_ELEMS: int = 131072         # elements per chunk-table entry (one workgroup), at most
 STEP_CHUNK_MIN: int = 16384       # shortest chunk the optimizer picks for a small tensor set
-STEP_TARGET_CHUNKS: int = 4096    # workgroups a step aims for (16 per CU) before shortening chunks
+STEP_TARGET_CHUNKS: int = 2048    # workgroups a step aims for (8 per CU) before shortening chunks
 THREADS_PER_BLOCK: int = 256      # four wave64 per workgroup
 ELEMS_PER_THREAD: int = 8         # consecutive elements per thread per iteration
 

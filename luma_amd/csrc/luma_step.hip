@@ -1191,6 +1191,35 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
                                 float inv, int64_t ci, int64_t beg, int64_t end, float &exm,
                                 float &exv, uint32_t &exi_m, uint32_t &exi_v, uint32_t *queue,
                                 Share sh) {
+  // Threads per chunk: kThreads, or one wavefront for a medium tensor; an
+  // iteration covers nt * kVec consecutive elements.
+  constexpr int nt = NT;
+  constexpr int it_shift = NT == kThreads ? kItShift : kItShift - 2;  // 64 = kThreads / 4
+  static_assert(NT == kThreads || NT == 64, "a workgroup or one wavefront per chunk");
+  const int64_t kStride = (int64_t)1 << it_shift;
+  const int n_it = (int)((end - beg + kStride - 1) >> it_shift);
+  const bool vec_ok = tensor_vec_ok(T);
+  // Iterations in which every lane's group is whole run in a loop of their
+  // own that loads each group one iteration ahead (below).
+  // (uniform: readfirstlane keeps the loop's group offsets in SGPRs)
+  const int n_whole = __builtin_amdgcn_readfirstlane(vec_ok ? (int)((end - beg) >> it_shift) : 0);
+  auto group_at = [&](int j) {
+    return beg + ((int64_t)(j < n_whole ? j : n_whole - 1) * nt + sh.tid()) * kVec;
+  };
+  // The first group's loads (and with SUMM the thread's summary word) go
+  // out before the per-tensor constants are derived, so that their latency
+  // covers that arithmetic.
+  static_assert(LUMA_SUMMARY_WORDS == kThreads, "one summary word per thread of a chunk");
+  Raw8 ra, rb;
+  uint32_t sw = 0;
+  if (n_whole > 0) {
+    if (SUMM) {
+      sw = T.summary[ci * LUMA_SUMMARY_WORDS + sh.tid()];
+      load_grads<GD>(T, group_at(0), ra);
+    } else {
+      load_raw<GD>(T, beg + (int64_t)sh.tid() * kVec, ra);
+    }
+  }
   const Bounds B = make_bounds((const Grid *)old, nullptr, h.beta1, h.beta2);
   const DecodeK D = decode_consts(old, h.eps);
   P1Const K;
@@ -1212,7 +1241,6 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   K.up_m = in_vgpr(1.0f + 8.0f * kU);
   K.up_v = in_vgpr(1.0f + 16.0f * kU);
   K.abs_v = in_vgpr(D.eps * D.eps * 1e-10f);
-  const bool vec_ok = tensor_vec_ok(T);
   const float lo_m = 1.0f - B.dlt_m, hi_m = 1.0f / (1.0f + B.dlt_m);
   const float lo_v = 1.0f - B.dlt_v, hi_v = 1.0f / (1.0f + B.dlt_v);
   const float sub_m = 2.0f * B.abs_m, sub_v = 2.0f * B.abs_v;
@@ -1295,26 +1323,11 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   // Every lane of a wave runs the same iterations (lanes past the end carry
   // n = 0), so the ballots and the queue length stay uniform across the wave;
   // a wave stops once all its groups lie past the end.
-  // Threads per chunk: kThreads, or one wavefront for a medium tensor; an
-  // iteration covers nt * kVec consecutive elements.
-  constexpr int nt = NT;
-  constexpr int it_shift = NT == kThreads ? kItShift : kItShift - 2;  // 64 = kThreads / 4
-  static_assert(NT == kThreads || NT == 64, "a workgroup or one wavefront per chunk");
-  const int64_t kStride = (int64_t)1 << it_shift;
-  const int n_it = (int)((end - beg + kStride - 1) >> it_shift);
-  // Iterations in which every lane's group is whole run in a loop of their
-  // own that loads each group one iteration ahead: raw holds the codes and
-  // gradients of the lane's next group (the current one again after the last
-  // whole group, so that every iteration issues the same loads).
-  // (uniform: readfirstlane keeps the loop's group offsets in SGPRs)
-  const int n_whole = __builtin_amdgcn_readfirstlane(vec_ok ? (int)((end - beg) >> it_shift) : 0);
   int it = 0;
   if (SUMM && n_whole > 0) {
-    // This thread's summary word (written by the previous pass 2 for the
+    // This thread's summary word sw (written by the previous pass 2 for the
     // same thread of the same chunk) and, once, the decode of its code
     // bound; each iteration then bounds with the lane's largest |g| alone.
-    static_assert(LUMA_SUMMARY_WORDS == kThreads, "one summary word per thread of a chunk");
-    const uint32_t sw = T.summary[ci * LUMA_SUMMARY_WORDS + sh.tid()];
     const FastEma d = fast_ema<SMALL ? kRegSmall : kRegGeneral, false>((int)(sw & 0xFFFFu), (int)(kCodeFloat | (sw >> 16)),
                                              0.0f, K.dm, K.ndw, K.nbias, K.iwmin, K.eps, K.b1,
                                              K.omb1, K.b2, K.omb2, K.sign);
@@ -1352,12 +1365,7 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     // Two gradient buffers, each loaded one iteration before its use, in a
     // loop unrolled by two: copying a buffer whose load is in flight (a
     // single buffer carried across iterations) would make every iteration
-    // wait for the load just issued.
-    auto group_at = [&](int j) {
-      return beg + ((int64_t)(j < n_whole ? j : n_whole - 1) * nt + sh.tid()) * kVec;
-    };
-    Raw8 ra, rb;
-    load_grads<GD>(T, group_at(0), ra);
+    // wait for the load just issued.  (ra: group 0, loaded above.)
     seed_thresholds();
     for (; it < n_whole; it += 2) {
       load_grads<GD>(T, group_at(it + 1), rb);
@@ -1368,8 +1376,10 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     }
     it = n_whole;
   } else if (n_whole > 0) {
-    Raw8 raw;
-    load_raw<GD>(T, beg + (int64_t)sh.tid() * kVec, raw);
+    // raw holds the codes and gradients of the lane's next group (the
+    // current one again after the last whole group, so that every iteration
+    // issues the same loads); group 0 was loaded above
+    Raw8 &raw = ra;
     seed_thresholds();
     for (; it < n_whole; ++it) {
       const int64_t e0 = beg + ((int64_t)it * nt + sh.tid()) * kVec;
@@ -1890,6 +1900,26 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
                                 const LUMA_GLOBAL Grid *nw, float inv, int64_t ci, int64_t beg,
                                 int64_t end, uint32_t k0, uint32_t k1, uint4 *queue,
                                 Share sh) {
+  // Threads per chunk: kThreads, or one wavefront for a medium tensor; an
+  // iteration covers nt * kVec = 1 << it_shift consecutive elements.
+  const int nt = sh.nt;
+  const int it_shift = __builtin_ctz((unsigned)nt) + 3;
+  const bool vec_ok = tensor_vec_ok(T);
+  // Iterations in which every lane's group is whole stage their
+  // preconditioner codes; before a slot is reused, the iteration it holds has
+  // its queued entries run and is written back.
+  const int n_whole = vec_ok ? (int)((end - beg) >> it_shift) : 0;
+  // Each iteration's vectors are loaded one iteration ahead, into two
+  // buffers in a loop unrolled by two (copying a buffer whose loads are in
+  // flight would make the copy wait for them); past the last whole group the
+  // loads repeat the last group, and are not used.
+  auto group_at = [&](int j) {
+    return beg + ((int64_t)(j < n_whole ? j : n_whole - 1) * nt + sh.tid()) * kVec;
+  };
+  // The first group's loads go out before the per-tensor constants below
+  // are derived, so that their latency covers that arithmetic.
+  P2Raw ra, rb;
+  if (n_whole > 0) load_p2raw<GD>(T, group_at(0), ra);
   const Bounds B = make_bounds((const Grid *)old, (const Grid *)nw, h.beta1, h.beta2);
   P2Const C;
   C.D = decode_consts(old, h.eps);
@@ -1948,7 +1978,6 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   const uint32_t marg_m = em < 32767.0f ? (uint32_t)fmaxf(1.0f, ceilf(em)) : 32767u;
   const uint32_t marg_w = ew < 65535.0f ? (uint32_t)fmaxf(1.0f, ceilf(ew)) : 65535u;
   launder(C);
-  const bool vec_ok = tensor_vec_ok(T);
   const uint32_t lane = lane_id();
   // the wave's LDS block: momentum ring, preconditioner ring, staging slots
   uint4 *queue_m = queue, *queue_w = queue + kQueueCapM;
@@ -1982,10 +2011,6 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   auto u_hi = [&](uint32_t top, const LUMA_GLOBAL float *u, int64_t i) -> float {
     return INJ ? u[i] : (float)((top << 8) | 0xFFu) * 0x1p-24f;
   };
-  // Threads per chunk: kThreads, or one wavefront for a medium tensor; an
-  // iteration covers nt * kVec = 1 << it_shift consecutive elements.
-  const int nt = sh.nt;
-  const int it_shift = __builtin_ctz((unsigned)nt) + 3;
   // Staging: whole-group iterations [staged_lo, staged_hi) keep their
   // preconditioner codes in stage[(it % kStage) * 64 + lane] until written
   // back.  Chunk offset o belongs to iteration o >> it_shift and to lane
@@ -2125,17 +2150,6 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   const int64_t kStride = (int64_t)1 << it_shift;
   const int n_it = (int)((end - beg + kStride - 1) >> it_shift);
   CodeAcc acc{0u, 0u, 0xFFFFFFFFu};
-  // Iterations in which every lane's group is whole stage their
-  // preconditioner codes; before a slot is reused, the iteration it holds has
-  // its queued entries run and is written back.
-  const int n_whole = vec_ok ? (int)((end - beg) >> it_shift) : 0;
-  // Each iteration's vectors are loaded one iteration ahead, into two
-  // buffers in a loop unrolled by two (copying a buffer whose loads are in
-  // flight would make the copy wait for them); past the last whole group the
-  // loads repeat the last group, and are not used.
-  auto group_at = [&](int j) {
-    return beg + ((int64_t)(j < n_whole ? j : n_whole - 1) * nt + sh.tid()) * kVec;
-  };
   auto whole_iter = [&](const P2Raw &R, int j) {
     const int64_t e0 = group_at(j);
     Group8 Q;
@@ -2154,8 +2168,6 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   };
   int it = 0;
   if (n_whole > 0) {
-    P2Raw ra, rb;
-    load_p2raw<GD>(T, group_at(0), ra);
     for (; it < n_whole; it += 2) {
       load_p2raw<GD>(T, group_at(it + 1), rb);
       whole_iter(ra, it);

@@ -142,8 +142,8 @@ class _Engine:
         self.chunk_elems = 0         # fixed chunk length (a power of two), 0: chunk_for's choice
         self.small_tensors = True    # step tensors of <= SMALL_TENSOR elements a wavefront each
         self._small_chunks = 0       # trailing chunk records of such tensors (uploaded table)
-        self.medium_tensors = True   # step tensors of <= MEDIUM_TENSOR elements a one-wavefront
-                                     # workgroup each (the fast kernels)
+        self.medium_tensors = True   # step tensors of <= MEDIUM_TENSOR elements one wavefront
+                                     # each (inside the fast kernels' launches)
         self._medium_chunks = 0      # the records of such tensors, before the small ones
         self._d_tensors = None
         self._table_cache = {}       # tensor-table bytes -> device copy (most recent last)
@@ -289,7 +289,7 @@ class _Engine:
         return int(L.SMALL_TENSOR) if self.small_tensors else 0
 
     def _medium_limit(self) -> int:
-        """Largest tensor stepped by a one-wavefront workgroup (0: none)."""
+        """Largest tensor stepped one wavefront each by the fast kernels (0: none)."""
         return int(L.MEDIUM_TENSOR) if self.medium_tensors else 0
 
     def _wave_limit(self) -> int:
@@ -303,8 +303,8 @@ class _Engine:
         in that order (luma.h, LumaStepArgs.medium_chunks / small_chunks).
         Tensors of at most SMALL_TENSOR elements are stepped a wavefront per
         chunk by the exact kernels, and those above it and of at most
-        MEDIUM_TENSOR elements (and one chunk) by a one-wavefront workgroup
-        of the fast kernels; each run is ordered largest first, so the four
+        MEDIUM_TENSOR elements (and one chunk) one wavefront each by the fast
+        kernels, four to a workgroup; each run is ordered largest first, so the four
         wavefronts of a small-tensor workgroup step tensors of about one size
         and every launch ends on its shortest work.  The others keep their
         order, unless there are STEP_TARGET_CHUNKS of them or more (chunk_for

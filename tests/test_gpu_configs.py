@@ -99,10 +99,10 @@ def test_cfg3_many_small():
         gen = _gen(3000 + t)
         gd = [normal_grad(p.shape, 1e-4, gen, DEV, torch.float32, zeros=0.01) for p in params]
         pair.step(gd, {i: g.cpu() for i, g in enumerate(gd)})
-        # more than 4096 tensors above the single-wavefront routes: one
+        # more than 2048 tensors above the single-wavefront routes: one
         # chunk per tensor (the largest has 32769 to 65536 elements),
-        # largest first; tensors of 513 to 4096 elements a one-wavefront
-        # workgroup each, those of at most 512 the exact wavefront kernels
+        # largest first; tensors of 513 to 4096 elements a wavefront each
+        # in the fast kernels, those of at most 512 the exact wavefront kernels
         eng = pair.opt._engine
         assert 32768 < max(p.numel() for p in params) <= 65536
         assert eng._chunk == 65536 and eng._n_chunks == len(params)

@@ -1,5 +1,5 @@
 """Small tensors stepped one wavefront each (LumaStepArgs.small_chunks), and
-medium tensors stepped by one-wavefront workgroups of the fast kernels
+medium tensors stepped one wavefront each by the fast kernels
 (LumaStepArgs.medium_chunks).
 
 Tensors of at most LUMA_SMALL_TENSOR elements take the last chunk records
@@ -94,7 +94,7 @@ def test_small_route_matches_workgroup_route():
 
 
 # medium tensors: above LUMA_SMALL_TENSOR and up to LUMA_MEDIUM_TENSOR
-# elements, a one-wavefront workgroup each through the fast kernels
+# elements, one wavefront each through the fast kernels
 MEDIUM = [513, 600, 1000, 2047, 2048, 2049, 3000, 4095, 4096, 4097, 1, 300, 70000, 9000]
 
 
@@ -116,7 +116,8 @@ def test_medium_tensors_match_oracle(dtype):
 
 def test_medium_route_for_every_tensor(monkeypatch):
     """Step 2 routes every tensor of one chunk (here up to 16384 elements)
-    through one-wavefront workgroups, step 3 none, step 4 the default: every
+    through the wavefront-per-tensor route of the fast kernels, step 3 none,
+    step 4 the default: every
     step matches the oracle, and the code summaries that step 2 did not
     write are not used by step 3."""
     pair = SampledPair(_params(13), range(len(SIZES)))

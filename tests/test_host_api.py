@@ -151,7 +151,7 @@ def test_sparse_grad_rejected():
 
 
 def test_step_chunk_policy():
-    """The step's chunk length: 131072 while 4096 chunks of it fit in the
+    """The step's chunk length: 131072 while 2048 chunks of it fit in the
     set's total size, else halved down to 16384; a fixed length overrides it."""
     import types
     import numpy as np
@@ -159,23 +159,26 @@ def test_step_chunk_policy():
     pick = _Engine.chunk_for
     auto = _engine_stub(chunk_elems=0)
     assert pick(auto, np.array([4096 * 4096], dtype=np.int64)) == 16384
-    assert pick(auto, np.array([65536] * 4096, dtype=np.int64)) == 65536
-    assert pick(auto, np.array([65536] * 8192, dtype=np.int64)) == 131072
-    assert pick(auto, np.array([131072] * 2048, dtype=np.int64)) == 65536
-    assert pick(auto, np.array([65536] * 4095, dtype=np.int64)) == 32768
-    assert pick(auto, np.array([65536] * 2048, dtype=np.int64)) == 32768
-    assert pick(auto, np.array([65536] * 2047, dtype=np.int64)) == 16384
+    # (fewer than 2048 tensors above the wavefront limit in these)
+    assert pick(auto, np.array([65536] * 1024 + [1] * 3000, dtype=np.int64)) == 32768
+    assert pick(auto, np.array([131072] * 2047, dtype=np.int64)) == 65536
+    assert pick(auto, np.array([131072] * 1024, dtype=np.int64)) == 65536
+    assert pick(auto, np.array([65536] * 2047, dtype=np.int64)) == 32768
+    assert pick(auto, np.array([65536] * 1024, dtype=np.int64)) == 32768
+    assert pick(auto, np.array([65536] * 1023, dtype=np.int64)) == 16384
     assert pick(auto, np.array([1] * 20000, dtype=np.int64)) == 16384
     assert pick(auto, np.array([65536] * 1000 + [1] * 20000, dtype=np.int64)) == 16384
     assert pick(_engine_stub(chunk_elems=2048), np.array([10], dtype=np.int64)) == 2048
-    # 4096 or more tensors above the wavefront limit: one chunk per tensor,
+    # 2048 or more tensors above the wavefront limit: one chunk per tensor,
     # as long as the largest of them (at most 131072)
-    assert pick(auto, np.array([600] * 4095 + [40000], dtype=np.int64)) == 65536
-    assert pick(auto, np.array([600] * 4096 + [300000], dtype=np.int64)) == 131072
-    assert pick(auto, np.array([600] * 4095 + [40000] + [1] * 10, dtype=np.int64)) == 65536
-    assert pick(auto, np.array([600] * 4095 + [1] * 10, dtype=np.int64)) == 16384
+    assert pick(auto, np.array([65536] * 2048, dtype=np.int64)) == 65536
+    assert pick(auto, np.array([65536] * 4096, dtype=np.int64)) == 131072
+    assert pick(auto, np.array([600] * 2047 + [40000], dtype=np.int64)) == 65536
+    assert pick(auto, np.array([600] * 2048 + [300000], dtype=np.int64)) == 131072
+    assert pick(auto, np.array([600] * 2047 + [40000] + [1] * 10, dtype=np.int64)) == 65536
+    assert pick(auto, np.array([600] * 2047 + [1] * 10, dtype=np.int64)) == 16384
     assert pick(_engine_stub(small_tensors=False),
-                np.array([600] * 4095 + [1] * 10, dtype=np.int64)) == 16384
+                np.array([600] * 2047 + [1] * 10, dtype=np.int64)) == 16384
 
 
 def test_step_rejects_bad_chunk_length():
