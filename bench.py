@@ -345,8 +345,8 @@ def traffic_report(config, kernel, fetch_csv, write_csv, copy_fetch_csv, copy_wr
         f"# HBM traffic of {kernel} on {config} ({n_params} params, {gbytes}-byte grads)",
         "",
         "Commands (each a separate rocprofv3 run):",
-        f"    rocprofv3 --pmc FETCH_SIZE --output-format csv -d <dir> -- python bench.py --config {config} --steps 3 --warmup 1 --no-cpu",
-        f"    rocprofv3 --pmc WRITE_SIZE --output-format csv -d <dir> -- python bench.py --config {config} --steps 3 --warmup 1 --no-cpu",
+        f"    rocprofv3 --pmc FETCH_SIZE --output-format csv -d <dir> -- python bench.py --config {config} --steps 3 --warmup 1 --no-cpu --no-others",
+        f"    rocprofv3 --pmc WRITE_SIZE --output-format csv -d <dir> -- python bench.py --config {config} --steps 3 --warmup 1 --no-cpu --no-others",
         "    rocprofv3 --pmc FETCH_SIZE --output-format csv -d <dir> -- python bench.py --copy-calibration 3",
         "    rocprofv3 --pmc WRITE_SIZE --output-format csv -d <dir> -- python bench.py --copy-calibration 3",
         f"    python bench.py --traffic-report {config} {kernel} <fetch.csv> <write.csv> <copy_fetch.csv> <copy_write.csv>",
@@ -361,6 +361,12 @@ def traffic_report(config, kernel, fetch_csv, write_csv, copy_fetch_csv, copy_wr
         f"traffic_bytes_per_launch: {fetch + write:.0f}",
         f"traffic_over_algorithmic: {(fetch + write) / algo:.4f}",
     ]
+    if kernel == "luma::pass1":
+        # what pass 1 fetched beyond its gradients and summaries, as a share
+        # of the 4 code bytes per parameter it would read without them
+        extra = fetch - algo
+        lines.append(f"fetched beyond gradients and summaries: {extra:.0f} B = "
+                     f"{100 * extra / (4 * n_params):.2f}% of the code bytes (4 B/param)")
     with open(out, "w") as f:
         f.write("\n".join(lines) + "\n")
     print("\n".join(lines))
@@ -394,7 +400,7 @@ def stats_report(config, trace_csv, bench_json, out):
         "",
         "Commands (MI355X, one GPU):",
         f"    rocprofv3 --kernel-trace --stats --output-format csv -d <dir> -o kt -- python bench.py --config {config} "
-        f"--steps {bench['steps']} --warmup {bench['warmup']} --no-cpu > <bench.json>",
+        f"--steps {bench['steps']} --warmup {bench['warmup']} --no-cpu --no-others > <bench.json>",
         f"    python bench.py --stats-report {config} <dir>/.../kt_kernel_trace.csv <bench.json> <out.md>",
         "",
         f"{bench['warmup'] + bench['steps']} launches of each kernel: {bench['warmup']} warm-up + "
@@ -449,7 +455,7 @@ def issue_report(config, kernel, pmc_csv, out):
         "",
         "Commands (MI355X, one GPU):",
         f"    rocprofv3 --pmc {ISSUE_COUNTERS} --output-format csv -d <dir> -- "
-        f"python bench.py --config {config} --steps 3 --warmup 1 --no-cpu",
+        f"python bench.py --config {config} --steps 3 --warmup 1 --no-cpu --no-others",
         f"    python bench.py --issue-report {config} {kernel} <counter_collection.csv> <out.md>",
         "",
         f"kernel time from SQ_BUSY_CYCLES at 2.4 GHz: {se_cycles / 2.4e6:.2f} ms",
