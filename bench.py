@@ -349,9 +349,9 @@ def traffic_report(config, kernel, fetch_csv, write_csv, copy_fetch_csv, copy_wr
     lines = [
         f"# HBM traffic of {kernel} on {config} ({n_params} params, {gbytes}-byte grads)",
         "",
-        "Commands (each a separate rocprofv3 run):",
-        f"    rocprofv3 --pmc FETCH_SIZE --output-format csv -d <dir> -- python bench.py --config {config} --steps 3 --warmup 1 --no-cpu --no-others",
-        f"    rocprofv3 --pmc WRITE_SIZE --output-format csv -d <dir> -- python bench.py --config {config} --steps 3 --warmup 1 --no-cpu --no-others",
+        "Commands (each a separate rocprofv3 run, after `python bench.py --pretouch-only`):",
+        f"    rocprofv3 --pmc FETCH_SIZE --output-format csv -d <dir> -- python bench.py --config {config} --steps 3 --warmup 1 --no-cpu --no-others --no-pretouch",
+        f"    rocprofv3 --pmc WRITE_SIZE --output-format csv -d <dir> -- python bench.py --config {config} --steps 3 --warmup 1 --no-cpu --no-others --no-pretouch",
         "    rocprofv3 --pmc FETCH_SIZE --output-format csv -d <dir> -- python bench.py --copy-calibration 3",
         "    rocprofv3 --pmc WRITE_SIZE --output-format csv -d <dir> -- python bench.py --copy-calibration 3",
         f"    python bench.py --traffic-report {config} {kernel} <fetch.csv> <write.csv> <copy_fetch.csv> <copy_write.csv>",
@@ -404,8 +404,9 @@ def stats_report(config, trace_csv, bench_json, out):
         f"{str(cfg['grad']).replace('torch.', '')} grads)",
         "",
         "Commands (MI355X, one GPU):",
+        "    python bench.py --pretouch-only",
         f"    rocprofv3 --kernel-trace --stats --output-format csv -d <dir> -o kt -- python bench.py --config {config} "
-        f"--steps {bench['steps']} --warmup {bench['warmup']} --no-cpu --no-others > <bench.json>",
+        f"--steps {bench['steps']} --warmup {bench['warmup']} --no-cpu --no-others --no-pretouch > <bench.json>",
         f"    python bench.py --stats-report {config} <dir>/.../kt_kernel_trace.csv <bench.json> <out.md>",
         "",
         f"{bench['warmup'] + bench['steps']} launches of each kernel: {bench['warmup']} warm-up + "
@@ -459,8 +460,9 @@ def issue_report(config, kernel, pmc_csv, out):
         f"# Instruction issue of {kernel} on {config} ({n_params} params)",
         "",
         "Commands (MI355X, one GPU):",
+        "    python bench.py --pretouch-only",
         f"    rocprofv3 --pmc {ISSUE_COUNTERS} --output-format csv -d <dir> -- "
-        f"python bench.py --config {config} --steps 3 --warmup 1 --no-cpu --no-others",
+        f"python bench.py --config {config} --steps 3 --warmup 1 --no-cpu --no-others --no-pretouch",
         f"    python bench.py --issue-report {config} {kernel} <counter_collection.csv> <out.md>",
         "",
         f"kernel time from SQ_BUSY_CYCLES at 2.4 GHz: {se_cycles / 2.4e6:.2f} ms",
@@ -609,6 +611,9 @@ def main():
                          "tensor, the GPT-2-small list and the 20,000-tensor set)")
     ap.add_argument("--no-pretouch", dest="pretouch", action="store_false",
                     help="skip writing the HBM once from a child process before the run")
+    ap.add_argument("--pretouch-only", action="store_true",
+                    help="only write the HBM once (from a child process) and exit: run it before "
+                         "a profiled bench.py --no-pretouch")
     ap.add_argument("--ceilings", action="store_true",
                     help="time torch's copy and max over 16 GiB (achievable HBM rates)")
     ap.add_argument("--copy-calibration", type=int, metavar="REPS",
@@ -622,6 +627,9 @@ def main():
     ap.add_argument("--stats-report", nargs=4, metavar=("CONFIG", "TRACE_CSV", "BENCH_JSON", "OUT"),
                     help="summarise a rocprofv3 --kernel-trace --stats run of bench.py into OUT")
     args = ap.parse_args()
+    if args.pretouch_only:
+        print(f"bench.py: wrote {pretouch_hbm()} GiB of HBM once", file=sys.stderr)
+        return
     if args.traffic_report:
         traffic_report(*args.traffic_report)
         return
