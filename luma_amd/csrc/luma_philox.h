@@ -81,7 +81,13 @@ LUMA_PHILOX_FN U4 philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t 
 
 #if defined(__HIPCC__)
 // Device variant with the multipliers passed in (callers keep them, and the
-// key, in VGPRs; see in_vgpr in luma_step.hip).
+// key, in VGPRs; see in_vgpr in luma_step.hip).  Each three-way xor is one
+// v_bitop3_b32 (truth table 0x96, gfx950) instead of two v_xor_b32: the
+// compiler does not form it from a ^ b ^ c by itself.
+__device__ __forceinline__ uint32_t xor3(uint32_t a, uint32_t b, uint32_t c) {
+  return __builtin_amdgcn_bitop3_b32(a, b, c, 0x96);
+}
+
 __device__ __forceinline__ U4 philox4x32_10_v(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3,
                                               uint32_t k0, uint32_t k1, uint32_t m0,
                                               uint32_t m1) {
@@ -89,8 +95,8 @@ __device__ __forceinline__ U4 philox4x32_10_v(uint32_t c0, uint32_t c1, uint32_t
   for (int r = 0; r < 10; ++r) {
     const uint64_t p0 = (uint64_t)m0 * c0;
     const uint64_t p1 = (uint64_t)m1 * c2;
-    const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0;
-    const uint32_t n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1;
+    const uint32_t n0 = xor3((uint32_t)(p1 >> 32), c1, k0);
+    const uint32_t n2 = xor3((uint32_t)(p0 >> 32), c3, k1);
     c0 = n0;
     c1 = (uint32_t)p1;
     c2 = n2;
