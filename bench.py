@@ -519,7 +519,9 @@ def pretouch_hbm() -> int:
     if r.returncode != 0:
         raise RuntimeError(f"bench.py: HBM pre-touch failed ({r.returncode}): {r.stderr[-2000:]}")
     return int(r.stdout.split()[-1])
-# the other BASELINE workloads timed by the default run (name, timed steps:
+
+
+# the other benchmark workloads timed by the default run (name, timed steps:
 # the step counts the workloads are stated with), and their CPU baselines on
 # the whole parameter set (untimed warm-up steps incl. the init step, timed)
 OTHER_CONFIGS = (("single_4096", 100), ("gpt2_small", 200), ("many_small", 100))
@@ -667,7 +669,7 @@ def main():
 
     others = {}
     if args.others and args.config == "llama3_8b":
-        # the other BASELINE workloads at their stated step counts, after the
+        # the other benchmark workloads at their stated step counts, after the
         # headline's memory is released
         for name, steps in OTHER_CONFIGS:
             r = run_gpu(name, steps, 3, dev)
