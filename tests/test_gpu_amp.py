@@ -27,9 +27,11 @@ class _Classic(LUMA):
 
 
 def _model():
+    # weights of 8192 (a workgroup per chunk), 3072 (one wavefront each: the
+    # medium route) and 24 elements (the small-tensor kernels), and biases
     torch.manual_seed(0)
-    return nn.Sequential(nn.Linear(64, 128), nn.GELU(), nn.Linear(128, 64), nn.GELU(),
-                         nn.Linear(64, 1)).to(DEV)
+    return nn.Sequential(nn.Linear(64, 128), nn.GELU(), nn.Linear(128, 24), nn.GELU(),
+                         nn.Linear(24, 1)).to(DEV)
 
 
 def _state(opt, model):

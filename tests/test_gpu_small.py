@@ -114,6 +114,47 @@ def test_medium_tensors_match_oracle(dtype):
         assert eng._small_chunks == sum(1 for n in MEDIUM if n <= L.SMALL_TENSOR)
 
 
+@pytest.mark.parametrize("scaled", [False, True])
+def test_medium_route_matches_workgroup_route(scaled):
+    """With Philox draws (and, scaled, GradScaler's scale handed to the
+    kernels): the medium tensors' wavefront route and the workgroup route
+    run the same per-element arithmetic on the same draws, so codes, scales
+    and parameters agree bit for bit."""
+    from luma_amd import LUMA
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    sizes = [513, 700, 1024, 2047, 2048, 2500, 4095, 4096] * 6 + [9000, 100]
+    a = [(torch.randn(n, device=DEV, generator=gen) * 0.02).requires_grad_(True) for n in sizes]
+    b = [p.detach().clone().requires_grad_(True) for p in a]
+    for p in a + b:
+        p.grad_dtype = None        # allow bf16 gradients on fp32 parameters
+    oa, ob = LUMA(a, lr=1e-3, weight_decay=0.01), LUMA(b, lr=1e-3, weight_decay=0.01)
+    ob._base_seed = oa._base_seed
+    ob._get_engine(b[0].device).medium_tensors = False
+    scale = 2.0 ** 12
+    if scaled:
+        for o in (oa, ob):
+            o.grad_scale = torch.tensor([scale], device=DEV)
+            o.found_inf = torch.tensor([0.0], device=DEV)
+    for t in range(5):
+        for p, q in zip(a, b):
+            g = torch.randn(p.shape, device=DEV, generator=gen) * 1e-3
+            if t == 2:
+                g[::97] *= 100.0          # outliers: codes near the top of the grid
+            g = (g * scale if scaled else g).to(torch.bfloat16)
+            p.grad, q.grad = g, g.clone()
+        oa.step()
+        ob.step()
+    torch.cuda.synchronize()
+    n_med = sum(1 for n in sizes if L.SMALL_TENSOR < n <= L.MEDIUM_TENSOR)
+    assert oa._engine._medium_chunks == n_med and ob._engine._medium_chunks == 0
+    sa, sb = oa.state_dict()["state"], ob.state_dict()["state"]
+    for i, (p, q) in enumerate(zip(a, b)):
+        assert torch.equal(sa[i]["Q_m"], sb[i]["Q_m"]), i
+        assert torch.equal(sa[i]["Q_w"], sb[i]["Q_w"]), i
+        assert sa[i]["S_m"] == sb[i]["S_m"] and sa[i]["S_v"] == sb[i]["S_v"], i
+        assert torch.equal(p.detach(), q.detach()), i
+
+
 def test_medium_route_for_every_tensor(monkeypatch):
     """Step 2 routes every tensor of one chunk (here up to 16384 elements)
     through the wavefront-per-tensor route of the fast kernels, step 3 none,
