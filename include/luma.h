@@ -81,7 +81,7 @@ extern "C" {
  * stepped one wavefront each (LumaStepArgs.medium_chunks): a whole
  * workgroup would leave most of its wavefronts idle on them.
  */
-#define LUMA_MEDIUM_TENSOR 4096
+#define LUMA_MEDIUM_TENSOR 8192
 
 /*
  * Bytes of one slot: a tensor's persistent device state (step count, S_m,

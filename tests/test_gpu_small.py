@@ -95,7 +95,8 @@ def test_small_route_matches_workgroup_route():
 
 # medium tensors: above LUMA_SMALL_TENSOR and up to LUMA_MEDIUM_TENSOR
 # elements, one wavefront each through the fast kernels
-MEDIUM = [513, 600, 1000, 2047, 2048, 2049, 3000, 4095, 4096, 4097, 1, 300, 70000, 9000]
+MEDIUM = [513, 600, 1000, 2047, 2048, 2049, 3000, 4095, 4096, 4097, 8191, 8192, 8193, 1, 300,
+          70000, 9000]
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
@@ -122,7 +123,7 @@ def test_medium_route_matches_workgroup_route(scaled):
     and parameters agree bit for bit."""
     from luma_amd import LUMA
     gen = torch.Generator(device=DEV).manual_seed(5)
-    sizes = [513, 700, 1024, 2047, 2048, 2500, 4095, 4096] * 6 + [9000, 100]
+    sizes = [513, 700, 1024, 2047, 2048, 2500, 4095, 4096, 6000, 8192] * 5 + [9000, 100]
     a = [(torch.randn(n, device=DEV, generator=gen) * 0.02).requires_grad_(True) for n in sizes]
     b = [p.detach().clone().requires_grad_(True) for p in a]
     for p in a + b:
@@ -163,11 +164,12 @@ def test_medium_route_for_every_tensor(monkeypatch):
     write are not used by step 3."""
     pair = SampledPair(_params(13), range(len(SIZES)))
     _step(pair, 1)
+    medium = L.MEDIUM_TENSOR
     monkeypatch.setattr(L, "MEDIUM_TENSOR", 1 << 20)
     _step(pair, 2)
     eng = pair.opt._engine
     assert eng._medium_chunks == sum(1 for n in SIZES if L.SMALL_TENSOR < n <= eng._chunk)
-    monkeypatch.setattr(L, "MEDIUM_TENSOR", 4096)
+    monkeypatch.setattr(L, "MEDIUM_TENSOR", medium)
     eng.medium_tensors = False
     _step(pair, 3)
     assert eng._medium_chunks == 0

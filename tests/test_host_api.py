@@ -299,7 +299,8 @@ def test_chunk_layout_medium_tensors():
     workgroup tensors keep their order and come first."""
     import numpy as np
     from luma_amd.optimizer import _Engine
-    numels = np.array([5000, 3, 512, 513, 40000, 1, 20000, 4096, 2000], dtype=np.int64)
+    M = L.MEDIUM_TENSOR
+    numels = np.array([M + 904, 3, 512, 513, 40000, 1, 20000, M, 2000], dtype=np.int64)
     eng = _engine_stub(medium_tensors=True)
     first, ch, n_small, n_med = _Engine.chunk_layout(eng, numels, 16384)
     assert (n_med, n_small) == (3, 3)
@@ -311,9 +312,10 @@ def test_chunk_layout_medium_tensors():
     first, ch, n_small, n_med = _Engine.chunk_layout(eng, numels, 2048)
     assert (n_med, n_small) == (2, 3)
     assert ch["tensor"].tolist()[-5:] == [8, 3, 2, 1, 5]
-    # 4096 or more tensors above the medium limit decide the one-chunk-per-tensor rule
+    # the tensors above the medium limit decide the one-chunk-per-tensor rule
+    # (2048 or more of them)
     assert _Engine.chunk_for(eng, np.array([3000] * 5000 + [40000], dtype=np.int64)) == 16384
-    assert _Engine.chunk_for(eng, np.array([5000] * 4096 + [40000], dtype=np.int64)) == 65536
+    assert _Engine.chunk_for(eng, np.array([M + 904] * 2048 + [40000], dtype=np.int64)) == 65536
 
 
 def test_moved_pointer_tables_are_reused():
