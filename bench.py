@@ -427,7 +427,7 @@ def stats_report(config, trace_csv, bench_json, out):
     lines += ["",
               "The bench's HIP-event intervals bracket each pass: pass 1's includes "
               "`luma::pass1_small_kernel`, pass 2's `luma::pass2_small_kernel` (tensors of at most "
-              "512 elements, one wavefront each) when the set has any.",
+              "256 elements, one wavefront each) when the set has any.",
               "",
               f"Step time in the same run (bench wall clock): {bench['ms_per_step']:.3f} ms; "
               f"{bench['value']} Gparams/s.",

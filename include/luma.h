@@ -71,10 +71,11 @@ extern "C" {
 
 /*
  * Tensors of at most this many elements are best stepped one wavefront each
- * (LumaStepArgs.small_chunks): a workgroup of their own would spend most of
- * its time in set-up.
+ * by the exact path (LumaStepArgs.small_chunks): a workgroup of their own
+ * would spend most of its time in set-up, and the fast kernels' wavefront
+ * route (medium_chunks) runs a partial group for them.
  */
-#define LUMA_SMALL_TENSOR 512
+#define LUMA_SMALL_TENSOR 256
 
 /*
  * Tensors above LUMA_SMALL_TENSOR and of at most this many elements are best

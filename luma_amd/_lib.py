@@ -18,7 +18,7 @@ LIB_PATH = os.path.join(HERE, LIB_NAME)
 
 CHUNK_ELEMS = 131072         # LUMA_CHUNK_ELEMS (default and largest chunk length)
 CHUNK_ELEMS_MIN = 2048       # LUMA_CHUNK_ELEMS_MIN
-SMALL_TENSOR = 512           # LUMA_SMALL_TENSOR
+SMALL_TENSOR = 256           # LUMA_SMALL_TENSOR
 MEDIUM_TENSOR = 8192         # LUMA_MEDIUM_TENSOR
 STEP_TENSOR_CHUNK_MIN = 16384  # LUMA_STEP_TENSOR_CHUNK_MIN
 SLOT_BYTES = 512             # LUMA_SLOT_BYTES

@@ -103,11 +103,11 @@ def test_cfg3_many_small():
         # more than 2048 tensors above the single-wavefront routes: one
         # chunk per tensor (the largest has 32769 to 65536 elements),
         # largest first; tensors of 513 to 8192 elements a wavefront each
-        # in the fast kernels, those of at most 512 the exact wavefront kernels
+        # in the fast kernels, those of at most 256 the exact wavefront kernels
         eng = pair.opt._engine
         assert 32768 < max(p.numel() for p in params) <= 65536
         assert eng._chunk == 65536 and eng._n_chunks == len(params)
-        assert eng._small_chunks == sum(1 for p in params if p.numel() <= 512)
+        assert eng._small_chunks == sum(1 for p in params if p.numel() <= L.SMALL_TENSOR)
         assert eng._medium_chunks == sum(1 for p in params
                                          if L.SMALL_TENSOR < p.numel() <= L.MEDIUM_TENSOR)
         rows = pair.check()

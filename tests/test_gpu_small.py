@@ -20,7 +20,8 @@ pytestmark = pytest.mark.gpu
 
 DEV = torch.device("cuda")
 # around the limit, tiny, and a few tensors that take whole workgroups
-SIZES = [1, 2, 7, 64, 100, 511, 512, 513, 1000, 2047, 2048, 4096, 5000, 70000, 300, 8]
+SIZES = [1, 2, 7, 64, 100, 255, 256, 257, 511, 512, 513, 1000, 2047, 2048, 4096, 5000, 70000, 300,
+         8]
 
 
 def _params(seed=11):
@@ -52,10 +53,11 @@ def test_routes_change_between_steps(monkeypatch):
     step 3's pass 1."""
     pair = SampledPair(_params(12), range(len(SIZES)))
     _step(pair, 1)
+    small = L.SMALL_TENSOR
     monkeypatch.setattr(L, "SMALL_TENSOR", 1 << 20)
     _step(pair, 2)
     assert pair.opt._engine._small_chunks == pair.opt._engine._n_chunks
-    monkeypatch.setattr(L, "SMALL_TENSOR", 512)
+    monkeypatch.setattr(L, "SMALL_TENSOR", small)
     pair.opt._engine.small_tensors = False
     _step(pair, 3)
     assert pair.opt._engine._small_chunks == 0
@@ -70,12 +72,13 @@ def test_small_route_matches_workgroup_route():
     the fast path's, within 1e-6 of the exact one)."""
     from luma_amd import LUMA
     gen = torch.Generator(device=DEV).manual_seed(3)
-    sizes = [1, 5, 64, 200, 512, 333] * 20
+    sizes = [1, 5, 64, 200, L.SMALL_TENSOR, L.SMALL_TENSOR - 67] * 20
     a = [(torch.randn(n, device=DEV, generator=gen) * 0.02).requires_grad_(True) for n in sizes]
     b = [p.detach().clone().requires_grad_(True) for p in a]
     oa, ob = LUMA(a, lr=1e-3), LUMA(b, lr=1e-3)
     ob._base_seed = oa._base_seed
-    ob._get_engine(b[0].device).small_tensors = False
+    eb = ob._get_engine(b[0].device)
+    eb.small_tensors = eb.medium_tensors = False
     for t in range(4):
         for p, q in zip(a, b):
             g = torch.randn(p.shape, device=DEV, generator=gen) * 1e-3

@@ -250,7 +250,8 @@ def test_chunk_layout_small_tensors_last():
     import types
     import numpy as np
     from luma_amd.optimizer import _Engine
-    numels = np.array([5000, 3, 512, 513, 40000, 1, 20000], dtype=np.int64)
+    S = L.SMALL_TENSOR
+    numels = np.array([5000, 3, S, S + 1, 40000, 1, 20000], dtype=np.int64)
     eng = _engine_stub(small_tensors=True)
     first, ch, n_small, n_med = _Engine.chunk_layout(eng, numels, 16384)
     assert n_small == 3
@@ -272,7 +273,8 @@ def test_chunk_layout_many_tensors_largest_first(monkeypatch):
     small tensors still last; first_chunk points at each tensor's records."""
     import numpy as np
     import luma_amd.optimizer as O
-    numels = np.array([5000, 3, 512, 513, 40000, 1, 20000, 5000], dtype=np.int64)
+    S = L.SMALL_TENSOR
+    numels = np.array([5000, 3, S, S + 1, 40000, 1, 20000, 5000], dtype=np.int64)
     eng = _engine_stub()
     monkeypatch.setattr(O, "STEP_TARGET_CHUNKS", 5)
     assert O._Engine.chunk_for(eng, numels) == 65536
@@ -300,7 +302,8 @@ def test_chunk_layout_medium_tensors():
     import numpy as np
     from luma_amd.optimizer import _Engine
     M = L.MEDIUM_TENSOR
-    numels = np.array([M + 904, 3, 512, 513, 40000, 1, 20000, M, 2000], dtype=np.int64)
+    S = L.SMALL_TENSOR
+    numels = np.array([M + 904, 3, S, S + 1, 40000, 1, 20000, M, 2000], dtype=np.int64)
     eng = _engine_stub(medium_tensors=True)
     first, ch, n_small, n_med = _Engine.chunk_layout(eng, numels, 16384)
     assert (n_med, n_small) == (3, 3)
