@@ -11,8 +11,10 @@
 //   pass 2   (grid = chunks)  recompute m', v' bit-identically, AdamW update of
 //                             the parameter, LogSR re-quantisation on the new
 //                             grid (functional.py:278-279, 293-295).
-// Tensors of at most LUMA_SMALL_TENSOR elements take a kernel of their own in
-// each pass (a wavefront per tensor).  Nothing is materialised between the
+// A chunk takes a workgroup; a medium tensor's one chunk takes a wavefront of
+// the same launches (four to a workgroup).  Tensors of at most
+// LUMA_SMALL_TENSOR elements take a kernel of their own in each pass (a
+// wavefront per tensor, the exact path).  Nothing is materialised between the
 // passes except 16 bytes per chunk.  With GradScaler's scaling (LumaScaling)
 // every kernel unscales the gradients as it loads them, and returns at once
 // when the overflow flag is set.
