@@ -408,12 +408,20 @@ __device__ __forceinline__ void finalize_wave(const StepSrc &src, const Tensor &
                   seed_at(cv, ov, src.chunk_shift));
 }
 
-// Waves [0, n_tensors): one tensor each, except the tensors whose records
-// start in the medium and small runs; those (one record each, as a rule)
-// take a lane each in the waves after, 64 records per wave, so that the
-// float64 tail of 64 small tensors runs side by side.
+// Tensors of at most kLaneChunks chunks take a lane each: 64 to a wavefront,
+// the float64 tail of 64 tensors side by side.  The others take a wavefront.
+constexpr int kLaneChunks = 4;
+
+__device__ __forceinline__ int tensor_chunks(const Tensor &T, int32_t shift) {
+  return (int)(((T.numel - 1) >> shift) + 1);
+}
+
+// Waves [0, n_tensors): one tensor each (those of more than kLaneChunks
+// chunks; the others return at once); then, from a tensor table, one lane
+// per chunk record: the lane of a tensor's first record steps a tensor of at
+// most kLaneChunks chunks.
 __device__ __host__ inline int32_t finalize_waves(const StepSrc &src, int32_t n_tensors) {
-  return n_tensors + (src.tensors ? (src.n_chunks - src.medium_from + 63) / 64 : 0);
+  return n_tensors + (src.tensors ? (src.n_chunks + 63) / 64 : 0);
 }
 
 __global__ __launch_bounds__(kThreads) void finalize_kernel(StepSrc src,
@@ -428,17 +436,18 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(StepSrc src,
       return;
     }
     const Tensor T = src.tensors[w];
-    if (T.first_chunk >= src.medium_from) return;   // a lane's (below)
+    if (tensor_chunks(T, src.chunk_shift) <= kLaneChunks) return;   // a lane's (below)
     finalize_wave(src, T, src.groups[T.group], partials);
     return;
   }
   if (!src.tensors) return;
-  const int64_t r = (int64_t)src.medium_from + (int64_t)(w - n_tensors) * 64 + lane_id();
+  const int64_t r = (int64_t)(w - n_tensors) * 64 + lane_id();
   if (r >= src.n_chunks) return;   // (no wave operations below)
   const Tensor T = src.tensors[src.chunks[r].tensor];
-  if (T.first_chunk != r) return;   // not the tensor's first record
+  // the tensor's first record, and few enough chunks for one lane
+  if (T.first_chunk != r || tensor_chunks(T, src.chunk_shift) > kLaneChunks) return;
   const int64_t prev = T.slot->step;
-  const int nch = (int)(((T.numel - 1) >> src.chunk_shift) + 1);
+  const int nch = tensor_chunks(T, src.chunk_shift);
   float am = 0.0f, av = 0.0f;
   uint32_t cm = kNoArg, cv = kNoArg, om = kNoArg, ov = kNoArg;
   for (int c = 0; c < nch; ++c) {
