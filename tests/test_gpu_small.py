@@ -37,7 +37,7 @@ def _step(pair, t, dtype=torch.float32):
     return pair.check()
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_small_tensors_match_oracle(dtype):
     pair = SampledPair(_params(), range(len(SIZES)))
     for t in range(1, 5):
@@ -102,7 +102,7 @@ MEDIUM = [513, 600, 1000, 2047, 2048, 2049, 3000, 4095, 4096, 4097, 8191, 8192, 
           70000, 9000]
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_medium_tensors_match_oracle(dtype):
     gen = torch.Generator(device=DEV).manual_seed(21)
     params = [(torch.randn(n, device=DEV, generator=gen) * 0.02) for n in MEDIUM]
