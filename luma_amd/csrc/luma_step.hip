@@ -1221,12 +1221,13 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   // out before the per-tensor constants are derived, so that their latency
   // covers that arithmetic.
   static_assert(LUMA_SUMMARY_WORDS == kThreads, "one summary word per thread of a chunk");
-  Raw8 ra, rb;
+  Raw8 ra, rb, rc;
   uint32_t sw = 0;
   if (n_whole > 0) {
     if (SUMM) {
       sw = T.summary[ci * LUMA_SUMMARY_WORDS + sh.tid()];
       load_grads<GD>(T, group_at(0), ra);
+      load_grads<GD>(T, group_at(1), rb);
     } else {
       load_raw<GD>(T, beg + (int64_t)sh.tid() * kVec, ra);
     }
@@ -1234,24 +1235,26 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   const Bounds B = make_bounds((const Grid *)old, nullptr, h.beta1, h.beta2);
   const DecodeK D = decode_consts(old, h.eps);
   P1Const K;
-  K.dm = in_vgpr(D.dm);
-  K.ndw = in_vgpr(-D.dw);
-  K.nbias = in_vgpr(8388608.0f * D.dw);
-  K.iwmin = in_vgpr(D.iwmin);
-  K.eps = in_vgpr(D.eps);
-  K.b1 = in_vgpr(h.beta1);
-  K.omb1 = in_vgpr(h.omb1);
-  K.b2 = in_vgpr(h.beta2);
-  K.omb2 = in_vgpr(h.omb2);
-  K.inv = in_vgpr(inv);
-  K.sign = in_vgpr(0x80000000u);
+  // (the constants stay where the compiler puts them, in SGPRs: pass 1
+  // waits on memory, not on issue, and the VGPRs hold its loads in flight)
+  K.dm = (D.dm);
+  K.ndw = (-D.dw);
+  K.nbias = (8388608.0f * D.dw);
+  K.iwmin = (D.iwmin);
+  K.eps = (D.eps);
+  K.b1 = (h.beta1);
+  K.omb1 = (h.omb1);
+  K.b2 = (h.beta2);
+  K.omb2 = (h.omb2);
+  K.inv = (inv);
+  K.sign = (0x80000000u);
   // 8u covers the rounding of the bound's own products and the non-monotone
   // wobble of the hardware exp2 / of the expm1 branch switch (a few ulp);
   // abs_v covers decodes whose 1/w - eps rounds slightly below zero
   // (|rr| <= 4u eps, so rr^2 <= 1e-13 eps^2)
-  K.up_m = in_vgpr(1.0f + 8.0f * kU);
-  K.up_v = in_vgpr(1.0f + 16.0f * kU);
-  K.abs_v = in_vgpr(D.eps * D.eps * 1e-10f);
+  K.up_m = (1.0f + 8.0f * kU);
+  K.up_v = (1.0f + 16.0f * kU);
+  K.abs_v = (D.eps * D.eps * 1e-10f);
   const float lo_m = 1.0f - B.dlt_m, hi_m = 1.0f / (1.0f + B.dlt_m);
   const float lo_v = 1.0f - B.dlt_v, hi_v = 1.0f / (1.0f + B.dlt_v);
   const float sub_m = 2.0f * B.abs_m, sub_v = 2.0f * B.abs_v;
@@ -1373,17 +1376,21 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
       p1_compute<SMALL, true>(G, K, kVec, Tm, Tv, am, av);
       take(e0, kVec, am, av);
     };
-    // Two gradient buffers, each loaded one iteration before its use, in a
-    // loop unrolled by two: copying a buffer whose load is in flight (a
-    // single buffer carried across iterations) would make every iteration
-    // wait for the load just issued.  (ra: group 0, loaded above.)
+    // Three gradient buffers, each loaded two iterations before its use, in
+    // a loop unrolled by three: the loop waits on memory, so each wave keeps
+    // two groups' loads in flight; no buffer whose load is in flight is
+    // copied (the copy would wait for it).  (ra, rb: groups 0 and 1, loaded
+    // above.)
     seed_thresholds();
-    for (; it < n_whole; it += 2) {
-      load_grads<GD>(T, group_at(it + 1), rb);
+    for (; it < n_whole; it += 3) {
+      load_grads<GD>(T, group_at(it + 2), rc);
       visit(ra, it);
       if (it + 1 >= n_whole) break;
-      load_grads<GD>(T, group_at(it + 2), ra);
+      load_grads<GD>(T, group_at(it + 3), ra);
       visit(rb, it + 1);
+      if (it + 2 >= n_whole) break;
+      load_grads<GD>(T, group_at(it + 4), rb);
+      visit(rc, it + 2);
     }
     it = n_whole;
   } else if (n_whole > 0) {
