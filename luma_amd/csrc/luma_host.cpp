@@ -25,6 +25,7 @@
 #include <algorithm>
 #include <condition_variable>
 #include <cstdint>
+#include <cstring>
 #include <functional>
 #include <mutex>
 #include <thread>
@@ -301,6 +302,27 @@ int refresh(py::list groups, py::list planned, carray<uint8_t> has_grad,
   return out;
 }
 
+// Whether the gradient and parameter pointers of the table's rows are those
+// of cols (one (grad, param) pair per row; the table has at least as many
+// rows).  Stops at the first difference: a table that matches no cached
+// pointer set costs one row per cached set.
+bool same_pointers(uintptr_t table, int64_t row_bytes, int64_t grad_off, int64_t param_off,
+                   carray<uint64_t> cols) {
+  if (cols.ndim() != 2 || cols.shape(1) != 2)
+    throw py::value_error("same_pointers: cols must be an (n, 2) array");
+  const int64_t n = cols.shape(0);
+  const uint64_t *c = cols.data();
+  const char *t = reinterpret_cast<const char *>(table);
+  for (int64_t r = 0; r < n; ++r) {
+    const char *row = t + r * row_bytes;
+    uint64_t g, p;
+    std::memcpy(&g, row + grad_off, sizeof g);
+    std::memcpy(&p, row + param_off, sizeof p);
+    if (g != c[2 * r] || p != c[2 * r + 1]) return false;
+  }
+  return true;
+}
+
 // state["step"] += 1 for every state dict of the list.  The dicts of one
 // plan usually hold the same count object, so the sum is formed once per
 // distinct object.  The dicts lie scattered in memory: each one, and then its
@@ -348,6 +370,7 @@ PYBIND11_MODULE(_luma_host, m) {
   Py_INCREF(g_tensor_type);
   Py_INCREF(g_param_type);
   m.def("refresh", &refresh);
+  m.def("same_pointers", &same_pointers);
   m.def("bump_steps", &bump_steps);
   // the torch whose headers this module was compiled against: it reads
   // TensorImpl fields in that version's inline layout

@@ -147,7 +147,9 @@ class _Engine:
         self._medium_chunks = 0      # the records of such tensors, before the small ones
         self._d_tensors = None
         self._table_cache = {}       # tensor-table bytes -> device copy (most recent last)
-        self._ptr_cache = {}         # pointer fingerprint -> (table, grads, params, device copy)
+        self._ptr_cache = {}         # sequence number -> (table, (n, 2) grad and param
+                                     # pointers, device copy), least recent first
+        self._ptr_seq = 0
         self._d_chunks = None
         self._n_chunks = 0
         self._group_key = None
@@ -374,32 +376,46 @@ class _Engine:
             self._d_tensors = cached
             self._tensor_key = key
 
-    # odd multipliers of the pointer fingerprint (uint64 arithmetic wraps)
-    _FP_G = np.uint64(0x9E3779B97F4A7C15)
-    _FP_P = np.uint64(0xC2B2AE3D27D4EB4F)
+    def _same_pointers(self, tt: np.ndarray, cols: np.ndarray) -> bool:
+        """Whether tt's gradient and parameter columns equal cols ((n, 2))."""
+        if len(cols) != len(tt):
+            return False
+        if self.host is not None:
+            return self.host.same_pointers(tt.ctypes.data, tt.dtype.itemsize,
+                                           tt.dtype.fields["grad"][1],
+                                           tt.dtype.fields["param"][1], cols)
+        return bool(np.array_equal(cols[:, 0], tt["grad"])
+                    and np.array_equal(cols[:, 1], tt["param"]))
 
     def _match_pointers(self, tt: np.ndarray, capturing: bool):
         """Device table for tt, which differs from the table last matched for
         it in its gradient and parameter pointers only (a planned step whose
         gradients moved, e.g. a loop that alternates gradient buffers): a
-        table uploaded for the same pointers is re-used (looked up by a
-        fingerprint of the two columns, then compared with them), so such a
-        loop uploads each table once."""
-        g, p = tt["grad"], tt["param"]
-        with np.errstate(over="ignore"):
-            fp = int((g * self._FP_G).sum(dtype=np.uint64) ^ (p * self._FP_P).sum(dtype=np.uint64))
-        hit = self._ptr_cache.pop(fp, None)
-        if hit is not None and not (hit[0] is tt and np.array_equal(hit[1], g)
-                                    and np.array_equal(hit[2], p)):
-            hit = None
-        if hit is None:
+        table uploaded for the same pointers is re-used, so such a loop
+        uploads each table once.  The cached pointer sets of tt are compared
+        with its two columns, most recent first; the host module's comparison
+        stops at the first row that differs, so a set that does not match
+        costs about one row."""
+        key = None
+        for k in reversed(self._ptr_cache):
+            ent = self._ptr_cache[k]
+            if ent[0] is tt and self._same_pointers(tt, ent[1]):
+                key = k
+                break
+        if key is None:
             if capturing:
                 raise self._capture_error("the parameter or gradient set")
-            hit = (tt, g.copy(), p.copy(), self._upload(tt))
-        self._ptr_cache[fp] = hit
+            cols = np.empty((len(tt), 2), dtype=np.uint64)
+            cols[:, 0] = tt["grad"]
+            cols[:, 1] = tt["param"]
+            self._ptr_seq += 1
+            key, ent = self._ptr_seq, (tt, cols, self._upload(tt))
+        else:
+            ent = self._ptr_cache.pop(key)
+        self._ptr_cache[key] = ent
         while len(self._ptr_cache) > self.TABLE_CACHE:
             self._ptr_cache.pop(next(iter(self._ptr_cache)))
-        self._d_tensors = hit[3]
+        self._d_tensors = ent[2]
         self._tensor_key = None   # (the bytes key of _match_table no longer applies)
 
     def set_scales(self, items):

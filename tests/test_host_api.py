@@ -321,13 +321,19 @@ def test_chunk_layout_medium_tensors():
     assert _Engine.chunk_for(eng, np.array([M + 904] * 2048 + [40000], dtype=np.int64)) == 65536
 
 
-def test_moved_pointer_tables_are_reused():
+@pytest.mark.parametrize("with_host", [True, False])
+def test_moved_pointer_tables_are_reused(with_host):
     """A planned step whose gradients alternate between buffers uploads each
-    pointer set's table once (_Engine._match_pointers), and a fingerprint
-    collision or another table object never returns a wrong table."""
+    pointer set's table once (_Engine._match_pointers), and a cached set
+    whose pointers differ, or another table object, never returns a wrong
+    table; the host module's comparison and numpy's agree."""
     from luma_amd.optimizer import _Engine
     eng = _Engine.__new__(_Engine)
+    eng.host = L.load_host() if with_host else None
+    if with_host and eng.host is None:
+        pytest.skip("host module not built")
     eng._ptr_cache = {}
+    eng._ptr_seq = 0
     eng._tensor_key = b""
     uploads = []
     eng._upload = lambda arr: uploads.append(arr.copy()) or len(uploads)
@@ -344,10 +350,19 @@ def test_moved_pointer_tables_are_reused():
     tt2 = tt.copy()
     eng._match_pointers(tt2, capturing=False)
     assert len(uploads) == 3
-    # a cached entry whose columns differ (a forced collision): uploaded afresh
-    fp = list(eng._ptr_cache)[-1]                      # tt2's entry
-    ent = eng._ptr_cache[fp]
-    assert ent[0] is tt2
-    eng._ptr_cache = {fp: (ent[0], ent[1] + 1, ent[2], ent[3])}
+    # two gradients swapped, and the last parameter moved: new tables
+    tt["grad"] = sets[0][[1, 0, 2, 3, 4]]
+    eng._match_pointers(tt, capturing=False)
+    assert len(uploads) == 4
+    tt["grad"] = sets[0]
+    tt["param"][4] += 256
+    eng._match_pointers(tt, capturing=False)
+    assert len(uploads) == 5 and eng._d_tensors == 5
+    assert len(eng._ptr_cache) == _Engine.TABLE_CACHE
+    # a cached entry whose columns differ from the table's: uploaded afresh
+    key = list(eng._ptr_cache)[-1]
+    ent = eng._ptr_cache[key]
+    assert ent[0] is tt
+    eng._ptr_cache = {key: (ent[0], ent[1] + 1, ent[2])}
     with pytest.raises(RuntimeError):
         eng._match_pointers(ent[0], capturing=True)   # would need an upload under capture
