@@ -1380,18 +1380,24 @@ __device__ void pass1_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     // a loop unrolled by three: the loop waits on memory, so each wave keeps
     // two groups' loads in flight; no buffer whose load is in flight is
     // copied (the copy would wait for it).  (ra, rb: groups 0 and 1, loaded
-    // above.)
+    // above.)  The loop runs whole triples only and the last one or two
+    // groups follow it: an exit from the middle of the body would reach the
+    // loop's latch with the buffers' loads in another order, and the wait
+    // for the first buffer, placed for every path into the header, would
+    // then also wait for the second.
     seed_thresholds();
-    for (; it < n_whole; it += 3) {
+    const int n3 = n_whole - n_whole % 3;
+    for (; it < n3; it += 3) {
       load_grads<GD>(T, group_at(it + 2), rc);
       visit(ra, it);
-      if (it + 1 >= n_whole) break;
       load_grads<GD>(T, group_at(it + 3), ra);
       visit(rb, it + 1);
-      if (it + 2 >= n_whole) break;
       load_grads<GD>(T, group_at(it + 4), rb);
       visit(rc, it + 2);
     }
+    // ra, rb: groups n3 and n3 + 1 (the last group where that lies past it)
+    if (it < n_whole) visit(ra, it);
+    if (it + 1 < n_whole) visit(rb, it + 1);
     it = n_whole;
   } else if (n_whole > 0) {
     // raw holds the codes and gradients of the lane's next group (the
@@ -2186,14 +2192,17 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
   };
   int it = 0;
   if (n_whole > 0) {
-    for (; it < n_whole; it += 2) {
+    // Whole pairs only: an exit from the middle of the body would reach the
+    // loop's latch too, and the waits placed for every path into the header
+    // would then wait for more than the current buffer.  An odd last whole
+    // group is stepped by the loop below (its own loads, no staging).
+    const int n2 = n_whole & ~1;
+    for (; it < n2; it += 2) {
       load_p2raw<GD>(T, group_at(it + 1), rb);
       whole_iter(ra, it);
-      if (it + 1 >= n_whole) break;
       load_p2raw<GD>(T, group_at(it + 2), ra);
       whole_iter(rb, it + 1);
     }
-    it = n_whole;
   }
   // drain the staged iterations
   while (qlen_w > 0) batch_w();
