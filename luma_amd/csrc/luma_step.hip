@@ -2196,11 +2196,16 @@ __device__ void pass2_fast_body(const Tensor &T, const Hyper &h, const LUMA_GLOB
     // loop's latch too, and the waits placed for every path into the header
     // would then wait for more than the current buffer.  An odd last whole
     // group is stepped by the loop below (its own loads, no staging).
+    // (the scheduling barriers keep each half's loads ahead of its first use
+    // of the buffer loaded one half earlier: moved above them, that use
+    // waits first and the loads go out late)
     const int n2 = n_whole & ~1;
     for (; it < n2; it += 2) {
       load_p2raw<GD>(T, group_at(it + 1), rb);
+      __builtin_amdgcn_sched_barrier(0);
       whole_iter(ra, it);
       load_p2raw<GD>(T, group_at(it + 2), ra);
+      __builtin_amdgcn_sched_barrier(0);
       whole_iter(rb, it + 1);
     }
   }
