@@ -244,8 +244,9 @@ int64_t luma_summary_words(int64_t numel, int32_t chunk_elems);
  * step count + 1, step scalars), pass 2 (re-decode + EMA + AdamW update +
  * LogSR re-quantisation).  A tensor whose slot holds step count 0 takes the
  * init step.  Three kernel launches on `stream` (a hipStream_t), plus one
- * per pass for the small tensors (small_chunks > 0), which follow the
- * workgroup kernels; no host synchronisation.  No device table is written, so the sequence may
+ * for pass 2 of the small tensors (small_chunks > 0; their pass 1 runs in
+ * workgroups past pass 1's own, and with LUMA_FLAG_EXACT_ONLY in a launch
+ * of its own too); no host synchronisation.  No device table is written, so the sequence may
  * be captured into a HIP graph and replayed.
  */
 int luma_step(const LumaStepArgs *args, void *stream);

@@ -545,10 +545,11 @@ __global__ __launch_bounds__(kThreads) void pass1_exact_kernel(StepSrc src,
 // loops cover any chunk length, so a larger tensor routed here is stepped
 // correctly, only slowly.
 
-// The chunk of this wavefront (false: none, the wavefront exits).
-__device__ __forceinline__ bool small_job(const StepSrc &src, Tensor &T, LumaGroup &g,
+// The chunk of small wavefront w (w-th record from small_from on; false:
+// none, the wavefront exits).
+__device__ __forceinline__ bool small_job(const StepSrc &src, int64_t w, Tensor &T, LumaGroup &g,
                                           int64_t &ci, int64_t &cidx) {
-  cidx = (int64_t)src.small_from + (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  cidx = (int64_t)src.small_from + w;
   if (cidx >= src.n_chunks) return false;
   const LumaChunk c = src.chunks[cidx];
   T = src.tensors[c.tensor];
@@ -557,13 +558,20 @@ __device__ __forceinline__ bool small_job(const StepSrc &src, Tensor &T, LumaGro
   return true;
 }
 
-__global__ __launch_bounds__(kThreads) void pass1_small_kernel(StepSrc src,
-                                                               float *__restrict__ partials) {
-  if (skip_step(src)) return;
+// Workgroup b of the small tensors' launches: small wavefronts 4b .. 4b + 3.
+__device__ __forceinline__ int64_t small_wave(int64_t b) {
+  return b * (kThreads / 64) + (int64_t)(threadIdx.x >> 6);
+}
+
+// Pass 1 of small wavefront w.  The fast pass 1 runs it in workgroups past
+// its own records (the exact-only mode in a kernel of its own), so that the
+// small tensors fill the CUs that its last round of large chunks leaves
+// idle.
+__device__ __forceinline__ void pass1_small_body(const StepSrc &src, float *partials, int64_t w) {
   Tensor T;
   LumaGroup grp;
   int64_t ci, cidx;
-  if (!small_job(src, T, grp, ci, cidx)) return;   // no barriers below
+  if (!small_job(src, w, T, grp, ci, cidx)) return;   // no barriers below
   const Hyper h = group_hyper(grp);
   const bool scaled = src.scaling.grad_scale != nullptr;
   const float inv = inv_scale(src);
@@ -591,6 +599,12 @@ __global__ __launch_bounds__(kThreads) void pass1_small_kernel(StepSrc src,
   wave_argmax(am, im);
   wave_argmax(av, iv);
   if (lane == 0) put_partial(partials, cidx, am, av, im, iv);
+}
+
+__global__ __launch_bounds__(kThreads) void pass1_small_kernel(StepSrc src,
+                                                               float *__restrict__ partials) {
+  if (skip_step(src)) return;
+  pass1_small_body(src, partials, small_wave(blockIdx.x));
 }
 
 // The exact pass 2 of elements e0 .. min(e0 + 8, end) - 1: update, draws
@@ -652,14 +666,13 @@ __global__ __launch_bounds__(kThreads) void pass2_exact_kernel(StepSrc src, uint
     exact_group(T, h, old, G, e0, end, scaled, inv, inj, pb, k0, k1);
 }
 
-// Pass 2 of the small tensors (see pass1_small_kernel).
-__global__ __launch_bounds__(kThreads) void pass2_small_kernel(StepSrc src, uint64_t base_seed,
-                                                               int noise_mode) {
-  if (skip_step(src)) return;
+// Pass 2 of small wavefront w (in a kernel of its own in every mode).
+__device__ __forceinline__ void pass2_small_body(const StepSrc &src, uint64_t base_seed,
+                                                 int noise_mode, int64_t w) {
   Tensor T;
   LumaGroup grp;
   int64_t ci, cidx;
-  if (!small_job(src, T, grp, ci, cidx)) return;
+  if (!small_job(src, w, T, grp, ci, cidx)) return;
   const bool scaled = src.scaling.grad_scale != nullptr;
   const float inv = inv_scale(src);
   const Slot &S = *(const Slot *)T.slot;
@@ -711,6 +724,12 @@ __global__ __launch_bounds__(kThreads) void pass2_small_kernel(StepSrc src, uint
     T.q_m[i] = (int16_t)exact_quant_m(mn, G, um);
     T.q_w[i] = (int16_t)(uint16_t)exact_quant_w(vn, G, h.eps, uw);
   }
+}
+
+__global__ __launch_bounds__(kThreads) void pass2_small_kernel(StepSrc src, uint64_t base_seed,
+                                                               int noise_mode) {
+  if (skip_step(src)) return;
+  pass2_small_body(src, base_seed, noise_mode, small_wave(blockIdx.x));
 }
 
 // ---------------------------------------------------------------------------
@@ -1522,6 +1541,14 @@ __device__ __forceinline__ bool summaries_valid(const Tensor &T, const LUMA_GLOB
 __global__ __launch_bounds__(kThreads, 4) void pass1_fast_kernel(StepSrc src,
                                                               float *__restrict__ partials) {
   if (skip_step(src)) return;
+  {
+    // workgroups past the workgroup and medium records: small tensors
+    const int32_t own = pass_blocks(src.medium_from, src.small_from);
+    if (src.tensors && (int32_t)blockIdx.x >= own) {
+      pass1_small_body(src, partials, small_wave((int64_t)blockIdx.x - own));
+      return;
+    }
+  }
   Tensor T;
   LumaGroup grp;
   int64_t ci, rec;
@@ -2532,8 +2559,9 @@ void luma_layout(int32_t out[8]) {
 }
 
 // The launches of one step over `n_chunks` chunks of `n_tensors` tensors,
-// with optional event records between them: pass 1, finalize, pass 2; sets
-// with small tensors add the wavefront-per-tensor kernel of each pass.
+// with optional event records between them: pass 1, finalize, pass 2; a set
+// with small tensors adds pass 2's wavefront-per-tensor kernel (and, in the
+// exact-only mode, pass 1's).
 static int launch_step(StepSrc src, int32_t n_tensors, int32_t n_chunks, float *partials,
                        uint64_t base_seed, int32_t noise_mode, int32_t flags, hipStream_t s,
                        void *const *events) {
@@ -2551,16 +2579,21 @@ static int launch_step(StepSrc src, int32_t n_tensors, int32_t n_chunks, float *
   // chunks [0, medium_from): a workgroup each; [medium_from, small_from): a
   // wavefront each, four per workgroup, in the same launches;
   // [small_from, n_chunks): small tensors, a wavefront each
+  // (the fast pass 1 runs the small tensors in workgroups past its own, the
+  // exact-only pass 1 leaves them to the small kernel; pass 2 always gives
+  // them a kernel of their own: inside the fast pass 2 their float64 path
+  // would raise its register count past three waves per SIMD)
   const int32_t blocks = pass_blocks(src.medium_from, src.small_from);
   const int32_t small_blocks = (n_chunks - src.small_from + kThreads / 64 - 1) / (kThreads / 64);
-  if (blocks > 0) {
+  const int32_t fast_blocks = blocks + (src.tensors ? small_blocks : 0);
+  if (exact ? blocks > 0 : fast_blocks > 0) {
     if (exact)
       hipLaunchKernelGGL(pass1_exact_kernel, dim3(blocks), dim3(kThreads), 0, s, src, partials);
     else
-      hipLaunchKernelGGL(pass1_fast_kernel, dim3(blocks), dim3(kThreads), 0, s, src, partials);
+      hipLaunchKernelGGL(pass1_fast_kernel, dim3(fast_blocks), dim3(kThreads), 0, s, src, partials);
     if (int r = check_launch("luma_step: pass 1 launch")) return r;
   }
-  if (small_blocks > 0) {
+  if (exact && small_blocks > 0) {
     hipLaunchKernelGGL(pass1_small_kernel, dim3(small_blocks), dim3(kThreads), 0, s, src, partials);
     if (int r = check_launch("luma_step: pass 1 (small tensors) launch")) return r;
   }
