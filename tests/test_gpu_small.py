@@ -179,3 +179,38 @@ def test_medium_route_for_every_tensor(monkeypatch):
     eng.medium_tensors = True
     _step(pair, 4)
     assert eng._medium_chunks > 0
+
+
+def test_fast_launches_equal_exact_launches_on_every_route():
+    """A set with small, medium and workgroup tensors: the fast launches (the
+    small tensors' pass 1 inside the pass-1 launch, each medium tensor one
+    wavefront) and the exact-only launches (the small tensors' pass 1 in a
+    kernel of its own) give the same codes and scales, and parameters within
+    1e-6 of their scale (the fast update's bound)."""
+    from luma_amd import LUMA
+    gen = torch.Generator(device=DEV).manual_seed(9)
+    sizes = [1, 3, 64, 200, L.SMALL_TENSOR, L.SMALL_TENSOR + 1, 1000, 4096, L.MEDIUM_TENSOR,
+             L.MEDIUM_TENSOR + 1, 70000] * 3
+    a = [(torch.randn(n, device=DEV, generator=gen) * 0.02).requires_grad_(True) for n in sizes]
+    b = [p.detach().clone().requires_grad_(True) for p in a]
+    oa, ob = LUMA(a, lr=1e-3), LUMA(b, lr=1e-3)
+    ob._base_seed = oa._base_seed
+    ob._flags = L.FLAG_EXACT_ONLY
+    for t in range(4):
+        for p, q in zip(a, b):
+            g = torch.randn(p.shape, device=DEV, generator=gen) * 1e-3
+            p.grad, q.grad = g, g.clone()
+        oa.step()
+        ob.step()
+    torch.cuda.synchronize()
+    ea = oa._engine
+    assert ea._small_chunks == 3 * sum(1 for n in set(sizes) if n <= L.SMALL_TENSOR)
+    assert ea._medium_chunks == 3 * sum(1 for n in set(sizes)
+                                        if L.SMALL_TENSOR < n <= L.MEDIUM_TENSOR)
+    sa, sb = oa.state_dict()["state"], ob.state_dict()["state"]
+    for i, (p, q) in enumerate(zip(a, b)):
+        assert torch.equal(sa[i]["Q_m"], sb[i]["Q_m"]), i
+        assert torch.equal(sa[i]["Q_w"], sb[i]["Q_w"]), i
+        assert sa[i]["S_m"] == sb[i]["S_m"] and sa[i]["S_v"] == sb[i]["S_v"], i
+        d = float((p.detach() - q.detach()).abs().max())
+        assert d <= 1e-6 * float(q.detach().abs().max()) + 1e-8, (i, d)
