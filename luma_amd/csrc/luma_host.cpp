@@ -133,6 +133,8 @@ inline void prefetch_impl(const c10::TensorImpl *t) {
 PyTypeObject *g_tensor_type = nullptr;
 PyTypeObject *g_param_type = nullptr;
 
+constexpr int kMaxCands = 8;   // cached pointer sets compared during a refresh
+
 struct Plan {
   PyObject *const *params;   // planned parameter objects
   const uint8_t *has_grad;   // per parameter
@@ -143,11 +145,15 @@ struct Plan {
   char *table;               // tensor table rows
   int64_t row_bytes, grad_off, param_off;
   int64_t device;
+  int n_cands;               // cached (grad, param) pointer sets, one pair per row
+  const uint64_t *cands[kMaxCands];
 };
 
 // Checks parameters [a, b) and the rows [ra, rb) that step them, writing
 // the rows' pointers.  0: mismatch, 1: pointers unchanged, 2: some moved.
-int check_range(const Plan &P, int64_t a, int64_t b, int64_t ra, int64_t rb) noexcept {
+// *same: bit k cleared when a row's new pointers differ from cands[k]'s.
+int check_range(const Plan &P, int64_t a, int64_t b, int64_t ra, int64_t rb,
+                uint32_t *same) noexcept {
   try {
     const int64_t n = b - a;
     std::vector<const c10::TensorImpl *> pimpl(n), gimpl(n);
@@ -215,6 +221,9 @@ int check_range(const Plan &P, int64_t a, int64_t b, int64_t ra, int64_t rb) noe
       changed |= (*gp != ga) | (*pp != pa);
       *gp = ga;
       *pp = pa;
+      for (int k = 0; k < P.n_cands; ++k)
+        if (((*same >> k) & 1u) && (P.cands[k][2 * r] != ga || P.cands[k][2 * r + 1] != pa))
+          *same &= ~(1u << k);
     }
     return changed ? 2 : 1;
   } catch (...) {
@@ -237,19 +246,24 @@ int check_range(const Plan &P, int64_t a, int64_t b, int64_t ra, int64_t rb) noe
 //   table      -- address of the tensor table (LumaTensor rows), its row
 //                 size and the byte offsets of the grad and param fields
 //   device     -- the planned CUDA device index
+//   cands      -- optional: up to 8 (n_rows, 2) uint64 arrays of gradient and
+//                 parameter pointers (pointer sets whose tables the caller
+//                 keeps on the device)
 // Returns 0 when anything differs from the plan (a parameter added, removed
 // or replaced by another object, a gradient that appeared or disappeared, a
 // gradient of another dtype, shape, layout or device, a tensor subclass, or
 // a parameter whose storage was replaced by one of another dtype or layout);
 // the table is then to be rebuilt, whatever this call wrote into it.
-// Otherwise 1 when every pointer was already in the table, 2 when some moved.
+// Otherwise 1 when every pointer was already in the table, 2 when some moved,
+// plus bit 2 + k when every row's new pointers equal cands[k]'s (compared
+// while they are written, so the caller need not scan the table again).
 template <typename T>
 using carray = py::array_t<T, py::array::c_style | py::array::forcecast>;
 
 int refresh(py::list groups, py::list planned, carray<uint8_t> has_grad,
             carray<int64_t> row_param, carray<int64_t> layout_at, carray<int64_t> layout,
             carray<int32_t> gdtype, uintptr_t table, int64_t row_bytes, int64_t grad_off,
-            int64_t param_off, int64_t device) {
+            int64_t param_off, int64_t device, py::object cands) {
   const int64_t n_params = (int64_t)planned.size();
   const int64_t n_rows = row_param.shape(0);
   if (has_grad.ndim() != 1 || row_param.ndim() != 1 || layout_at.ndim() != 1 ||
@@ -280,26 +294,45 @@ int refresh(py::list groups, py::list planned, carray<uint8_t> has_grad,
   }
   if (k != n_params || !g_tensor_type || !g_param_type) return 0;
 
-  const Plan P{pl, has_grad.data(), rp, gdtype.data(), lat, lay,
-               reinterpret_cast<char *>(table), row_bytes, grad_off, param_off, device};
+  Plan P{pl, has_grad.data(), rp, gdtype.data(), lat, lay,
+         reinterpret_cast<char *>(table), row_bytes, grad_off, param_off, device, 0, {}};
+  // the candidate arrays (held here for the call's duration); one of another
+  // shape is never a match and never read (its bit starts cleared)
+  std::vector<carray<uint64_t>> held;
+  uint32_t usable = 0;
+  if (!cands.is_none()) {
+    const py::list cl = cands.cast<py::list>();
+    for (py::handle h : cl) {
+      if (P.n_cands == kMaxCands) break;
+      held.push_back(h.cast<carray<uint64_t>>());
+      const carray<uint64_t> &c = held.back();
+      const bool fits = c.ndim() == 2 && c.shape(0) == n_rows && c.shape(1) == 2;
+      P.cands[P.n_cands] = fits ? c.data() : nullptr;
+      if (fits) usable |= 1u << P.n_cands;
+      ++P.n_cands;
+    }
+  }
   const int T = (int)std::min<int64_t>(kMaxThreads, std::max<int64_t>(1, n_params / kPerThread));
   std::vector<int> res(T, 1);
+  std::vector<uint32_t> same(T, usable);
   const std::function<void(int)> part = [&](int t) {
     const int64_t a = n_params * t / T, b = n_params * (t + 1) / T;
     const int64_t ra = std::lower_bound(rp, rp + n_rows, a) - rp;
     const int64_t rb = std::lower_bound(rp, rp + n_rows, b) - rp;
-    res[t] = check_range(P, a, b, ra, rb);
+    res[t] = check_range(P, a, b, ra, rb, &same[t]);
   };
   if (T == 1)
     part(0);
   else
     Pool::get().run(T, part);
   int out = 1;
-  for (int r : res) {
-    if (r == 0) return 0;
-    if (r == 2) out = 2;
+  uint32_t match = usable;
+  for (int t = 0; t < T; ++t) {
+    if (res[t] == 0) return 0;
+    if (res[t] == 2) out = 2;
+    match &= same[t];
   }
-  return out;
+  return out | (int)(match << 2);
 }
 
 // Whether the gradient and parameter pointers of the table's rows are those
@@ -369,7 +402,10 @@ PYBIND11_MODULE(_luma_host, m) {
   // the module holds them for its lifetime
   Py_INCREF(g_tensor_type);
   Py_INCREF(g_param_type);
-  m.def("refresh", &refresh);
+  m.def("refresh", &refresh, py::arg("groups"), py::arg("planned"), py::arg("has_grad"),
+        py::arg("row_param"), py::arg("layout_at"), py::arg("layout"), py::arg("gdtype"),
+        py::arg("table"), py::arg("row_bytes"), py::arg("grad_off"), py::arg("param_off"),
+        py::arg("device"), py::arg("cands") = py::none());
   m.def("same_pointers", &same_pointers);
   m.def("bump_steps", &bump_steps);
   // the torch whose headers this module was compiled against: it reads

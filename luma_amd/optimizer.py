@@ -236,21 +236,23 @@ class _Engine:
 
     def launch(self, tt: np.ndarray, groups: np.ndarray, base_seed: int, noise_mode: int,
                flags: int = 0, scaling: Tuple[int, int] = (0, 0), same_table: bool = False,
-               moved: bool = False):
+               moved: bool = False, ptr_match=None):
         """One step over the tensors of table tt (luma_step), uploading only the
         tables whose contents changed since the previous launch.  With
         ``same_table`` the caller vouches that tt is the array of the previous
         launch, unchanged since: the comparison of its contents is skipped.
         With ``moved`` it vouches that tt is that array with only its gradient
         and parameter pointers rewritten: the device tables of earlier pointer
-        sets are looked up by those two columns alone."""
+        sets are looked up by those two columns alone, and ``ptr_match`` (a
+        key of pointer_candidates(tt)) names the set they equal when the
+        caller has compared them already."""
         capturing = torch.cuda.is_current_stream_capturing()
         n = len(tt)
         setting = (self.chunk_elems, self._small_limit(), self._medium_limit())
         same_src = (self._tensor_src is not None and self._tensor_src[0] is tt
                     and self._tensor_src[1] == setting)
         if moved and same_src:
-            self._match_pointers(tt, capturing)
+            self._match_pointers(tt, capturing, match=ptr_match)
         elif not (same_table and same_src):
             self._tensor_src = None     # stays unset if the upload fails
             self._match_table(tt, capturing)
@@ -387,21 +389,39 @@ class _Engine:
         return bool(np.array_equal(cols[:, 0], tt["grad"])
                     and np.array_equal(cols[:, 1], tt["param"]))
 
-    def _match_pointers(self, tt: np.ndarray, capturing: bool):
+    def pointer_candidates(self, tt: np.ndarray):
+        """(key, (n, 2) pointer array) of the cached pointer sets of tt, most
+        recent first (at most eight): what a planned step's refresh compares
+        the new pointers with while it writes them."""
+        out = []
+        for k in reversed(self._ptr_cache):
+            ent = self._ptr_cache[k]
+            if ent[0] is tt:
+                out.append((k, ent[1]))
+                if len(out) == 8:
+                    break
+        return out
+
+    def _match_pointers(self, tt: np.ndarray, capturing: bool, match=None):
         """Device table for tt, which differs from the table last matched for
         it in its gradient and parameter pointers only (a planned step whose
         gradients moved, e.g. a loop that alternates gradient buffers): a
         table uploaded for the same pointers is re-used, so such a loop
-        uploads each table once.  The cached pointer sets of tt are compared
-        with its two columns, most recent first; the host module's comparison
+        uploads each table once.  ``match``: the key of a cached set that the
+        caller found equal to tt's two columns (the host module's refresh
+        compares them while it writes them).  Otherwise the cached sets of tt
+        are compared here, most recent first; the host module's comparison
         stops at the first row that differs, so a set that does not match
         costs about one row."""
         key = None
-        for k in reversed(self._ptr_cache):
-            ent = self._ptr_cache[k]
-            if ent[0] is tt and self._same_pointers(tt, ent[1]):
-                key = k
-                break
+        if match is not None and match in self._ptr_cache and self._ptr_cache[match][0] is tt:
+            key = match
+        else:
+            for k in reversed(self._ptr_cache):
+                ent = self._ptr_cache[k]
+                if ent[0] is tt and self._same_pointers(tt, ent[1]):
+                    key = k
+                    break
         if key is None:
             if capturing:
                 raise self._capture_error("the parameter or gradient set")
@@ -507,13 +527,15 @@ class _Plan:
                    for w in work) and all(
             r[1] is w[1].grad and type(r[1]) is torch.Tensor for w, r in zip(work, rows))
 
-    def refresh(self, param_groups) -> int:
+    def refresh(self, param_groups, cands=None) -> int:
         """0: the plan no longer applies; 1: it applies and the table is
         unchanged; 2: it applies with new gradient or parameter pointers
-        (written into the table)."""
+        (written into the table).  With cands (a list of (n, 2) pointer
+        arrays), bit 2 + k of the result is set when the new pointers equal
+        cands[k]'s."""
         return self.host.refresh(param_groups, self.all_params, self.has_grad, self.work_idx,
                                  self.layout_at, self.layout, self.gdtypes, self.tt.ctypes.data,
-                                 *self._FIELDS, self.device_index)
+                                 *self._FIELDS, self.device_index, cands)
 
 
 class LUMA(Optimizer):
@@ -808,12 +830,16 @@ class LUMA(Optimizer):
         plan = self._plan
         if (plan is not None and self._noise is None
                 and plan.chunk_setting == self._engine.chunk_elems):
-            r = plan.refresh(self.param_groups)
+            eng = self._engine
+            cands = eng.pointer_candidates(plan.tt)
+            res = plan.refresh(self.param_groups, [c for _, c in cands] if cands else None)
+            r, same = res & 3, res >> 2
+            match = next((k for i, (k, _) in enumerate(cands) if (same >> i) & 1), None)
             if r:
                 self._engine.launch(plan.tt, self._group_table(), self._base_seed,
                                     L.NOISE_PHILOX, self._flags,
                                     self._scaling(self._engine.device), same_table=(r == 1),
-                                    moved=(r == 2))
+                                    moved=(r == 2), ptr_match=match)
                 plan.host.bump_steps(plan.states)
                 return loss
         self._plan = None

@@ -11,6 +11,7 @@ import pytest
 import torch
 
 from luma_amd import LUMA
+from luma_amd import _lib as L
 
 pytestmark = pytest.mark.gpu
 
@@ -59,9 +60,9 @@ def test_plan_steps_like_a_rebuilt_table():
         for name in ("_match_table", "_match_pointers"):
             orig = getattr(engine, name)
 
-            def wrapped(tt, capturing, orig=orig):
+            def wrapped(tt, capturing, orig=orig, **kw):
                 matches.append(len(tt))
-                return orig(tt, capturing)
+                return orig(tt, capturing, **kw)
             setattr(engine, name, wrapped)
 
     def set_grads(gs):
@@ -97,18 +98,24 @@ def test_plan_steps_like_a_rebuilt_table():
     _same(a, b, oa, ob)
 
     # gradients alternating between two sets of buffers: each set's table is
-    # uploaded once and then re-used
+    # uploaded once and then re-used, found by the host module's refresh
+    # (which compares the cached pointer sets while it writes the pointers:
+    # no comparison in Python from the third step on)
     sets = [grads(), grads()]
-    uploads = []
-    up = oa._engine._upload
-    oa._engine._upload = lambda arr: uploads.append(len(arr)) or up(arr)
+    uploads, compared = [], []
+    eng = oa._engine
+    up, same = eng._upload, eng._same_pointers
+    # (tensor tables only: state_dict() below uploads slot pointers too)
+    eng._upload = lambda arr: (arr.dtype == L.TENSOR_DTYPE and uploads.append(len(arr))) or up(arr)
     for k in range(4):
+        eng._same_pointers = lambda tt, cols, k=k: compared.append(k) or same(tt, cols)
         for p, q, g in zip(a, b, sets[k % 2]):
             p.grad, q.grad = g, g.clone()
         _step(oa, ob)
-    oa._engine._upload = up
+        _same(a, b, oa, ob)
+    eng._upload, eng._same_pointers = up, same
     assert uploads == [len(SHAPES)] * 2 and oa._plan is not None
-    _same(a, b, oa, ob)
+    assert not [k for k in compared if k >= 2]
 
     # bf16 gradients: the plan no longer applies, the table is rebuilt
     plan = oa._plan

@@ -366,3 +366,37 @@ def test_moved_pointer_tables_are_reused(with_host):
     eng._ptr_cache = {key: (ent[0], ent[1] + 1, ent[2])}
     with pytest.raises(RuntimeError):
         eng._match_pointers(ent[0], capturing=True)   # would need an upload under capture
+
+
+def test_pointer_match_named_by_the_caller():
+    """_match_pointers takes a cached set named by the caller (the host
+    module's refresh compared it) without comparing; a key that names no
+    set of this table falls back to the comparison."""
+    from luma_amd.optimizer import _Engine
+    eng = _Engine.__new__(_Engine)
+    eng.host = None
+    eng._ptr_cache = {}
+    eng._ptr_seq = 0
+    eng._tensor_key = b""
+    uploads = []
+    eng._upload = lambda arr: uploads.append(arr.copy()) or len(uploads)
+    tt = np.zeros(3, dtype=L.TENSOR_DTYPE)
+    tt["param"] = np.arange(3) * 4096 + (1 << 40)
+    sets = [np.arange(3, dtype=np.uint64) * 512 + (k + 1) * (1 << 36) for k in range(2)]
+    for k in range(2):
+        tt["grad"] = sets[k]
+        eng._match_pointers(tt, capturing=False)
+    cands = eng.pointer_candidates(tt)
+    assert [c[1][:, 0].tolist() for c in cands] == [sets[1].tolist(), sets[0].tolist()]
+    compared = []
+    eng._same_pointers = lambda t, cols: compared.append(1) or _Engine._same_pointers(eng, t, cols)
+    tt["grad"] = sets[0]
+    eng._match_pointers(tt, capturing=True, match=cands[1][0])   # no upload, no comparison
+    assert eng._d_tensors == 1 and not compared
+    tt["grad"] = sets[1]
+    eng._match_pointers(tt, capturing=False, match=-5)           # unknown key: compared
+    assert eng._d_tensors == 2 and compared and len(uploads) == 2
+    # another table's key is not taken
+    tt2 = tt.copy()
+    eng._match_pointers(tt2, capturing=False, match=cands[0][0])
+    assert len(uploads) == 3

@@ -135,6 +135,25 @@ def test_refresh_rejects_a_subclass_gradient_without_python():
     assert _Recording.calls == 0
 
 
+def test_refresh_candidates_of_any_shape():
+    """Candidate pointer arrays of the wrong shape are ignored (never read);
+    a plan that does not apply returns 0 whatever the candidates."""
+    ps = [torch.zeros(3, requires_grad=True) for _ in range(3)]
+    for p in ps:
+        p.grad = torch.zeros(3)
+    tt = np.zeros(3, dtype=L.TENSOR_DTYPE)
+    groups = [{"params": ps}]
+    args = (groups, ps, np.ones(3, dtype=np.uint8), np.arange(3, dtype=np.int64),
+            np.array([0, 3, 6], dtype=np.int64), np.array([1, 3, 1] * 3, dtype=np.int64),
+            np.zeros(3, dtype=np.int32), tt.ctypes.data, tt.dtype.itemsize,
+            tt.dtype.fields["grad"][1], tt.dtype.fields["param"][1], 0)
+    cands = [np.zeros((2, 2), dtype=np.uint64), np.zeros((3, 2), dtype=np.uint64),
+             np.zeros(6, dtype=np.uint64)]
+    # CPU tensors: the plan does not apply (not on the planned GPU)
+    assert H.refresh(*args, cands) == 0
+    assert H.refresh(*args) == 0
+
+
 def test_refresh_pool_after_fork():
     """The check's worker threads belong to the process that made them: a
     forked child (a DataLoader worker, say) that steps makes its own."""
