@@ -425,9 +425,9 @@ def stats_report(config, trace_csv, bench_json, out):
                      f"{min(d):.3f} | {max(d):.3f} | {100 * sum(d) / total:.2f} | "
                      f"{'' if bev is None else f'{bev:.3f}'} |")
     lines += ["",
-              "The bench's HIP-event intervals bracket each pass: pass 2's includes "
-              "`luma::pass2_small_kernel` (tensors of at most 256 elements, one wavefront each) "
-              "when the set has any; their pass 1 runs inside `luma::pass1_fast_kernel`.",
+              "The bench's HIP-event intervals bracket each pass; the tensors of at most 256 "
+              "elements (one wavefront each) are stepped inside `luma::pass1_fast_kernel` and "
+              "`luma::pass2_fast_kernel`.",
               "",
               f"Step time in the same run (bench wall clock): {bench['ms_per_step']:.3f} ms; "
               f"{bench['value']} Gparams/s.",

@@ -243,10 +243,10 @@ int64_t luma_summary_words(int64_t numel, int32_t chunk_elems);
  * per-chunk maxima), per-tensor finalize (new S_m/S_v and grid in float64,
  * step count + 1, step scalars), pass 2 (re-decode + EMA + AdamW update +
  * LogSR re-quantisation).  A tensor whose slot holds step count 0 takes the
- * init step.  Three kernel launches on `stream` (a hipStream_t), plus one
- * for pass 2 of the small tensors (small_chunks > 0; their pass 1 runs in
- * workgroups past pass 1's own, and with LUMA_FLAG_EXACT_ONLY in a launch
- * of its own too); no host synchronisation.  No device table is written, so the sequence may
+ * init step.  Three kernel launches on `stream` (a hipStream_t): the small
+ * tensors (small_chunks > 0) are stepped by workgroups of the pass-1 and
+ * pass-2 launches past their own (with LUMA_FLAG_EXACT_ONLY by a kernel of
+ * their own in each pass); no host synchronisation.  No device table is written, so the sequence may
  * be captured into a HIP graph and replayed.
  */
 int luma_step(const LumaStepArgs *args, void *stream);

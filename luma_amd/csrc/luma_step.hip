@@ -163,9 +163,11 @@ __device__ __forceinline__ float unscale_rt(float g, float inv, int dt) {
 
 // The chunk of this workgroup, or from medium_from on of this wavefront:
 // its record, tensor, group, chunk index and thread share.  False: the
-// wavefront has no record (the last workgroup of the medium run).
+// wavefront has no record (the last workgroup of the wavefront run, which
+// ends at small_from, or with to_end at the table's end).
 __device__ __forceinline__ bool chunk_job(const StepSrc &src, Tensor &T, LumaGroup &g,
-                                          int64_t &index, int64_t &rec, Share &sh) {
+                                          int64_t &index, int64_t &rec, Share &sh,
+                                          bool to_end = false) {
   if (src.tensors) {
     if ((int32_t)blockIdx.x < src.medium_from) {
       rec = blockIdx.x;
@@ -176,7 +178,7 @@ __device__ __forceinline__ bool chunk_job(const StepSrc &src, Tensor &T, LumaGro
       rec = __builtin_amdgcn_readfirstlane(
           src.medium_from + (int32_t)(blockIdx.x - (uint32_t)src.medium_from) * (kThreads / 64) +
           (int32_t)(threadIdx.x >> 6));
-      if (rec >= src.small_from) return false;
+      if (rec >= (to_end ? src.n_chunks : src.small_from)) return false;
       sh = Share{64};
     }
     const LumaChunk c = src.chunks[rec];
@@ -666,7 +668,8 @@ __global__ __launch_bounds__(kThreads) void pass2_exact_kernel(StepSrc src, uint
     exact_group(T, h, old, G, e0, end, scaled, inv, inj, pb, k0, k1);
 }
 
-// Pass 2 of small wavefront w (in a kernel of its own in every mode).
+// Pass 2 of small wavefront w through the exact path (the exact-only mode's
+// kernel; the fast pass 2 steps small tensors like medium ones).
 __device__ __forceinline__ void pass2_small_body(const StepSrc &src, uint64_t base_seed,
                                                  int noise_mode, int64_t w) {
   Tensor T;
@@ -2327,7 +2330,8 @@ __global__ __launch_bounds__(kThreads) void pass2_fast_kernel(StepSrc src, uint6
   LumaGroup grp;
   int64_t ci, rec;
   Share sh;
-  if (!chunk_job(src, T, grp, ci, rec, sh)) return;   // (no barriers below)
+  // (the small tensors too: one wavefront each, after the medium ones)
+  if (!chunk_job(src, T, grp, ci, rec, sh, true)) return;   // (no barriers below)
   const LUMA_GLOBAL Slot *S = T.slot;
   const int64_t t = S->step;   // advanced by finalize
   const Hyper h = S->hyp;
@@ -2559,9 +2563,9 @@ void luma_layout(int32_t out[8]) {
 }
 
 // The launches of one step over `n_chunks` chunks of `n_tensors` tensors,
-// with optional event records between them: pass 1, finalize, pass 2; a set
-// with small tensors adds pass 2's wavefront-per-tensor kernel (and, in the
-// exact-only mode, pass 1's).
+// with optional event records between them: pass 1, finalize, pass 2 (in the
+// exact-only mode a set with small tensors adds the wavefront-per-tensor
+// kernel of each pass).
 static int launch_step(StepSrc src, int32_t n_tensors, int32_t n_chunks, float *partials,
                        uint64_t base_seed, int32_t noise_mode, int32_t flags, hipStream_t s,
                        void *const *events) {
@@ -2579,10 +2583,9 @@ static int launch_step(StepSrc src, int32_t n_tensors, int32_t n_chunks, float *
   // chunks [0, medium_from): a workgroup each; [medium_from, small_from): a
   // wavefront each, four per workgroup, in the same launches;
   // [small_from, n_chunks): small tensors, a wavefront each
-  // (the fast pass 1 runs the small tensors in workgroups past its own, the
-  // exact-only pass 1 leaves them to the small kernel; pass 2 always gives
-  // them a kernel of their own: inside the fast pass 2 their float64 path
-  // would raise its register count past three waves per SIMD)
+  // (the fast pass 1 runs the small tensors' exact pass 1 in workgroups past
+  // its own, and the fast pass 2 steps them as it steps the medium ones; the
+  // exact-only mode leaves them to the small kernels)
   const int32_t blocks = pass_blocks(src.medium_from, src.small_from);
   const int32_t small_blocks = (n_chunks - src.small_from + kThreads / 64 - 1) / (kThreads / 64);
   const int32_t fast_blocks = blocks + (src.tensors ? small_blocks : 0);
@@ -2603,19 +2606,22 @@ static int launch_step(StepSrc src, int32_t n_tensors, int32_t n_chunks, float *
                      dim3(kThreads), 0, s, src, (const float *)partials, n_tensors);
   if (int r = check_launch("luma_step: finalize launch")) return r;
   if (int r = mark(2)) return r;
-  if (blocks > 0) {
+  // the fast pass 2 steps the small tensors as it does the medium ones, one
+  // wavefront each in workgroups after theirs
+  const int32_t p2_blocks = pass_blocks(src.medium_from, src.tensors ? n_chunks : src.small_from);
+  if (exact ? blocks > 0 : p2_blocks > 0) {
     if (exact)
       hipLaunchKernelGGL(pass2_exact_kernel, dim3(blocks), dim3(kThreads), 0, s, src, base_seed,
                          (int)noise_mode);
     else if (noise_mode == LUMA_NOISE_INJECTED)
-      hipLaunchKernelGGL(pass2_fast_kernel<true>, dim3(blocks), dim3(kThreads), 0, s, src,
+      hipLaunchKernelGGL(pass2_fast_kernel<true>, dim3(p2_blocks), dim3(kThreads), 0, s, src,
                          base_seed, (int)noise_mode);
     else
-      hipLaunchKernelGGL(pass2_fast_kernel<false>, dim3(blocks), dim3(kThreads), 0, s, src,
+      hipLaunchKernelGGL(pass2_fast_kernel<false>, dim3(p2_blocks), dim3(kThreads), 0, s, src,
                          base_seed, (int)noise_mode);
     if (int r = check_launch("luma_step: pass 2 launch")) return r;
   }
-  if (small_blocks > 0) {
+  if (exact && small_blocks > 0) {
     hipLaunchKernelGGL(pass2_small_kernel, dim3(small_blocks), dim3(kThreads), 0, s, src,
                        base_seed, (int)noise_mode);
     if (int r = check_launch("luma_step: pass 2 (small tensors) launch")) return r;
