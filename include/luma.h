@@ -71,8 +71,8 @@ extern "C" {
 
 /*
  * Tensors of at most this many elements are best stepped one wavefront each
- * by the exact path (LumaStepArgs.small_chunks): a workgroup of their own
- * would spend most of its time in set-up, and the fast kernels' wavefront
+ * with an exact pass 1 (LumaStepArgs.small_chunks): a workgroup of their own
+ * would spend most of its time in set-up, and the fast pass 1's wavefront
  * route (medium_chunks) runs a partial group for them.
  */
 #define LUMA_SMALL_TENSOR 256
@@ -200,7 +200,8 @@ typedef struct LumaStepArgs {
                                 [LUMA_CHUNK_ELEMS_MIN, LUMA_CHUNK_ELEMS]; 0 = LUMA_CHUNK_ELEMS */
   int32_t small_chunks;      /* the last small_chunks records of the chunk table, one
                                 chunk per tensor, are stepped one wavefront each (four
-                                per workgroup) by the exact path; meant for tensors of at
+                                per workgroup): pass 1 by the exact path, pass 2 by the
+                                fast kernel's wavefront route; meant for tensors of at
                                 most LUMA_SMALL_TENSOR elements (any tensor is stepped
                                 correctly).  0: every chunk takes a workgroup */
   int32_t medium_chunks;     /* the medium_chunks records just before the small ones
